@@ -1,0 +1,190 @@
+/*
+ * q4rdna.h -- C ABI of the MI355X (gfx950) Q4_RDNA group-64 dequant-GEMV.
+ *
+ * A drop-in for the reference's llama.cpp entry points
+ * (source/q4rdna.cuh:5-24, defined at source/q4rdna.cu:713-793) with ggml
+ * types replaced by plain pointers and sizes.  The packed layout is the
+ * reference's byte-exact Q4_RDNA sidecar: 32-row tiles of 1088 bytes (32 fp16
+ * scales, then 32x32 lane-interleaved bytes of two's-complement nibbles, low
+ * nibble = even k) in (row tile, group) order.
+ *
+ * Conventions
+ *  - Every call returns a status.  Q4RDNA_NOT_APPLICABLE is the reference's
+ *    "return false": the call touched nothing and the caller should run its
+ *    own path.  Negative values are errors; q4rdna_last_error() describes the
+ *    last one on the calling thread.
+ *  - Device pointers are caller-owned except the sidecar's weights, which the
+ *    library owns until q4rdna_sidecar_close().
+ *  - `stream` is a hipStream_t (NULL = the null stream).  Launches are
+ *    asynchronous on that stream; nothing here synchronises it.
+ *  - A launch needs the weights' device to be the current device.
+ */
+#ifndef Q4RDNA_H
+#define Q4RDNA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q4RDNA_ABI_VERSION 1
+
+/* status codes */
+#define Q4RDNA_OK 0
+#define Q4RDNA_NOT_APPLICABLE 1
+#define Q4RDNA_ERR_ARGUMENT (-1)
+#define Q4RDNA_ERR_FORMAT (-2)
+#define Q4RDNA_ERR_IO (-3)
+#define Q4RDNA_ERR_HIP (-4)
+#define Q4RDNA_ERR_MEMORY (-5)
+
+/* format constants (source/q4rdna.cu:20-22) */
+#define Q4RDNA_GROUP 64
+#define Q4RDNA_TILE_ROWS 32
+#define Q4RDNA_TILE_BYTES 1088
+
+/* scale-search algorithms of the packers */
+#define Q4RDNA_ALGO_SIDECAR 0 /* source/q4rdna_sidecar_pack.cpp:126-179 */
+#define Q4RDNA_ALGO_ABSMAX 1  /* source/q4rdna_cpu_experiment.cpp:209-211 */
+#define Q4RDNA_ALGO_RANGE 2   /* source/q4rdna_cpu_experiment.cpp:213-223 */
+#define Q4RDNA_ALGO_MSE 3     /* source/q4rdna_cpu_experiment.cpp:225-236 */
+
+/* GLU operations accepted by q4rdna_mul_mat_glu (source/q4rdna.cu:776) */
+#define Q4RDNA_GLU_SWIGLU 0
+
+/* A packed tensor resident on a device: rows x columns weights, rows%32 == 0,
+ * columns%64 == 0, `tiles` 16-byte aligned, rows*columns*34/64 bytes. */
+typedef struct q4rdna_weight {
+    const uint8_t *tiles;
+    uint32_t rows;
+    uint32_t columns;
+    int32_t device;
+    uint32_t reserved;
+} q4rdna_weight;
+
+typedef struct q4rdna_sidecar q4rdna_sidecar;
+
+/* Library version (Q4RDNA_ABI_VERSION) and the last error on this thread. */
+int q4rdna_abi_version(void);
+const char *q4rdna_last_error(void);
+
+/* ---- sidecar container --------------------------------------------------
+ * q4rdna_sidecar_inspect: host-only validation of a sidecar image prefix that
+ * holds at least the header and the index; `file_size` is the size of the
+ * whole file.  Applies the loader's acceptance rules of
+ * source/q4rdna.cu:129-155 (magic, version, group 64, 32 rows, 1088-byte
+ * tiles, NUL-terminated names, offsets inside the data region, rows%32,
+ * columns%64, size = rows*columns*34/64) and the data-length check of
+ * source/q4rdna.cu:163-170.  On success *count receives the entry count. */
+int q4rdna_sidecar_inspect(const void *image, uint64_t image_size, uint64_t file_size,
+                           uint32_t *count);
+
+/* Open a sidecar file and upload its data region to `device` once
+ * (source/q4rdna.cu:119-179, without the device-0 restriction). */
+int q4rdna_sidecar_open(const char *path, int device, q4rdna_sidecar **out);
+/* Same from an in-memory image of `size` bytes. */
+int q4rdna_sidecar_open_memory(const void *image, uint64_t size, int device, q4rdna_sidecar **out);
+void q4rdna_sidecar_close(q4rdna_sidecar *sidecar);
+uint32_t q4rdna_sidecar_count(const q4rdna_sidecar *sidecar);
+/* Entry metadata; name receives up to 64 bytes including the NUL. */
+int q4rdna_sidecar_entry(const q4rdna_sidecar *sidecar, uint32_t index, char name[64],
+                         uint32_t *rows, uint32_t *columns, uint64_t *offset, uint64_t *size);
+
+/* Name lookup with the reference's shape check: `ne0` = columns (K) and
+ * `ne1` = rows (M) as ggml stores them.  NOT_APPLICABLE when the name is
+ * absent or the shape differs (source/q4rdna.cu:682-705). */
+int q4rdna_find(const q4rdna_sidecar *sidecar, const char *name, int64_t ne0, int64_t ne1,
+                q4rdna_weight *out);
+
+/* Describe tiles already resident on `device` (synthetic or externally
+ * uploaded tensors). */
+int q4rdna_weight_from_device(const void *tiles, uint32_t rows, uint32_t columns, int device,
+                              q4rdna_weight *out);
+
+/* Sidecar named by LLAMA_Q4_RDNA_SIDECAR, opened once per process on the
+ * first call (source/q4rdna.cu:683,698).  NULL when unset or invalid. */
+q4rdna_sidecar *q4rdna_default_sidecar(int device);
+/* The reference's LLAMA_Q4_RDNA_SCOPE name filter (source/q4rdna.cu:685-696):
+ * scope NULL/"" admits every name; "ffn", "qkv-fallback", "hotspot", "attn"
+ * as in the reference.  Returns 1 if `name` is in scope, else 0. */
+int q4rdna_scope_allows(const char *scope, const char *name);
+
+/* ---- GEMV entry points ---------------------------------------------------
+ * y[M] = W[M][K] x[K] in fp32 accumulation.  x_ne0 must equal K and y_ne0 M
+ * (the reference's src1->ne[0] / dst->ne[0] checks); any mismatch, a weight
+ * on another device or a NULL weight returns NOT_APPLICABLE with nothing
+ * launched.  x and y are contiguous fp32 device buffers (4-byte aligned).
+ *
+ * Replaces ggml_cuda_q4rdna_mul_mat (source/q4rdna.cuh:5-9, q4rdna.cu:713-745). */
+int q4rdna_mul_mat(const q4rdna_weight *w, const float *x, int64_t x_ne0, float *y, int64_t y_ne0,
+                   void *stream);
+
+/* y = W x + add, add[M] fp32.
+ * Replaces ggml_cuda_q4rdna_mul_mat_add (source/q4rdna.cuh:11-16, q4rdna.cu:747-767). */
+int q4rdna_mul_mat_add(const q4rdna_weight *w, const float *x, int64_t x_ne0, const float *add,
+                       int64_t add_ne, float *y, int64_t y_ne0, void *stream);
+
+/* y = (W_up x) * silu(W_gate x), both weights of one shape; glu_op must be
+ * Q4RDNA_GLU_SWIGLU (anything else is NOT_APPLICABLE).
+ * Replaces ggml_cuda_q4rdna_mul_mat_glu (source/q4rdna.cuh:18-24, q4rdna.cu:769-793). */
+int q4rdna_mul_mat_glu(const q4rdna_weight *up, const q4rdna_weight *gate, const float *x,
+                       int64_t x_ne0, int glu_op, float *y, int64_t y_ne0, void *stream);
+
+/* Launch options for sweeps: split_k = number of K chunks reduced across
+ * workgroups (0 = the shape policy, the reference's launch policy at
+ * source/q4rdna.cu:578-680 and its LLAMA_Q4_RDNA_COOP override :579-584). */
+typedef struct q4rdna_launch_options {
+    uint32_t split_k;
+    uint32_t reserved[7];
+} q4rdna_launch_options;
+
+/* q4rdna_mul_mat / _add / _glu with explicit options (add, gate may be NULL). */
+int q4rdna_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x,
+                      const float *add, float *y, const q4rdna_launch_options *options,
+                      void *stream);
+
+/* Split-K factor the shape policy picks for rows x columns on `device`. */
+uint32_t q4rdna_policy_split_k(uint32_t rows, uint32_t columns, int device);
+
+/* ---- multi-tensor stack --------------------------------------------------
+ * One launch that sweeps many independent GEMVs in order (a decode step's
+ * weight streaming).  No reference counterpart: the reference launches one
+ * kernel per tensor (source/q4rdna.cu:736-741). */
+typedef struct q4rdna_gemv_desc {
+    q4rdna_weight weight;      /* W (the up projection for SwiGLU) */
+    const uint8_t *gate_tiles; /* SwiGLU gate tiles of the same shape, or NULL */
+    const float *x;            /* [columns] */
+    const float *add;          /* [rows] or NULL */
+    float *y;                  /* [rows] */
+} q4rdna_gemv_desc;
+
+typedef struct q4rdna_plan q4rdna_plan;
+
+/* Build a plan for `count` descriptors (uploads the descriptor table once). */
+int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device,
+                       q4rdna_plan **out);
+/* Launch the whole plan on `stream`; allocates nothing. */
+int q4rdna_plan_launch(q4rdna_plan *plan, void *stream);
+void q4rdna_plan_destroy(q4rdna_plan *plan);
+/* Workgroups the plan launches (persistent grid). */
+uint32_t q4rdna_plan_workgroups(const q4rdna_plan *plan);
+
+/* ---- packing and dequantisation ------------------------------------------
+ * Quantize fp32 W[rows][columns] (device, row-major) into tiles (device) with
+ * the chosen scale search, bit-identical to the reference CPU packers
+ * (source/q4rdna_sidecar_pack.cpp:126-179,259-279 for Q4RDNA_ALGO_SIDECAR;
+ * source/q4rdna_cpu_experiment.cpp:136-273,387-399 for absmax/range/mse). */
+int q4rdna_pack(const float *w, uint32_t rows, uint32_t columns, int algorithm, uint8_t *tiles,
+                void *stream);
+
+/* Test/inspection: out[rows][columns] = fp32(scale) * code, the exact
+ * product (source/q4rdna_cpu_experiment.cpp:270-271). */
+int q4rdna_dequantize(const q4rdna_weight *w, float *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q4RDNA_H */

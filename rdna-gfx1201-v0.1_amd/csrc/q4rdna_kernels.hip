@@ -1,0 +1,598 @@
+// gfx950 (CDNA4) kernels for the Q4_RDNA group-64 dequant-GEMV.
+//
+// Tile layout (restated from source/q4rdna.cu:20-24,346,359,370): row tile rt
+// and group g form tile t = rt*G + g of 1088 bytes: 32 fp16 scales (row lane
+// l at byte 2l), then byte 64 + 32*i + l holds the codes of k = 64g + 2i (low
+// nibble) and 2i+1 (high nibble), two's complement in [-8, 7].
+//
+// Wave64 mapping.  One wave consumes one whole tile per step.  Lane
+// (q = lane & 7, a = lane >> 3) loads four dwords at 64 + 32*(a + 8j) + 4q,
+// j = 0..3: rows 4q..4q+3 at k-pairs i = a, a+8, a+16, a+24.  For each j one
+// load instruction reads one contiguous 256-byte block of the tile, so the
+// 1024 code bytes arrive in four fully coalesced loads, plus one 8-byte load
+// of the lane's four scales.
+//
+// Decode.  XOR 0x88888888 turns every nibble into offset binary u = q + 8;
+// the low nibbles (mask 0x0F0F0F0F) and the high nibbles kept in place (mask
+// 0xF0F0F0F0, i.e. 16*u) convert with one v_cvt_f32_ubyteN each.  The 1/16
+// of the high nibbles is folded into the staged activation, and the -8 offset
+// into a per-(group, lane) constant c = -8 * sum of the lane's eight x values,
+// so per weight the inner loop is one conversion and one fma.  The fp16
+// scale multiplies the lane's per-(row, group) partial once per group.
+//
+// Activations.  The workgroup stages x for up to 64 groups at a time in LDS,
+// rearranged so lane a reads its 4 even-k values, its 4 odd-k values (/16)
+// and c with two ds_read_b128 and one ds_read_b32 (8 lanes share each
+// address, a broadcast).
+//
+// Reduction.  Lane partials are summed over a with xor-8/16/32 shuffles, the
+// four waves' results in LDS in wave order, and K chunks split across
+// workgroups through a partial buffer summed in chunk order by the last
+// workgroup to arrive, so every result is bit-reproducible run to run.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "q4rdna_internal.h"
+
+namespace q4rdna {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kStageGroups = 64;  // groups of x staged in LDS at once
+constexpr int kBatch = 4;         // tiles in flight per wave per loop trip
+
+struct XStage {
+    float4 v[kStageGroups][16];  // [g][a] even-k x, [g][8 + a] odd-k x / 16
+    float c[kStageGroups][8];    // -8 * sum of the lane's 8 x values
+};
+
+struct TileRegs {
+    uint32_t d[4];
+    uint32_t s01, s23;
+};
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(bits & 0xffffu)));
+}
+
+__device__ __forceinline__ TileRegs load_tile(const uint8_t *__restrict__ tile, int q, int a) {
+    TileRegs r;
+    const uint8_t *codes = tile + 64 + 4 * q + 32 * a;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r.d[j] = *reinterpret_cast<const uint32_t *>(codes + 256 * j);
+    const uint2 s = *reinterpret_cast<const uint2 *>(tile + 8 * q);
+    r.s01 = s.x;
+    r.s23 = s.y;
+    return r;
+}
+
+// acc[r] += scale(row 4q+r) * sum over the lane's 8 k of code * x.
+__device__ __forceinline__ void tile_fma(const TileRegs &r, const float4 xl, const float4 xh,
+                                         const float c, float acc[4]) {
+    const float xlv[4] = {xl.x, xl.y, xl.z, xl.w};
+    const float xhv[4] = {xh.x, xh.y, xh.z, xh.w};
+    float p0 = c, p1 = c, p2 = c, p3 = c;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t e = r.d[j] ^ 0x88888888u;
+        uint32_t lo = e & 0x0f0f0f0fu;
+        uint32_t hi = e & 0xf0f0f0f0u;
+        // Hide the masks' known bits so each byte converts with
+        // v_cvt_f32_ubyte{0,1,2,3} instead of an extract plus ubyte0.
+        asm("" : "+v"(lo));
+        asm("" : "+v"(hi));
+        p0 = fmaf(static_cast<float>(lo & 0xffu), xlv[j], p0);
+        p1 = fmaf(static_cast<float>((lo >> 8) & 0xffu), xlv[j], p1);
+        p2 = fmaf(static_cast<float>((lo >> 16) & 0xffu), xlv[j], p2);
+        p3 = fmaf(static_cast<float>(lo >> 24), xlv[j], p3);
+        p0 = fmaf(static_cast<float>(hi & 0xffu), xhv[j], p0);
+        p1 = fmaf(static_cast<float>((hi >> 8) & 0xffu), xhv[j], p1);
+        p2 = fmaf(static_cast<float>((hi >> 16) & 0xffu), xhv[j], p2);
+        p3 = fmaf(static_cast<float>(hi >> 24), xhv[j], p3);
+    }
+    acc[0] = fmaf(half_bits_to_float(r.s01), p0, acc[0]);
+    acc[1] = fmaf(half_bits_to_float(r.s01 >> 16), p1, acc[1]);
+    acc[2] = fmaf(half_bits_to_float(r.s23), p2, acc[2]);
+    acc[3] = fmaf(half_bits_to_float(r.s23 >> 16), p3, acc[3]);
+}
+
+// Stage x for groups [g0, g0 + ng) into LDS.
+__device__ __forceinline__ void stage_x(XStage &st, const float *__restrict__ x, uint32_t g0, int ng) {
+    for (int idx = threadIdx.x; idx < ng * 8; idx += kThreads) {
+        const int g = idx >> 3, a = idx & 7;
+        const float *b = x + (static_cast<size_t>(g0) + g) * kGroup + 2 * a;
+        const float l0 = b[0], h0 = b[1], l1 = b[16], h1 = b[17];
+        const float l2 = b[32], h2 = b[33], l3 = b[48], h3 = b[49];
+        st.v[g][a] = make_float4(l0, l1, l2, l3);
+        st.v[g][8 + a] = make_float4(h0 * 0.0625f, h1 * 0.0625f, h2 * 0.0625f, h3 * 0.0625f);
+        st.c[g][a] = -8.0f * (((((((l0 + h0) + l1) + h1) + l2) + h2) + l3) + h3);
+    }
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+struct Shared {
+    XStage st;
+    float red[2][kWaves][32];
+    uint32_t last;
+};
+
+// Partial dot products of row tile `rt` over groups [g_begin, g_end), summed
+// over the workgroup.  Threads 0..31 return the row partials (out, gout).
+template <bool GATE>
+__device__ __forceinline__ void tile_row_partial(Shared &sh, const uint8_t *__restrict__ w,
+                                                 const uint8_t *__restrict__ gw,
+                                                 const float *__restrict__ x, uint32_t cols,
+                                                 uint32_t rt, uint32_t g_begin, uint32_t g_end,
+                                                 float &out, float &gout) {
+    const uint32_t groups = cols / kGroup;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = lane & 7, a = lane >> 3;
+    const size_t row_tile_offset = static_cast<size_t>(rt) * groups * kTileBytes;
+    const uint8_t *wt = w + row_tile_offset;
+    const uint8_t *gt = GATE ? gw + row_tile_offset : nullptr;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float gacc[4] = {0.f, 0.f, 0.f, 0.f};
+
+    for (uint32_t s0 = g_begin; s0 < g_end; s0 += kStageGroups) {
+        const int ng = static_cast<int>(min(static_cast<uint32_t>(kStageGroups), g_end - s0));
+        __syncthreads();
+        stage_x(sh.st, x, s0, ng);
+        __syncthreads();
+        for (int g = wave; g < ng; g += kWaves * kBatch) {
+            TileRegs t[kBatch];
+            TileRegs u[GATE ? kBatch : 1];
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) {
+                const int gg = g + kWaves * b;
+                if (gg < ng) {
+                    t[b] = load_tile(wt + static_cast<size_t>(s0 + gg) * kTileBytes, q, a);
+                    if constexpr (GATE) u[b] = load_tile(gt + static_cast<size_t>(s0 + gg) * kTileBytes, q, a);
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) {
+                const int gg = g + kWaves * b;
+                if (gg < ng) {
+                    const float4 xl = sh.st.v[gg][a];
+                    const float4 xh = sh.st.v[gg][8 + a];
+                    const float c = sh.st.c[gg][a];
+                    tile_fma(t[b], xl, xh, c, acc);
+                    if constexpr (GATE) tile_fma(u[b], xl, xh, c, gacc);
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        acc[r] += __shfl_xor(acc[r], 8);
+        acc[r] += __shfl_xor(acc[r], 16);
+        acc[r] += __shfl_xor(acc[r], 32);
+        if constexpr (GATE) {
+            gacc[r] += __shfl_xor(gacc[r], 8);
+            gacc[r] += __shfl_xor(gacc[r], 16);
+            gacc[r] += __shfl_xor(gacc[r], 32);
+        }
+    }
+    if (a == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sh.red[0][wave][4 * q + r] = acc[r];
+            if constexpr (GATE) sh.red[1][wave][4 * q + r] = gacc[r];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 32) {
+        const int t = threadIdx.x;
+        float v = sh.red[0][0][t];
+#pragma unroll
+        for (int wv = 1; wv < kWaves; ++wv) v += sh.red[0][wv][t];
+        out = v;
+        if constexpr (GATE) {
+            float gv = sh.red[1][0][t];
+#pragma unroll
+            for (int wv = 1; wv < kWaves; ++wv) gv += sh.red[1][wv][t];
+            gout = gv;
+        }
+    }
+}
+
+template <bool GATE, bool ADD>
+__device__ __forceinline__ float epilogue(float v, float gv, const float *__restrict__ add, uint32_t row) {
+    if constexpr (ADD) v += add[row];
+    if constexpr (GATE) v *= silu(gv);
+    return v;
+}
+
+// Workgroup b covers row tile rt and K chunk s of `split`.  Blocks are
+// remapped so the chunks of one row tile run on one XCD (the hardware deals
+// workgroups to the 8 XCDs round robin).
+__device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t n) {
+    const uint32_t xcd = b & 7u, idx = b >> 3, per = n >> 3, rem = n & 7u;
+    return xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+}
+
+template <bool GATE, bool ADD>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args) {
+    __shared__ Shared sh;
+    const uint32_t groups = args.cols / kGroup;
+    const uint32_t split = args.split;
+    const uint32_t logical = xcd_remap(blockIdx.x, gridDim.x);
+    const uint32_t rt = logical / split, s = logical % split;
+    const uint32_t g_begin = static_cast<uint32_t>((static_cast<uint64_t>(s) * groups) / split);
+    const uint32_t g_end = static_cast<uint32_t>((static_cast<uint64_t>(s + 1) * groups) / split);
+    float v = 0.f, gv = 0.f;
+    tile_row_partial<GATE>(sh, args.w, args.gate, args.x, args.cols, rt, g_begin, g_end, v, gv);
+    const uint32_t row = rt * kTileRows + (threadIdx.x & 31);
+    if (split == 1) {
+        if (threadIdx.x < 32) args.y[row] = epilogue<GATE, ADD>(v, gv, args.add, row);
+        return;
+    }
+    // Split K: publish this chunk, then the last workgroup of the row tile
+    // sums the chunks in chunk order.
+    if (threadIdx.x < 32) {
+        args.partial[static_cast<size_t>(s) * args.rows + row] = v;
+        if constexpr (GATE) args.partial[static_cast<size_t>(split + s) * args.rows + row] = gv;
+    }
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev = atomicAdd(&args.counters[rt], 1u);
+        sh.last = (prev == split - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (sh.last == 0u) return;
+    __threadfence();
+    if (threadIdx.x < 32) {
+        float sum = 0.f, gsum = 0.f;
+        for (uint32_t c = 0; c < split; ++c) {
+            sum = (c == 0) ? args.partial[row] : sum + args.partial[static_cast<size_t>(c) * args.rows + row];
+            if constexpr (GATE) {
+                const float p = args.partial[static_cast<size_t>(split + c) * args.rows + row];
+                gsum = (c == 0) ? p : gsum + p;
+            }
+        }
+        args.y[row] = epilogue<GATE, ADD>(sum, gsum, args.add, row);
+    }
+    if (threadIdx.x == 0) args.counters[rt] = 0u;
+}
+
+// Multi-tensor plan: a persistent grid sweeps work items (one row tile of one
+// GEMV, full K) in order; workgroup b takes items b, b + grid, ...
+__global__ __launch_bounds__(kThreads) void plan_kernel(const PlanDesc *__restrict__ descs,
+                                                        uint32_t count, uint32_t items) {
+    __shared__ Shared sh;
+    uint32_t d = 0;
+    for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
+        while (item >= descs[d + 1].item_begin) ++d;
+        const PlanDesc &desc = descs[d];
+        const uint32_t rt = item - desc.item_begin;
+        const uint32_t groups = desc.cols / kGroup;
+        const uint32_t row = rt * kTileRows + (threadIdx.x & 31);
+        float v = 0.f, gv = 0.f;
+        if (desc.gate != nullptr) {
+            tile_row_partial<true>(sh, desc.w, desc.gate, desc.x, desc.cols, rt, 0, groups, v, gv);
+            if (threadIdx.x < 32) {
+                if (desc.add != nullptr) v += desc.add[row];
+                desc.y[row] = v * silu(gv);
+            }
+        } else {
+            tile_row_partial<false>(sh, desc.w, nullptr, desc.x, desc.cols, rt, 0, groups, v, gv);
+            if (threadIdx.x < 32) desc.y[row] = desc.add != nullptr ? v + desc.add[row] : v;
+        }
+    }
+    (void)count;
+}
+
+// out[row][k] = fp32(scale) * code, one thread per code byte.
+__global__ __launch_bounds__(kThreads) void dequant_kernel(const uint8_t *__restrict__ w, uint32_t rows,
+                                                           uint32_t cols, float *__restrict__ out) {
+    const uint32_t groups = cols / kGroup;
+    const uint64_t total = static_cast<uint64_t>(rows) * cols / 2;
+    for (uint64_t idx = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+         idx += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        const uint64_t t = idx >> 10;
+        const uint32_t rem = static_cast<uint32_t>(idx & 1023u);
+        const uint32_t i = rem >> 5, l = rem & 31u;
+        const uint64_t rt = t / groups, g = t % groups;
+        const uint8_t *tile = w + t * kTileBytes;
+        const float scale = half_bits_to_float(tile[2 * l] | (static_cast<uint32_t>(tile[2 * l + 1]) << 8));
+        const uint8_t b = tile[64 + rem];
+        const int lo = static_cast<int>(static_cast<int8_t>(static_cast<uint8_t>(b << 4))) >> 4;
+        const int hi = static_cast<int>(static_cast<int8_t>(b)) >> 4;
+        const uint64_t row = rt * kTileRows + l;
+        const uint64_t k = g * kGroup + 2 * i;
+        out[row * cols + k] = scale * static_cast<float>(lo);
+        out[row * cols + k + 1] = scale * static_cast<float>(hi);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Packer: one thread per (row, group), bit-identical to the reference CPU
+// packers.  Contraction is off so every product and sum rounds exactly as the
+// sequential C++ code does; '/' is the correctly rounded IEEE division and
+// rintf ties to even like nearbyint under FE_TONEAREST.
+// ---------------------------------------------------------------------------
+#pragma clang fp contract(off)
+
+__device__ __forceinline__ float bits_to_float(uint32_t b) { return __uint_as_float(b); }
+
+// The reference packers' fp16 decode, subnormals halved as there
+// (source/q4rdna_sidecar_pack.cpp:73-94, 127-15-shift): the scale search runs
+// on it, so the packed bytes depend on it.  GEMV and dequant decode scales
+// exactly with v_cvt_f32_f16, as the reference's kernels do.
+__device__ float fp16_bits_to_float_packer(uint32_t value) {
+    const uint32_t sign = (value & 0x8000u) << 16;
+    uint32_t exponent = (value >> 10) & 0x1fu;
+    uint32_t mantissa = value & 0x03ffu;
+    if (exponent == 0) {
+        if (mantissa == 0) return bits_to_float(sign);
+        int shift = 0;
+        while ((mantissa & 0x0400u) == 0) {
+            mantissa <<= 1;
+            ++shift;
+        }
+        mantissa &= 0x03ffu;
+        exponent = static_cast<uint32_t>(127 - 15 - shift);
+    } else if (exponent == 31) {
+        exponent = 255;
+    } else {
+        exponent += 127 - 15;
+    }
+    return bits_to_float(sign | (exponent << 23) | (mantissa << 13));
+}
+
+// source/q4rdna_sidecar_pack.cpp:96-124 (NaN maps to inf there, kept).
+__device__ uint32_t float_to_fp16_bits(float value) {
+    const uint32_t bits = __float_as_uint(value);
+    const uint32_t sign = (bits >> 16) & 0x8000u;
+    const uint32_t mantissa = bits & 0x007fffffu;
+    const int exponent = static_cast<int>((bits >> 23) & 0xffu) - 127 + 15;
+    if (exponent <= 0) {
+        if (exponent < -10) return sign;
+        const uint32_t normalized = mantissa | 0x00800000u;
+        const int shift = 14 - exponent;
+        uint32_t rounded = normalized >> shift;
+        const uint32_t remainder = normalized & ((1u << shift) - 1u);
+        const uint32_t halfway = 1u << (shift - 1);
+        if (remainder > halfway || (remainder == halfway && (rounded & 1u))) ++rounded;
+        return sign | rounded;
+    }
+    if (exponent >= 31) return sign | 0x7c00u;
+    uint32_t rounded = mantissa >> 13;
+    const uint32_t remainder = mantissa & 0x1fffu;
+    if (remainder > 0x1000u || (remainder == 0x1000u && (rounded & 1u))) {
+        ++rounded;
+        if (rounded == 0x400u) {
+            if (exponent + 1 >= 31) return sign | 0x7c00u;
+            return sign | (static_cast<uint32_t>(exponent + 1) << 10);
+        }
+    }
+    return sign | (static_cast<uint32_t>(exponent) << 10) | rounded;
+}
+
+// int(t) of an integral float as x86-64 computes it (INT_MIN out of range),
+// which the reference's int(...) conversions yield on the CPU they ran on.
+__device__ __forceinline__ int x86_int(float t) {
+    if (!(t >= -2147483648.0f && t < 2147483648.0f)) return static_cast<int>(0x80000000u);
+    return static_cast<int>(t);
+}
+
+__device__ __forceinline__ int clamp_code(int v) { return v < -8 ? -8 : (v > 7 ? 7 : v); }
+__device__ __forceinline__ float max_ref(float a, float b) { return (a < b) ? b : a; }
+
+// source/q4rdna_sidecar_pack.cpp:126-129
+__device__ __forceinline__ int quantize_rne(float value, float scale) {
+    if (scale == 0.0f) return 0;
+    return clamp_code(x86_int(rintf(value / scale)));
+}
+
+// source/q4rdna_cpu_experiment.cpp:136-141
+__device__ __forceinline__ int quantize_round(float value, float scale) {
+    if (scale == 0.0f) return 0;
+    return clamp_code(x86_int(roundf(value / scale)));
+}
+
+// source/q4rdna_sidecar_pack.cpp:131-179
+__device__ uint32_t select_scale_sidecar(const float *v) {
+    float positive_max = 0.0f, negative_max = 0.0f;
+    for (int i = 0; i < 64; ++i) {
+        positive_max = max_ref(positive_max, v[i]);
+        negative_max = max_ref(negative_max, -v[i]);
+    }
+    if (positive_max == 0.0f && negative_max == 0.0f) return 0;
+    const float positive = max_ref(positive_max / 7.0f, negative_max / 8.0f);
+    const float negative = -max_ref(positive_max / 8.0f, negative_max / 7.0f);
+    const float factors[5] = {1.0f, 0.9f, 0.8f, 0.7f, 0.6f};
+    uint32_t best_bits = 0;
+    float best_error = __builtin_huge_valf();
+    for (int f = 0; f < 5; ++f) {
+        for (int sgn = 0; sgn < 2; ++sgn) {
+            uint32_t scale_bits = float_to_fp16_bits((sgn == 0 ? positive : negative) * factors[f]);
+            for (int iteration = 0; iteration < 12; ++iteration) {
+                const float scale = fp16_bits_to_float_packer(scale_bits);
+                float error = 0.0f;
+                for (int i = 0; i < 64; ++i) {
+                    const float delta = scale * static_cast<float>(quantize_rne(v[i], scale)) - v[i];
+                    error += delta * delta;
+                }
+                if (error < best_error) {
+                    best_error = error;
+                    best_bits = scale_bits;
+                }
+                float numerator = 0.0f, denominator = 0.0f;
+                for (int i = 0; i < 64; ++i) {
+                    const int quant = quantize_rne(v[i], scale);
+                    numerator += v[i] * static_cast<float>(quant);
+                    denominator += static_cast<float>(quant * quant);
+                }
+                if (denominator == 0.0f) break;
+                const uint32_t next_bits = float_to_fp16_bits(numerator / denominator);
+                if (next_bits == scale_bits) break;
+                scale_bits = next_bits;
+            }
+        }
+    }
+    return best_bits;
+}
+
+// source/q4rdna_cpu_experiment.cpp:143-152
+__device__ double experiment_error(const float *v, uint32_t scale_bits) {
+    const float scale = fp16_bits_to_float_packer(scale_bits);
+    double error = 0.0;
+    for (int i = 0; i < 64; ++i) {
+        const int quant = quantize_round(v[i], scale);
+        const double delta = static_cast<double>(scale) * static_cast<double>(quant) - static_cast<double>(v[i]);
+        error += delta * delta;
+    }
+    return error;
+}
+
+// source/q4rdna_cpu_experiment.cpp:154-164
+__device__ void consider_scale(const float *v, float scale, uint32_t &best_bits, double &best_error) {
+    if (!isfinite(scale)) return;
+    const uint32_t bits = float_to_fp16_bits(scale);
+    const double error = experiment_error(v, bits);
+    if (error < best_error) {
+        best_bits = bits;
+        best_error = error;
+    }
+}
+
+// source/q4rdna_cpu_experiment.cpp:166-195
+__device__ void refine_mse_scale(const float *v, float initial, uint32_t &best_bits, double &best_error) {
+    uint32_t scale_bits = float_to_fp16_bits(initial);
+    for (int iteration = 0; iteration < 12; ++iteration) {
+        const float scale = fp16_bits_to_float_packer(scale_bits);
+        consider_scale(v, scale, best_bits, best_error);
+        double numerator = 0.0, denominator = 0.0;
+        for (int i = 0; i < 64; ++i) {
+            const int quant = quantize_round(v[i], scale);
+            numerator += static_cast<double>(v[i]) * static_cast<double>(quant);
+            denominator += static_cast<double>(quant) * static_cast<double>(quant);
+        }
+        if (denominator == 0.0) break;
+        const uint32_t next_bits = float_to_fp16_bits(static_cast<float>(numerator / denominator));
+        if (next_bits == scale_bits) break;
+        scale_bits = next_bits;
+    }
+    if ((best_bits & 0x7fffu) != 0 && (best_bits & 0x7fffu) < 0x7bffu) {
+        const uint32_t magnitude = best_bits & 0x7fffu, sign = best_bits & 0x8000u;
+        consider_scale(v, fp16_bits_to_float_packer(sign | (magnitude - 1u)), best_bits, best_error);
+        consider_scale(v, fp16_bits_to_float_packer(sign | (magnitude + 1u)), best_bits, best_error);
+    }
+}
+
+// source/q4rdna_cpu_experiment.cpp:197-237
+__device__ uint32_t select_scale_experiment(const float *v, int algorithm) {
+    float positive_max = 0.0f, negative_max = 0.0f, max_abs = 0.0f;
+    for (int i = 0; i < 64; ++i) {
+        positive_max = max_ref(positive_max, v[i]);
+        negative_max = max_ref(negative_max, -v[i]);
+        max_abs = max_ref(max_abs, fabsf(v[i]));
+    }
+    if (max_abs == 0.0f) return 0;
+    if (algorithm == 1) return float_to_fp16_bits(max_abs / 7.0f);
+    const float positive_range = max_ref(positive_max / 7.0f, negative_max / 8.0f);
+    const float negative_range = -max_ref(positive_max / 8.0f, negative_max / 7.0f);
+    uint32_t best_bits = 0;
+    double best_error = __builtin_huge_val();
+    consider_scale(v, positive_range, best_bits, best_error);
+    consider_scale(v, negative_range, best_bits, best_error);
+    if (algorithm == 2) return best_bits;
+    const float factors[12] = {1.0f, 0.9f, 0.8f, 0.7f, 0.6f, 0.55f, 0.5f, 0.45f, 0.4f, 0.35f, 0.3f, 0.25f};
+    for (int f = 0; f < 12; ++f) {
+        refine_mse_scale(v, positive_range * factors[f], best_bits, best_error);
+        refine_mse_scale(v, negative_range * factors[f], best_bits, best_error);
+    }
+    return best_bits;
+}
+
+// Thread per (row, group) ordered (row tile, group, row lane) so a wave's
+// scale and code stores land in contiguous bytes of one tile.
+__global__ __launch_bounds__(kThreads) void pack_kernel(const float *__restrict__ w, uint32_t rows,
+                                                        uint32_t cols, int algorithm,
+                                                        uint8_t *__restrict__ tiles) {
+    const uint32_t groups = cols / kGroup;
+    const uint64_t total = static_cast<uint64_t>(rows) * groups;
+    for (uint64_t idx = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+         idx += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        const uint64_t t = idx >> 5;
+        const uint32_t l = static_cast<uint32_t>(idx & 31u);
+        const uint64_t rt = t / groups, g = t % groups;
+        const uint64_t row = rt * kTileRows + l;
+        float v[64];
+        const float4 *src = reinterpret_cast<const float4 *>(w + row * cols + g * kGroup);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float4 f = src[i];
+            v[4 * i] = f.x;
+            v[4 * i + 1] = f.y;
+            v[4 * i + 2] = f.z;
+            v[4 * i + 3] = f.w;
+        }
+        const uint32_t bits = algorithm == 0 ? select_scale_sidecar(v) : select_scale_experiment(v, algorithm);
+        const float scale = fp16_bits_to_float_packer(bits);
+        uint8_t *tile = tiles + t * kTileBytes;
+        tile[2 * l] = static_cast<uint8_t>(bits & 0xffu);
+        tile[2 * l + 1] = static_cast<uint8_t>(bits >> 8);
+        for (int i = 0; i < 32; ++i) {
+            const int lo = algorithm == 0 ? quantize_rne(v[2 * i], scale) : quantize_round(v[2 * i], scale);
+            const int hi = algorithm == 0 ? quantize_rne(v[2 * i + 1], scale) : quantize_round(v[2 * i + 1], scale);
+            tile[64 + 32 * i + l] = static_cast<uint8_t>((lo & 15) | ((hi & 15) << 4));
+        }
+    }
+}
+
+#pragma clang fp contract(on)
+
+template <bool GATE, bool ADD>
+hipError_t launch_gemv_t(const GemvArgs &args, hipStream_t stream) {
+    const uint32_t blocks = (args.rows / kTileRows) * args.split;
+    hipLaunchKernelGGL((gemv_kernel<GATE, ADD>), dim3(blocks), dim3(kThreads), 0, stream, args);
+    return hipGetLastError();
+}
+
+uint32_t grid_for(uint64_t work, uint32_t per_block) {
+    uint64_t blocks = (work + per_block - 1) / per_block;
+    if (blocks > 65536) blocks = 65536;
+    return static_cast<uint32_t>(blocks == 0 ? 1 : blocks);
+}
+
+}  // namespace
+
+hipError_t launch_gemv(const GemvArgs &args, hipStream_t stream) {
+    if (args.gate != nullptr) {
+        return args.add != nullptr ? launch_gemv_t<true, true>(args, stream)
+                                   : launch_gemv_t<true, false>(args, stream);
+    }
+    return args.add != nullptr ? launch_gemv_t<false, true>(args, stream)
+                               : launch_gemv_t<false, false>(args, stream);
+}
+
+hipError_t launch_plan(const PlanDesc *descs, uint32_t count, uint32_t items, uint32_t workgroups,
+                       hipStream_t stream) {
+    hipLaunchKernelGGL(plan_kernel, dim3(workgroups), dim3(kThreads), 0, stream, descs, count, items);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant(const uint8_t *w, uint32_t rows, uint32_t cols, float *out, hipStream_t stream) {
+    const uint64_t work = static_cast<uint64_t>(rows) * cols / 2;
+    hipLaunchKernelGGL(dequant_kernel, dim3(grid_for(work, kThreads)), dim3(kThreads), 0, stream, w, rows,
+                       cols, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack(const float *w, uint32_t rows, uint32_t cols, int algorithm, uint8_t *tiles,
+                       hipStream_t stream) {
+    const uint64_t work = static_cast<uint64_t>(rows) * (cols / kGroup);
+    hipLaunchKernelGGL(pack_kernel, dim3(grid_for(work, kThreads)), dim3(kThreads), 0, stream, w, rows, cols,
+                       algorithm, tiles);
+    return hipGetLastError();
+}
+
+uint32_t plan_workgroups_per_cu() { return 4; }
+
+}  // namespace q4rdna

@@ -1,0 +1,620 @@
+// Host runtime of the Q4_RDNA dequant-GEMV C ABI (include/q4rdna.h): sidecar
+// parsing and upload, the name registry, shape policy, split-K workspaces and
+// the entry points.  All compute runs in the gfx950 kernels of
+// q4rdna_kernels.hip; this file never computes a result on the CPU.
+#include "q4rdna.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <utility>
+#include <vector>
+
+#include "q4rdna_internal.h"
+
+namespace {
+
+using q4rdna::kGroup;
+using q4rdna::kTileBytes;
+using q4rdna::kTileRows;
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(Q4RDNA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// On-disk structures, little endian (source/q4rdna.cu:26-50).
+#pragma pack(push, 1)
+struct FileHeader {
+    char magic[8];
+    uint32_t version;
+    uint32_t count;
+    uint32_t group;
+    uint32_t tile_rows;
+    uint32_t tile_bytes;
+    uint32_t reserved;
+    uint64_t data_offset;
+    uint64_t data_bytes;
+};
+struct FileEntry {
+    char name[64];
+    uint32_t rows;
+    uint32_t columns;
+    uint64_t offset;
+    uint64_t size;
+    uint64_t reserved;
+};
+#pragma pack(pop)
+static_assert(sizeof(FileHeader) == 48, "sidecar header is 48 bytes");
+static_assert(sizeof(FileEntry) == 96, "sidecar entry is 96 bytes");
+
+struct Entry {
+    std::string name;
+    uint32_t rows;
+    uint32_t columns;
+    uint64_t offset;
+    uint64_t size;
+};
+
+// Restores the calling thread's current device on scope exit.
+class DeviceGuard {
+public:
+    explicit DeviceGuard(int device) {
+        if (hipGetDevice(&saved_) != hipSuccess) saved_ = -1;
+        if (saved_ != device) ok_ = hipSetDevice(device) == hipSuccess;
+    }
+    ~DeviceGuard() {
+        if (saved_ >= 0) (void)hipSetDevice(saved_);
+    }
+    bool ok() const { return ok_; }
+
+private:
+    int saved_ = -1;
+    bool ok_ = true;
+};
+
+int current_device() {
+    int d = -1;
+    if (hipGetDevice(&d) != hipSuccess) return -1;
+    return d;
+}
+
+uint32_t cu_count(int device) {
+    static std::mutex mu;
+    static std::map<int, uint32_t> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(device);
+    if (it != cache.end()) return it->second;
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n <= 0) n = 256;
+    cache[device] = static_cast<uint32_t>(n);
+    return static_cast<uint32_t>(n);
+}
+
+// Parse and validate a header + index (loader rules of source/q4rdna.cu:129-155
+// and the data-length check of :163-170).
+int parse_index(const uint8_t *image, uint64_t image_size, uint64_t file_size, FileHeader *header,
+                std::vector<Entry> *entries) {
+    if (image == nullptr) return fail(Q4RDNA_ERR_ARGUMENT, "sidecar image is NULL");
+    if (image_size < sizeof(FileHeader) || file_size < sizeof(FileHeader))
+        return fail(Q4RDNA_ERR_FORMAT, "invalid sidecar header: truncated");
+    FileHeader h;
+    std::memcpy(&h, image, sizeof(h));
+    if (std::memcmp(h.magic, "Q4RDNA1", 8) != 0 || h.version != 1 || h.group != kGroup ||
+        h.tile_rows != kTileRows || h.tile_bytes != kTileBytes)
+        return fail(Q4RDNA_ERR_FORMAT, "invalid sidecar header");
+    const uint64_t index_end = sizeof(FileHeader) + static_cast<uint64_t>(h.count) * sizeof(FileEntry);
+    if (file_size < index_end) return fail(Q4RDNA_ERR_FORMAT, "truncated sidecar index");
+    if (image_size < index_end)
+        return fail(Q4RDNA_ERR_ARGUMENT, "image holds %llu bytes, the index ends at %llu",
+                    static_cast<unsigned long long>(image_size), static_cast<unsigned long long>(index_end));
+    std::vector<Entry> out;
+    out.reserve(h.count);
+    for (uint32_t i = 0; i < h.count; ++i) {
+        FileEntry e;
+        std::memcpy(&e, image + sizeof(FileHeader) + static_cast<uint64_t>(i) * sizeof(FileEntry), sizeof(e));
+        if (std::memchr(e.name, '\0', sizeof(e.name)) == nullptr || e.offset < h.data_offset ||
+            e.offset + e.size < e.offset || e.offset + e.size > h.data_offset + h.data_bytes ||
+            e.rows % kTileRows != 0 || e.columns % kGroup != 0 ||
+            e.size != static_cast<uint64_t>(e.rows) * e.columns * 34 / kGroup)
+            return fail(Q4RDNA_ERR_FORMAT, "invalid sidecar entry %u", i);
+        out.push_back(Entry{std::string(e.name), e.rows, e.columns, e.offset, e.size});
+    }
+    if (h.data_offset > file_size || h.data_bytes > file_size - h.data_offset)
+        return fail(Q4RDNA_ERR_FORMAT, "truncated sidecar data");
+    if (header) *header = h;
+    if (entries) *entries = std::move(out);
+    return Q4RDNA_OK;
+}
+
+// Split-K scratch per (device, stream): partial sums and per-row-tile
+// arrival counters (kept zero between launches by the kernel itself).
+struct Workspace {
+    float *partial = nullptr;
+    uint32_t *counters = nullptr;
+    size_t partial_floats = 0;
+    size_t counter_count = 0;
+};
+
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+
+int get_workspace(int device, hipStream_t stream, size_t partial_floats, size_t counters, Workspace **out) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    Workspace &ws = g_ws[{device, stream}];
+    if (ws.partial_floats < partial_floats || ws.counter_count < counters) {
+        const size_t pf = std::max(partial_floats, ws.partial_floats);
+        const size_t cc = std::max(counters, ws.counter_count);
+        if (ws.partial != nullptr || ws.counters != nullptr) {
+            // Launches already queued on this stream may still use the old
+            // buffers: wait for them before releasing.
+            hipError_t e = hipStreamSynchronize(stream);
+            if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+            (void)hipFree(ws.partial);
+            (void)hipFree(ws.counters);
+            ws = Workspace{};
+        }
+        float *p = nullptr;
+        uint32_t *c = nullptr;
+        hipError_t e = hipMalloc(&p, pf * sizeof(float));
+        if (e != hipSuccess) return fail(Q4RDNA_ERR_MEMORY, "split-K workspace: %s", hipGetErrorString(e));
+        e = hipMalloc(&c, cc * sizeof(uint32_t));
+        if (e != hipSuccess) {
+            (void)hipFree(p);
+            return fail(Q4RDNA_ERR_MEMORY, "split-K counters: %s", hipGetErrorString(e));
+        }
+        e = hipMemset(c, 0, cc * sizeof(uint32_t));
+        if (e != hipSuccess) {
+            (void)hipFree(p);
+            (void)hipFree(c);
+            return hip_fail(e, "hipMemset");
+        }
+        ws.partial = p;
+        ws.counters = c;
+        ws.partial_floats = pf;
+        ws.counter_count = cc;
+    }
+    *out = &ws;
+    return Q4RDNA_OK;
+}
+
+bool valid_shape(uint32_t rows, uint32_t cols) {
+    return rows > 0 && cols > 0 && rows % kTileRows == 0 && cols % kGroup == 0;
+}
+
+bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+constexpr uint32_t kMaxSplit = 64;
+
+uint32_t policy_split(uint32_t rows, uint32_t cols, int device) {
+    // Fill the chip with ~4 workgroups (16 waves) per CU, keeping at least
+    // two groups per wave in every K chunk.
+    const uint32_t tiles = rows / kTileRows;
+    const uint32_t groups = cols / kGroup;
+    const uint32_t target = cu_count(device) * 4;
+    uint32_t split = (target + tiles - 1) / tiles;
+    const uint32_t max_by_groups = std::max<uint32_t>(1, groups / 8);
+    split = std::min(split, max_by_groups);
+    split = std::min(split, kMaxSplit);
+    return std::max<uint32_t>(split, 1);
+}
+
+int launch_one(const q4rdna_weight *w, const uint8_t *gate, const float *x, const float *add, float *y,
+               uint32_t split, hipStream_t stream) {
+    q4rdna::GemvArgs args{};
+    args.w = w->tiles;
+    args.gate = gate;
+    args.x = x;
+    args.add = add;
+    args.y = y;
+    args.rows = w->rows;
+    args.cols = w->columns;
+    const uint32_t groups = w->columns / kGroup;
+    if (split == 0) split = policy_split(w->rows, w->columns, w->device);
+    split = std::min(split, groups);
+    split = std::min(split, kMaxSplit);
+    args.split = std::max<uint32_t>(split, 1);
+    if (args.split > 1) {
+        Workspace *ws = nullptr;
+        const size_t pf = static_cast<size_t>(args.split) * w->rows * (gate ? 2 : 1);
+        int rc = get_workspace(w->device, stream, pf, w->rows / kTileRows, &ws);
+        if (rc != Q4RDNA_OK) return rc;
+        args.partial = ws->partial;
+        args.counters = ws->counters;
+    }
+    hipError_t e = q4rdna::launch_gemv(args, stream);
+    if (e != hipSuccess) return hip_fail(e, "GEMV launch");
+    return Q4RDNA_OK;
+}
+
+// Preconditions shared by the GEMV entry points.  NOT_APPLICABLE mirrors the
+// reference's `return false` (source/q4rdna.cu:718-733,753-758,776-783).
+int check_weight(const q4rdna_weight *w) {
+    if (w == nullptr || w->tiles == nullptr) return fail(Q4RDNA_NOT_APPLICABLE, "no weight");
+    if (!valid_shape(w->rows, w->columns)) return fail(Q4RDNA_ERR_ARGUMENT, "invalid weight shape %ux%u", w->rows, w->columns);
+    if (!aligned(w->tiles, 16)) return fail(Q4RDNA_ERR_ARGUMENT, "weight tiles must be 16-byte aligned");
+    if (current_device() != w->device)
+        return fail(Q4RDNA_NOT_APPLICABLE, "weight lives on device %d, current device is %d", w->device, current_device());
+    return Q4RDNA_OK;
+}
+
+int check_io(const float *x, const float *y) {
+    if (x == nullptr || y == nullptr) return fail(Q4RDNA_ERR_ARGUMENT, "NULL activation or output");
+    if (!aligned(x, 4) || !aligned(y, 4)) return fail(Q4RDNA_ERR_ARGUMENT, "activation/output must be 4-byte aligned");
+    return Q4RDNA_OK;
+}
+
+}  // namespace
+
+struct q4rdna_sidecar {
+    int device = 0;
+    uint8_t *data = nullptr;
+    uint64_t data_offset = 0;
+    uint64_t data_bytes = 0;
+    std::vector<Entry> entries;
+    std::unordered_map<std::string, uint32_t> by_name;
+};
+
+struct q4rdna_plan {
+    int device = 0;
+    q4rdna::PlanDesc *descs = nullptr;
+    uint32_t count = 0;
+    uint32_t items = 0;
+    uint32_t workgroups = 0;
+};
+
+namespace {
+
+// Upload helper shared by open() and open_memory(): `read` fills a host
+// chunk of the data region starting at a data-relative offset.
+template <typename ReadFn>
+int finish_open(const FileHeader &h, std::vector<Entry> &&entries, int device, ReadFn read, q4rdna_sidecar **out) {
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
+        return fail(Q4RDNA_ERR_ARGUMENT, "device %d is not available", device);
+    DeviceGuard guard(device);
+    if (!guard.ok()) return fail(Q4RDNA_ERR_HIP, "hipSetDevice(%d) failed", device);
+    auto sc = std::make_unique<q4rdna_sidecar>();
+    sc->device = device;
+    sc->data_offset = h.data_offset;
+    sc->data_bytes = h.data_bytes;
+    if (h.data_bytes > 0) {
+        hipError_t e = hipMalloc(&sc->data, h.data_bytes);
+        if (e != hipSuccess) return fail(Q4RDNA_ERR_MEMORY, "sidecar upload: %s", hipGetErrorString(e));
+        constexpr size_t kChunk = 64u << 20;  // source/q4rdna.cu:160
+        std::vector<uint8_t> host(std::min<uint64_t>(kChunk, h.data_bytes));
+        for (uint64_t copied = 0; copied < h.data_bytes;) {
+            const size_t n = static_cast<size_t>(std::min<uint64_t>(kChunk, h.data_bytes - copied));
+            if (!read(copied, host.data(), n)) {
+                (void)hipFree(sc->data);
+                return fail(Q4RDNA_ERR_FORMAT, "truncated sidecar data");
+            }
+            e = hipMemcpy(sc->data + copied, host.data(), n, hipMemcpyHostToDevice);
+            if (e != hipSuccess) {
+                (void)hipFree(sc->data);
+                return hip_fail(e, "sidecar upload");
+            }
+            copied += n;
+        }
+    }
+    sc->entries = std::move(entries);
+    for (uint32_t i = 0; i < sc->entries.size(); ++i) sc->by_name.emplace(sc->entries[i].name, i);
+    *out = sc.release();
+    return Q4RDNA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int q4rdna_abi_version(void) { return Q4RDNA_ABI_VERSION; }
+
+const char *q4rdna_last_error(void) { return g_last_error.c_str(); }
+
+int q4rdna_sidecar_inspect(const void *image, uint64_t image_size, uint64_t file_size, uint32_t *count) {
+    FileHeader h;
+    int rc = parse_index(static_cast<const uint8_t *>(image), image_size, file_size, &h, nullptr);
+    if (rc != Q4RDNA_OK) return rc;
+    if (count) *count = h.count;
+    return Q4RDNA_OK;
+}
+
+int q4rdna_sidecar_open(const char *path, int device, q4rdna_sidecar **out) {
+    if (path == nullptr || out == nullptr) return fail(Q4RDNA_ERR_ARGUMENT, "NULL path or handle");
+    *out = nullptr;
+    std::ifstream in(path, std::ios::binary | std::ios::ate);
+    if (!in) return fail(Q4RDNA_ERR_IO, "cannot open %s", path);
+    const uint64_t file_size = static_cast<uint64_t>(in.tellg());
+    std::vector<uint8_t> head(std::min<uint64_t>(file_size, sizeof(FileHeader)));
+    in.seekg(0);
+    if (!in.read(reinterpret_cast<char *>(head.data()), static_cast<std::streamsize>(head.size())))
+        return fail(Q4RDNA_ERR_IO, "cannot read %s", path);
+    FileHeader h{};
+    if (head.size() == sizeof(FileHeader)) std::memcpy(&h, head.data(), sizeof(h));
+    const uint64_t index_end = sizeof(FileHeader) + static_cast<uint64_t>(h.count) * sizeof(FileEntry);
+    std::vector<uint8_t> image(static_cast<size_t>(std::min(index_end, file_size)));
+    in.seekg(0);
+    if (!in.read(reinterpret_cast<char *>(image.data()), static_cast<std::streamsize>(image.size())))
+        return fail(Q4RDNA_ERR_IO, "cannot read %s", path);
+    std::vector<Entry> entries;
+    int rc = parse_index(image.data(), image.size(), file_size, &h, &entries);
+    if (rc != Q4RDNA_OK) return rc;
+    auto read = [&in, &h](uint64_t rel, uint8_t *dst, size_t n) {
+        in.seekg(static_cast<std::streamoff>(h.data_offset + rel));
+        return static_cast<bool>(in.read(reinterpret_cast<char *>(dst), static_cast<std::streamsize>(n)));
+    };
+    return finish_open(h, std::move(entries), device, read, out);
+}
+
+int q4rdna_sidecar_open_memory(const void *image, uint64_t size, int device, q4rdna_sidecar **out) {
+    if (image == nullptr || out == nullptr) return fail(Q4RDNA_ERR_ARGUMENT, "NULL image or handle");
+    *out = nullptr;
+    FileHeader h;
+    std::vector<Entry> entries;
+    const auto *bytes = static_cast<const uint8_t *>(image);
+    int rc = parse_index(bytes, size, size, &h, &entries);
+    if (rc != Q4RDNA_OK) return rc;
+    auto read = [bytes, &h](uint64_t rel, uint8_t *dst, size_t n) {
+        std::memcpy(dst, bytes + h.data_offset + rel, n);
+        return true;
+    };
+    return finish_open(h, std::move(entries), device, read, out);
+}
+
+void q4rdna_sidecar_close(q4rdna_sidecar *sidecar) {
+    if (sidecar == nullptr) return;
+    if (sidecar->data != nullptr) {
+        DeviceGuard guard(sidecar->device);
+        (void)hipFree(sidecar->data);
+    }
+    delete sidecar;
+}
+
+uint32_t q4rdna_sidecar_count(const q4rdna_sidecar *sidecar) {
+    return sidecar ? static_cast<uint32_t>(sidecar->entries.size()) : 0u;
+}
+
+int q4rdna_sidecar_entry(const q4rdna_sidecar *sidecar, uint32_t index, char name[64], uint32_t *rows,
+                         uint32_t *columns, uint64_t *offset, uint64_t *size) {
+    if (sidecar == nullptr || index >= sidecar->entries.size())
+        return fail(Q4RDNA_ERR_ARGUMENT, "entry %u out of range", index);
+    const Entry &e = sidecar->entries[index];
+    if (name) {
+        std::memset(name, 0, 64);
+        std::memcpy(name, e.name.data(), std::min<size_t>(e.name.size(), 63));
+    }
+    if (rows) *rows = e.rows;
+    if (columns) *columns = e.columns;
+    if (offset) *offset = e.offset;
+    if (size) *size = e.size;
+    return Q4RDNA_OK;
+}
+
+int q4rdna_find(const q4rdna_sidecar *sidecar, const char *name, int64_t ne0, int64_t ne1, q4rdna_weight *out) {
+    if (sidecar == nullptr || name == nullptr || out == nullptr)
+        return fail(Q4RDNA_NOT_APPLICABLE, "no sidecar or name");
+    auto it = sidecar->by_name.find(name);
+    if (it == sidecar->by_name.end()) return fail(Q4RDNA_NOT_APPLICABLE, "%s is not in the sidecar", name);
+    const Entry &e = sidecar->entries[it->second];
+    if (ne0 != static_cast<int64_t>(e.columns) || ne1 != static_cast<int64_t>(e.rows))
+        return fail(Q4RDNA_NOT_APPLICABLE, "shape mismatch for %s", name);
+    out->tiles = sidecar->data + (e.offset - sidecar->data_offset);
+    out->rows = e.rows;
+    out->columns = e.columns;
+    out->device = sidecar->device;
+    out->reserved = 0;
+    return Q4RDNA_OK;
+}
+
+int q4rdna_weight_from_device(const void *tiles, uint32_t rows, uint32_t columns, int device, q4rdna_weight *out) {
+    if (tiles == nullptr || out == nullptr) return fail(Q4RDNA_ERR_ARGUMENT, "NULL tiles or output");
+    if (!valid_shape(rows, columns)) return fail(Q4RDNA_ERR_ARGUMENT, "shape %ux%u is not 32-row x 64-column tiled", rows, columns);
+    if (!aligned(tiles, 16)) return fail(Q4RDNA_ERR_ARGUMENT, "tiles must be 16-byte aligned");
+    out->tiles = static_cast<const uint8_t *>(tiles);
+    out->rows = rows;
+    out->columns = columns;
+    out->device = device;
+    out->reserved = 0;
+    return Q4RDNA_OK;
+}
+
+q4rdna_sidecar *q4rdna_default_sidecar(int device) {
+    static std::once_flag once;
+    static q4rdna_sidecar *value = nullptr;
+    std::call_once(once, [device]() {
+        const char *path = std::getenv("LLAMA_Q4_RDNA_SIDECAR");
+        if (path == nullptr || path[0] == '\0') return;
+        q4rdna_sidecar *sc = nullptr;
+        if (q4rdna_sidecar_open(path, device, &sc) != Q4RDNA_OK) {
+            std::fprintf(stderr, "Q4_RDNA: %s\n", g_last_error.c_str());
+            return;
+        }
+        std::fprintf(stderr, "Q4_RDNA: loaded %u tensors, %.2f GiB on device %d from %s\n",
+                     static_cast<unsigned>(sc->entries.size()),
+                     static_cast<double>(sc->data_bytes) / (1024.0 * 1024.0 * 1024.0), device, path);
+        value = sc;
+    });
+    if (value == nullptr || value->device != device) return nullptr;
+    return value;
+}
+
+int q4rdna_scope_allows(const char *scope, const char *name) {
+    if (name == nullptr) return 0;
+    if (scope == nullptr || scope[0] == '\0') return 1;
+    if (std::strcmp(scope, "ffn") == 0 && std::strstr(name, ".ffn_") == nullptr) return 0;
+    if (std::strcmp(scope, "qkv-fallback") == 0 &&
+        (std::strstr(name, ".attn_q.") != nullptr || std::strstr(name, ".attn_k.") != nullptr ||
+         std::strstr(name, ".attn_v.") != nullptr))
+        return 0;
+    if (std::strcmp(scope, "hotspot") == 0 && std::strstr(name, ".ffn_gate.") == nullptr &&
+        std::strstr(name, ".ffn_up.") == nullptr)
+        return 0;
+    if (std::strcmp(scope, "attn") == 0 && std::strstr(name, ".attn_") == nullptr) return 0;
+    return 1;
+}
+
+uint32_t q4rdna_policy_split_k(uint32_t rows, uint32_t columns, int device) {
+    if (!valid_shape(rows, columns)) return 0;
+    return policy_split(rows, columns, device);
+}
+
+int q4rdna_mul_mat(const q4rdna_weight *w, const float *x, int64_t x_ne0, float *y, int64_t y_ne0, void *stream) {
+    int rc = check_weight(w);
+    if (rc != Q4RDNA_OK) return rc;
+    if (x_ne0 != static_cast<int64_t>(w->columns) || y_ne0 != static_cast<int64_t>(w->rows))
+        return fail(Q4RDNA_NOT_APPLICABLE, "shape mismatch: x %lld (K %u), y %lld (M %u)",
+                    static_cast<long long>(x_ne0), w->columns, static_cast<long long>(y_ne0), w->rows);
+    if ((rc = check_io(x, y)) != Q4RDNA_OK) return rc;
+    return launch_one(w, nullptr, x, nullptr, y, 0, static_cast<hipStream_t>(stream));
+}
+
+int q4rdna_mul_mat_add(const q4rdna_weight *w, const float *x, int64_t x_ne0, const float *add, int64_t add_ne,
+                       float *y, int64_t y_ne0, void *stream) {
+    int rc = check_weight(w);
+    if (rc != Q4RDNA_OK) return rc;
+    if (x_ne0 != static_cast<int64_t>(w->columns) || y_ne0 != static_cast<int64_t>(w->rows) ||
+        add_ne != static_cast<int64_t>(w->rows))
+        return fail(Q4RDNA_NOT_APPLICABLE, "shape mismatch");
+    if ((rc = check_io(x, y)) != Q4RDNA_OK) return rc;
+    if (add == nullptr || !aligned(add, 4)) return fail(Q4RDNA_ERR_ARGUMENT, "NULL or misaligned add");
+    return launch_one(w, nullptr, x, add, y, 0, static_cast<hipStream_t>(stream));
+}
+
+int q4rdna_mul_mat_glu(const q4rdna_weight *up, const q4rdna_weight *gate, const float *x, int64_t x_ne0, int glu_op,
+                       float *y, int64_t y_ne0, void *stream) {
+    if (glu_op != Q4RDNA_GLU_SWIGLU) return fail(Q4RDNA_NOT_APPLICABLE, "only SwiGLU is handled");
+    int rc = check_weight(up);
+    if (rc != Q4RDNA_OK) return rc;
+    if ((rc = check_weight(gate)) != Q4RDNA_OK) return rc;
+    if (up->rows != gate->rows || up->columns != gate->columns || up->device != gate->device)
+        return fail(Q4RDNA_NOT_APPLICABLE, "up and gate shapes differ");
+    if (x_ne0 != static_cast<int64_t>(up->columns) || y_ne0 != static_cast<int64_t>(up->rows))
+        return fail(Q4RDNA_NOT_APPLICABLE, "shape mismatch");
+    if ((rc = check_io(x, y)) != Q4RDNA_OK) return rc;
+    return launch_one(up, gate->tiles, x, nullptr, y, 0, static_cast<hipStream_t>(stream));
+}
+
+int q4rdna_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x, const float *add, float *y,
+                      const q4rdna_launch_options *options, void *stream) {
+    int rc = check_weight(w);
+    if (rc != Q4RDNA_OK) return rc;
+    if (gate != nullptr) {
+        if ((rc = check_weight(gate)) != Q4RDNA_OK) return rc;
+        if (gate->rows != w->rows || gate->columns != w->columns) return fail(Q4RDNA_NOT_APPLICABLE, "up and gate shapes differ");
+    }
+    if ((rc = check_io(x, y)) != Q4RDNA_OK) return rc;
+    if (add != nullptr && !aligned(add, 4)) return fail(Q4RDNA_ERR_ARGUMENT, "misaligned add");
+    const uint32_t split = options ? options->split_k : 0;
+    if (split > kMaxSplit) return fail(Q4RDNA_ERR_ARGUMENT, "split_k %u exceeds %u", split, kMaxSplit);
+    return launch_one(w, gate ? gate->tiles : nullptr, x, add, y, split, static_cast<hipStream_t>(stream));
+}
+
+int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device, q4rdna_plan **out) {
+    if (out == nullptr || (descs == nullptr && count > 0)) return fail(Q4RDNA_ERR_ARGUMENT, "NULL descriptors or handle");
+    *out = nullptr;
+    std::vector<q4rdna::PlanDesc> host(static_cast<size_t>(count) + 1);
+    uint64_t items = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        const q4rdna_gemv_desc &d = descs[i];
+        if (d.weight.tiles == nullptr || d.x == nullptr || d.y == nullptr)
+            return fail(Q4RDNA_ERR_ARGUMENT, "descriptor %u has a NULL pointer", i);
+        if (!valid_shape(d.weight.rows, d.weight.columns) || !aligned(d.weight.tiles, 16) ||
+            (d.gate_tiles != nullptr && !aligned(d.gate_tiles, 16)))
+            return fail(Q4RDNA_ERR_ARGUMENT, "descriptor %u: invalid shape or alignment", i);
+        if (d.weight.device != device) return fail(Q4RDNA_ERR_ARGUMENT, "descriptor %u lives on device %d", i, d.weight.device);
+        q4rdna::PlanDesc &p = host[i];
+        p.w = d.weight.tiles;
+        p.gate = d.gate_tiles;
+        p.x = d.x;
+        p.add = d.add;
+        p.y = d.y;
+        p.rows = d.weight.rows;
+        p.cols = d.weight.columns;
+        p.item_begin = static_cast<uint32_t>(items);
+        items += d.weight.rows / kTileRows;
+        if (items > 0xffffffffull) return fail(Q4RDNA_ERR_ARGUMENT, "plan too large");
+    }
+    host[count] = q4rdna::PlanDesc{};
+    host[count].item_begin = static_cast<uint32_t>(items);
+    DeviceGuard guard(device);
+    if (!guard.ok()) return fail(Q4RDNA_ERR_HIP, "hipSetDevice(%d) failed", device);
+    auto plan = std::make_unique<q4rdna_plan>();
+    plan->device = device;
+    plan->count = count;
+    plan->items = static_cast<uint32_t>(items);
+    const uint32_t resident = cu_count(device) * q4rdna::plan_workgroups_per_cu();
+    plan->workgroups = std::max<uint32_t>(1, std::min<uint32_t>(resident, plan->items));
+    hipError_t e = hipMalloc(&plan->descs, host.size() * sizeof(q4rdna::PlanDesc));
+    if (e != hipSuccess) return fail(Q4RDNA_ERR_MEMORY, "plan table: %s", hipGetErrorString(e));
+    e = hipMemcpy(plan->descs, host.data(), host.size() * sizeof(q4rdna::PlanDesc), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(plan->descs);
+        return hip_fail(e, "plan upload");
+    }
+    *out = plan.release();
+    return Q4RDNA_OK;
+}
+
+int q4rdna_plan_launch(q4rdna_plan *plan, void *stream) {
+    if (plan == nullptr) return fail(Q4RDNA_ERR_ARGUMENT, "NULL plan");
+    if (current_device() != plan->device)
+        return fail(Q4RDNA_NOT_APPLICABLE, "plan lives on device %d, current device is %d", plan->device, current_device());
+    if (plan->items == 0) return Q4RDNA_OK;
+    hipError_t e = q4rdna::launch_plan(plan->descs, plan->count, plan->items, plan->workgroups,
+                                       static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "plan launch");
+    return Q4RDNA_OK;
+}
+
+void q4rdna_plan_destroy(q4rdna_plan *plan) {
+    if (plan == nullptr) return;
+    if (plan->descs != nullptr) {
+        DeviceGuard guard(plan->device);
+        (void)hipFree(plan->descs);
+    }
+    delete plan;
+}
+
+uint32_t q4rdna_plan_workgroups(const q4rdna_plan *plan) { return plan ? plan->workgroups : 0u; }
+
+int q4rdna_pack(const float *w, uint32_t rows, uint32_t columns, int algorithm, uint8_t *tiles, void *stream) {
+    if (w == nullptr || tiles == nullptr) return fail(Q4RDNA_ERR_ARGUMENT, "NULL input or output");
+    if (!valid_shape(rows, columns)) return fail(Q4RDNA_ERR_ARGUMENT, "shape %ux%u is not 32-row x 64-column tiled", rows, columns);
+    if (algorithm < Q4RDNA_ALGO_SIDECAR || algorithm > Q4RDNA_ALGO_MSE) return fail(Q4RDNA_ERR_ARGUMENT, "unknown algorithm %d", algorithm);
+    if (!aligned(w, 16)) return fail(Q4RDNA_ERR_ARGUMENT, "weights must be 16-byte aligned");
+    hipError_t e = q4rdna::launch_pack(w, rows, columns, algorithm, tiles, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "pack launch");
+    return Q4RDNA_OK;
+}
+
+int q4rdna_dequantize(const q4rdna_weight *w, float *out, void *stream) {
+    int rc = check_weight(w);
+    if (rc != Q4RDNA_OK) return rc;
+    if (out == nullptr || !aligned(out, 4)) return fail(Q4RDNA_ERR_ARGUMENT, "NULL or misaligned output");
+    hipError_t e = q4rdna::launch_dequant(w->tiles, w->rows, w->columns, out, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "dequant launch");
+    return Q4RDNA_OK;
+}
+
+}  // extern "C"

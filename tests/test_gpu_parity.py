@@ -1,0 +1,276 @@
+"""GPU parity of the gfx950 kernels against the CPU oracle, through the C ABI.
+
+Bars: dequant and packing bit-exact; GEMV within the gate
+|y - y64| <= 1e-3 * max(|y64|, 0.01 * rms(y64)) per row against the fp64
+oracle (fp32 accumulation), plus the reference bench's own gate, relative L2
+<= 1e-5 against the sequential fp32 oracle (source/q4rdna_gemv_bench.hip:259).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+import q4rdna
+from q4rdna import api
+from conftest import bf16_to_f32
+
+pytestmark = pytest.mark.gpu
+
+GATE_TOL = 1e-3
+REL_L2_TOL = 1e-5
+ALGOS = [(q4rdna.ALGO_SIDECAR, "sidecar"), (q4rdna.ALGO_ABSMAX, "absmax"), (q4rdna.ALGO_RANGE, "range"),
+         (q4rdna.ALGO_MSE, "mse")]
+
+
+def dev_u8(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint8)).cuda()
+
+
+def dev_f32(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()
+
+
+def random_tiles(rows: int, cols: int, seed: int, subnormal: bool = False) -> np.ndarray:
+    """Uniform random code bytes and random fp16 scales (both signs)."""
+    rng = np.random.default_rng(seed)
+    g = cols // 64
+    t = rng.integers(0, 256, (rows // 32, g, 1088), dtype=np.uint8)
+    mag = rng.uniform(1e-3, 3e-2, (rows // 32, g, 32))
+    if subnormal:
+        mag[..., ::7] = rng.uniform(1e-7, 6e-5, mag[..., ::7].shape)
+    s = (mag * rng.choice([-1.0, 1.0], mag.shape)).astype(np.float16)
+    t[:, :, :64] = s.view(np.uint8).reshape(rows // 32, g, 64)
+    return t.reshape(-1)
+
+
+def check_gemv(y: torch.Tensor, tiles: np.ndarray, rows: int, cols: int, x: np.ndarray, label=""):
+    torch.cuda.synchronize()
+    yh = y.cpu().numpy()
+    y64, a64 = O.gemv_f64(tiles, rows, cols, x)
+    err = O.gemv_errors(yh, y64, a64)
+    assert err["gate"] <= GATE_TOL, (label, err)
+    yseq = O.gemv_seq_f32(tiles, rows, cols, x)
+    assert O.rel_l2(yh, yseq) <= REL_L2_TOL, (label, O.rel_l2(yh, yseq))
+    return err
+
+
+# ----------------------------------------------------------------- dequant
+
+def test_dequant_bit_exact_every_fp16_scale(cuda):
+    from test_oracle import all_scales_tiles
+    tiles, rows, cols = all_scales_tiles()
+    w = api.QWeight.from_tiles(dev_u8(tiles), rows, cols)
+    got = api.dequantize(w).cpu().numpy()
+    want = O.dequant(tiles, rows, cols)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("case", ["edge", "small", "outlier"])
+@pytest.mark.parametrize("name", ["sidecar", "absmax", "range", "mse"])
+def test_dequant_of_reference_packed_tiles(cuda, golden, case, name):
+    tiles = golden[f"{case}_{name}"]
+    rows, cols = golden[f"{case}_bf16"].shape
+    got = api.dequantize(api.QWeight.from_tiles(dev_u8(tiles), rows, cols)).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), O.dequant(tiles, rows, cols).view(np.uint32))
+    # Identical to the CPU experiment's own dequantized values wherever the
+    # stored scale is a normal fp16 number (it halves subnormal scales).
+    ref_cpu = O.dequant(tiles, rows, cols, ref_cpu_decode=True)
+    t = tiles.reshape(rows // 32, cols // 64, 1088)[:, :, :64].copy().view(np.uint16)
+    normal = ((t & 0x7C00) != 0) | ((t & 0x3FF) == 0)                  # [rt, g, lane]
+    mask = np.repeat(normal.transpose(0, 2, 1).reshape(rows, cols // 64), 64, axis=1)
+    assert np.array_equal(got[mask].view(np.uint32), ref_cpu[mask].view(np.uint32))
+
+
+# ----------------------------------------------------------------- packing
+
+@pytest.mark.parametrize("case", ["edge", "small", "outlier"])
+@pytest.mark.parametrize("algo,name", ALGOS)
+def test_gpu_pack_matches_reference_golden(cuda, golden, case, algo, name):
+    w = dev_f32(bf16_to_f32(golden[f"{case}_bf16"]))
+    got = api.pack(w, algo).cpu().numpy()
+    assert np.array_equal(got, golden[f"{case}_{name}"])
+
+
+@pytest.mark.parametrize("algo,name", ALGOS)
+def test_gpu_pack_matches_oracle_fp32_inputs(cuda, algo, name):
+    rows, cols = 256, 2048
+    w = O.gaussian_weights(rows, cols, 77 + algo)
+    w.reshape(-1, 64)[::97] *= 20
+    w.reshape(-1, 64)[5::211] *= 1e-4
+    got = api.pack(dev_f32(w), algo).cpu().numpy()
+    assert np.array_equal(got, O.pack(w, algo))
+
+
+# ----------------------------------------------------------------- GEMV
+
+SHAPES = [(32, 64), (64, 512), (96, 1024), (1024, 4096), (4096, 4096), (12288, 4096), (4096, 12288)]
+
+
+@pytest.mark.parametrize("rows,cols", SHAPES)
+def test_gemv_matches_oracle(cuda, rows, cols):
+    tiles = random_tiles(rows, cols, rows + cols, subnormal=True)
+    x = O.gaussian_x(cols, rows * 7 + cols)
+    w = api.QWeight.from_tiles(dev_u8(tiles), rows, cols)
+    y = api.mul_mat(w, dev_f32(x))
+    assert y is not None
+    check_gemv(y, tiles, rows, cols, x, f"{rows}x{cols}")
+
+
+def test_gemv_packed_gaussian_weights(cuda):
+    rows, cols = 4096, 4096
+    wf = O.gaussian_weights(rows, cols, 0x51EE0000)
+    tiles_dev = api.pack(dev_f32(wf))
+    tiles = tiles_dev.cpu().numpy()
+    # the GPU packer output equals the oracle's on a sample of row tiles
+    sample = O.pack(wf[:128], q4rdna.ALGO_SIDECAR)
+    assert np.array_equal(tiles[: sample.size], sample)
+    x = O.gaussian_x(cols, 0x51EE8000)
+    y = api.mul_mat(api.QWeight.from_tiles(tiles_dev, rows, cols), dev_f32(x))
+    check_gemv(y, tiles, rows, cols, x, "gaussian 4096x4096")
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 12288), (2048, 28672)])
+def test_split_k_sweep_with_outlier_groups(cuda, rows, cols):
+    wf = O.gaussian_weights(rows, cols, rows ^ cols)
+    g = wf.reshape(-1, 64)
+    g[np.random.default_rng(1).permutation(g.shape[0])[: g.shape[0] // 100]] *= 20
+    tiles_dev = api.pack(dev_f32(wf))
+    tiles = tiles_dev.cpu().numpy()
+    w = api.QWeight.from_tiles(tiles_dev, rows, cols)
+    x = O.gaussian_x(cols, 5)
+    xd = dev_f32(x)
+    y64, a64 = O.gemv_f64(tiles, rows, cols, x)
+    yseq = O.gemv_seq_f32(tiles, rows, cols, x)
+    for split in (1, 2, 3, 4, 5, 8, 12, 16, 24, 32):
+        y = torch.empty(rows, dtype=torch.float32, device="cuda")
+        assert api.mul_mat_ex(w, xd, y, split_k=split)
+        torch.cuda.synchronize()
+        yh = y.cpu().numpy()
+        assert O.gemv_errors(yh, y64, a64)["gate"] <= GATE_TOL, split
+        assert O.rel_l2(yh, yseq) <= REL_L2_TOL, split
+
+
+def test_gemv_is_deterministic(cuda):
+    rows, cols = 1024, 4096
+    tiles = random_tiles(rows, cols, 3)
+    w = api.QWeight.from_tiles(dev_u8(tiles), rows, cols)
+    xd = dev_f32(O.gaussian_x(cols, 4))
+    ys = [api.mul_mat(w, xd).cpu().numpy() for _ in range(5)]
+    for y in ys[1:]:
+        assert np.array_equal(y.view(np.uint32), ys[0].view(np.uint32))
+
+
+def test_mul_mat_add(cuda):
+    rows, cols = 4096, 4096
+    tiles = random_tiles(rows, cols, 11)
+    x = O.gaussian_x(cols, 12)
+    add = O.gaussian_x(rows, 13)
+    w = api.QWeight.from_tiles(dev_u8(tiles), rows, cols)
+    y = api.mul_mat_add(w, dev_f32(x), dev_f32(add))
+    torch.cuda.synchronize()
+    y64, a64 = O.gemv_f64(tiles, rows, cols, x)
+    want = y64 + add.astype(np.float64)
+    err = O.gemv_errors(y.cpu().numpy(), want, a64 + np.abs(add))
+    assert err["gate"] <= GATE_TOL, err
+
+
+@pytest.mark.parametrize("rows,cols", [(12288, 4096), (1024, 4096)])
+def test_mul_mat_glu_swiglu(cuda, rows, cols):
+    up_t = random_tiles(rows, cols, 21)
+    gate_t = random_tiles(rows, cols, 22)
+    x = O.gaussian_x(cols, 23)
+    up = api.QWeight.from_tiles(dev_u8(up_t), rows, cols)
+    gate = api.QWeight.from_tiles(dev_u8(gate_t), rows, cols)
+    y = api.mul_mat_glu(up, gate, dev_f32(x))
+    torch.cuda.synchronize()
+    u64, ua = O.gemv_f64(up_t, rows, cols, x)
+    g64, ga = O.gemv_f64(gate_t, rows, cols, x)
+    want = u64 * O.silu(g64)
+    # error bound: |du| * |silu(g)| + |u| * |silu'(g)| * |dg|, silu' <= 1.1
+    bound_abs = ua * np.abs(O.silu(g64)) + np.abs(u64) * 1.1 * ga
+    yh = y.cpu().numpy().astype(np.float64)
+    rms = np.sqrt(np.mean(want ** 2))
+    rel = np.abs(yh - want) / np.maximum(np.abs(want), 0.01 * rms)
+    assert rel.max() <= GATE_TOL, rel.max()
+    assert (np.abs(yh - want) <= 1e-5 * bound_abs + 1e-30).all()
+
+
+def test_not_applicable_leaves_output_untouched(cuda):
+    rows, cols = 64, 512
+    w = api.QWeight.from_tiles(dev_u8(random_tiles(rows, cols, 1)), rows, cols)
+    y = torch.full((rows + 32,), 7.0, device="cuda")
+    assert api.mul_mat(w, dev_f32(np.ones(cols, np.float32)), y) is None
+    x_short = dev_f32(np.ones(cols - 64, np.float32))
+    y2 = torch.full((rows,), 7.0, device="cuda")
+    assert api.mul_mat(w, x_short, y2) is None
+    torch.cuda.synchronize()
+    assert (y.cpu() == 7.0).all() and (y2.cpu() == 7.0).all()
+    assert "shape mismatch" in q4rdna.last_error()
+
+
+# ----------------------------------------------------------------- sidecar
+
+def test_sidecar_open_find_and_gemv(cuda, golden, tmp_path):
+    img = golden["sidecar_image"].tobytes()
+    path = tmp_path / "three.q4rdna"
+    path.write_bytes(img)
+    for sc in (api.Sidecar.open(str(path)), api.Sidecar.from_bytes(img)):
+        ents = sc.entries()
+        assert [e[0] for e in ents] == ["blk.0.attn_q.weight", "blk.0.attn_k.weight", "blk.0.ffn_down.weight"]
+        for name, rows, cols, off, size in ents:
+            w = sc.find(name, cols, rows)
+            assert w is not None
+            assert sc.find(name, rows + 32, cols) is None            # shape check (ne0 = cols)
+            tiles = np.frombuffer(img[off:off + size], np.uint8)
+            x = O.gaussian_x(cols, rows)
+            y = api.mul_mat(w, dev_f32(x))
+            check_gemv(y, tiles, rows, cols, x, name)
+            y2 = api.mul_mat(api.QWeight.from_tiles(dev_u8(tiles), rows, cols), dev_f32(x))
+            torch.cuda.synchronize()
+            assert torch.equal(y, y2)
+        assert sc.find("blk.9.attn_q.weight", 512, 64) is None
+        sc.close()
+
+
+# ----------------------------------------------------------------- multi-tensor plan
+
+def test_plan_matches_oracle(cuda):
+    shapes = [(128, 512, None), (32, 512, None), (32, 512, "add"), (128, 512, None), (384, 512, "glu"),
+              (128, 1536, None), (4096, 4096, None), (1024, 4096, "add")]
+    items, checks = [], []
+    for i, (rows, cols, kind) in enumerate(shapes):
+        t = random_tiles(rows, cols, 100 + i)
+        x = O.gaussian_x(cols, 200 + i)
+        w = api.QWeight.from_tiles(dev_u8(t), rows, cols)
+        y = torch.full((rows,), np.nan, device="cuda")
+        gate = add = None
+        gt = None
+        if kind == "glu":
+            gt = random_tiles(rows, cols, 300 + i)
+            gate = api.QWeight.from_tiles(dev_u8(gt), rows, cols)
+        if kind == "add":
+            add_np = O.gaussian_x(rows, 400 + i)
+            add = dev_f32(add_np)
+        xd = dev_f32(x)
+        items.append((w, xd, y, gate, add))
+        checks.append((t, gt, x, add_np if kind == "add" else None, rows, cols, y))
+    plan = api.Plan(items)
+    assert plan.workgroups >= 1
+    for _ in range(2):
+        assert plan.launch()
+    torch.cuda.synchronize()
+    for t, gt, x, add_np, rows, cols, y in checks:
+        yh = y.cpu().numpy().astype(np.float64)
+        y64, a64 = O.gemv_f64(t, rows, cols, x)
+        if gt is not None:
+            g64, _ = O.gemv_f64(gt, rows, cols, x)
+            want = y64 * O.silu(g64)
+        elif add_np is not None:
+            want = y64 + add_np
+        else:
+            want = y64
+        rms = np.sqrt(np.mean(want ** 2))
+        assert (np.abs(yh - want) / np.maximum(np.abs(want), 0.01 * rms)).max() <= GATE_TOL, (rows, cols)
+    plan.close()
