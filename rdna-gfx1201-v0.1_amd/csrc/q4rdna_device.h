@@ -1,0 +1,60 @@
+// Device helpers shared by the gfx950 kernels (q4rdna_kernels.hip,
+// q4rdna_mfma.hip).
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "q4rdna_internal.h"
+
+namespace q4rdna {
+
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Global-address-space views.  Pointers read from a descriptor table are
+// generic; without the cast their loads become flat loads, which also count
+// against lgkmcnt, so every wait for an LDS read would drain the in-flight
+// weight loads as well.
+typedef __attribute__((address_space(1))) const unsigned int *gptr_u32;
+typedef __attribute__((address_space(1))) const u32x2 *gptr_u32x2;
+typedef __attribute__((address_space(1))) const i32x4 *gptr_i32x4;
+typedef __attribute__((address_space(1))) const float *gptr_cf32;
+typedef __attribute__((address_space(1))) float *gptr_f32;
+typedef __attribute__((address_space(1))) uint8_t *gptr_u8;
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(bits & 0xffffu)));
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+// Device-scope (agent) relaxed atomics: on gfx950 these are single sc1
+// loads/stores and a plain atomic add, coherent across the XCDs' L2s without
+// the whole-L2 write-back/invalidate that release/acquire fences emit.
+__device__ __forceinline__ void store_agent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t add_agent(uint32_t *p, uint32_t v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until this wave's stores have completed (visible at device scope for
+// sc1 stores); the memory clobber keeps the compiler from moving memory
+// operations across it.
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Workgroups are dealt to the 8 XCDs round robin; remap so consecutive
+// logical indices run on one XCD.  A bijection on [0, n).
+__device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t n) {
+    const uint32_t xcd = b & 7u, idx = b >> 3, per = n >> 3, rem = n & 7u;
+    return xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+}
+
+}  // namespace q4rdna

@@ -28,22 +28,40 @@ struct GemvArgs {
     uint32_t *counters;
 };
 
-// Device-side descriptor of one GEMV in a multi-tensor plan.
+// Device-side descriptor of one GEMV in a multi-tensor plan.  Work items are
+// (64-row block, K chunk of up to kChunkGroups groups), numbered from
+// item_begin in block-major order.  The activation is first converted into
+// int8 limbs (kPrepBytes per 64-element group) in `prep`.  With chunks > 1
+// the chunks of a block meet in partial[chunk][rows] (and a second such array
+// for the SwiGLU gate) through counters[block], zero between launches.
 struct PlanDesc {
     const uint8_t *w;
     const uint8_t *gate;
     const float *x;
     const float *add;
     float *y;
+    uint8_t *prep;
+    float *partial;
+    uint32_t *counters;
     uint32_t rows;
     uint32_t cols;
-    uint32_t item_begin;  // first work item (row tile) of this GEMV
+    uint32_t item_begin;
+    uint32_t group_begin;
+    uint32_t chunks;
     uint32_t pad;
 };
 
+constexpr uint32_t kPrepBytes = 272;
+constexpr uint32_t kChunkGroups = 64;
+constexpr uint32_t kBlockRows = 64;
+
 hipError_t launch_gemv(const GemvArgs &args, hipStream_t stream);
-// descs[count] plus a sentinel whose item_begin == total items.
-hipError_t launch_plan(const PlanDesc *descs, uint32_t count, uint32_t items, uint32_t workgroups,
+// descs[count] plus a sentinel whose item_begin / group_begin are the totals.
+// The prep launch converts every activation into limbs; the plan launch then
+// sweeps the items.  sched holds two zeroed counters owned by the plan (left
+// zero after every launch).
+hipError_t launch_prep(const PlanDesc *descs, uint32_t count, uint32_t groups, hipStream_t stream);
+hipError_t launch_plan(const PlanDesc *descs, uint32_t items, bool any_gate, uint32_t workgroups, uint32_t *sched,
                        hipStream_t stream);
 hipError_t launch_dequant(const uint8_t *w, uint32_t rows, uint32_t cols, float *out,
                           hipStream_t stream);
@@ -51,8 +69,8 @@ hipError_t launch_pack(const float *w, uint32_t rows, uint32_t cols, int algorit
                        hipStream_t stream);
 
 // Workgroups of 256 threads the kernels are built for, and the number the
-// plan kernel can keep resident per CU.
+// plan kernel keeps resident per CU (two measured best on MI355X).
 constexpr uint32_t kThreads = 256;
-uint32_t plan_workgroups_per_cu();
+uint32_t plan_workgroups_per_cu(bool any_gate);
 
 }  // namespace q4rdna

@@ -29,18 +29,14 @@
 // four waves' results in LDS in wave order, and K chunks split across
 // workgroups through a partial buffer summed in chunk order by the last
 // workgroup to arrive, so every result is bit-reproducible run to run.
-#include <hip/hip_fp16.h>
-#include <hip/hip_runtime.h>
-#include <stdint.h>
-
-#include "q4rdna_internal.h"
+#include "q4rdna_device.h"
 
 namespace q4rdna {
 namespace {
 
 constexpr int kWaves = 4;
 constexpr int kStageGroups = 64;  // groups of x staged in LDS at once
-constexpr int kBatch = 4;         // tiles in flight per wave per loop trip
+constexpr int kBatch = 2;         // default tiles per wave per loop trip (x2 in flight)
 
 struct XStage {
     float4 v[kStageGroups][16];  // [g][a] even-k x, [g][8 + a] odd-k x / 16
@@ -52,16 +48,14 @@ struct TileRegs {
     uint32_t s01, s23;
 };
 
-__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
-    return __half2float(__ushort_as_half(static_cast<unsigned short>(bits & 0xffffu)));
-}
-
+// Weights are read exactly once per GEMV: nontemporal loads stream them past
+// the caches instead of evicting the activations and partial sums.
 __device__ __forceinline__ TileRegs load_tile(const uint8_t *__restrict__ tile, int q, int a) {
     TileRegs r;
     const uint8_t *codes = tile + 64 + 4 * q + 32 * a;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) r.d[j] = *reinterpret_cast<const uint32_t *>(codes + 256 * j);
-    const uint2 s = *reinterpret_cast<const uint2 *>(tile + 8 * q);
+    for (int j = 0; j < 4; ++j) r.d[j] = __builtin_nontemporal_load((gptr_u32)(codes + 256 * j));
+    const u32x2 s = __builtin_nontemporal_load((gptr_u32x2)(tile + 8 * q));
     r.s01 = s.x;
     r.s23 = s.y;
     return r;
@@ -101,7 +95,7 @@ __device__ __forceinline__ void tile_fma(const TileRegs &r, const float4 xl, con
 __device__ __forceinline__ void stage_x(XStage &st, const float *__restrict__ x, uint32_t g0, int ng) {
     for (int idx = threadIdx.x; idx < ng * 8; idx += kThreads) {
         const int g = idx >> 3, a = idx & 7;
-        const float *b = x + (static_cast<size_t>(g0) + g) * kGroup + 2 * a;
+        const gptr_cf32 b = (gptr_cf32)x + (static_cast<size_t>(g0) + g) * kGroup + 2 * a;
         const float l0 = b[0], h0 = b[1], l1 = b[16], h1 = b[17];
         const float l2 = b[32], h2 = b[33], l3 = b[48], h3 = b[49];
         st.v[g][a] = make_float4(l0, l1, l2, l3);
@@ -110,17 +104,49 @@ __device__ __forceinline__ void stage_x(XStage &st, const float *__restrict__ x,
     }
 }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
-
 struct Shared {
     XStage st;
     float red[2][kWaves][32];
     uint32_t last;
 };
 
+template <bool GATE, int BATCH>
+__device__ __forceinline__ void load_batch(TileRegs (&t)[BATCH], TileRegs (&u)[BATCH],
+                                           const uint8_t *__restrict__ wt, const uint8_t *__restrict__ gt,
+                                           uint32_t s0, int g, int ng, int q, int a) {
+#pragma unroll
+    for (int b = 0; b < BATCH; ++b) {
+        const int gg = g + kWaves * b;
+        if (gg < ng) {
+            t[b] = load_tile(wt + static_cast<size_t>(s0 + gg) * kTileBytes, q, a);
+            if constexpr (GATE) u[b] = load_tile(gt + static_cast<size_t>(s0 + gg) * kTileBytes, q, a);
+        }
+    }
+}
+
+template <bool GATE, int BATCH>
+__device__ __forceinline__ void compute_batch(const TileRegs (&t)[BATCH], const TileRegs (&u)[BATCH],
+                                              const XStage &st, int g, int ng, int a, float (&acc)[4],
+                                              float (&gacc)[4]) {
+#pragma unroll
+    for (int b = 0; b < BATCH; ++b) {
+        const int gg = g + kWaves * b;
+        if (gg < ng) {
+            const float4 xl = st.v[gg][a];
+            const float4 xh = st.v[gg][8 + a];
+            const float c = st.c[gg][a];
+            tile_fma(t[b], xl, xh, c, acc);
+            if constexpr (GATE) tile_fma(u[b], xl, xh, c, gacc);
+        }
+    }
+}
+
 // Partial dot products of row tile `rt` over groups [g_begin, g_end), summed
 // over the workgroup.  Threads 0..31 return the row partials (out, gout).
-template <bool GATE>
+// Wave w takes groups g_begin + w, + 4, ...; each wave keeps the next batch
+// of tiles in flight while it converts the current one, and the first batch
+// is issued before the activations are staged.
+template <bool GATE, int BATCH = kBatch>
 __device__ __forceinline__ void tile_row_partial(Shared &sh, const uint8_t *__restrict__ w,
                                                  const uint8_t *__restrict__ gw,
                                                  const float *__restrict__ x, uint32_t cols,
@@ -137,30 +163,20 @@ __device__ __forceinline__ void tile_row_partial(Shared &sh, const uint8_t *__re
 
     for (uint32_t s0 = g_begin; s0 < g_end; s0 += kStageGroups) {
         const int ng = static_cast<int>(min(static_cast<uint32_t>(kStageGroups), g_end - s0));
+        TileRegs cur[BATCH], gcur[BATCH];
+        load_batch<GATE, BATCH>(cur, gcur, wt, gt, s0, wave, ng, q, a);
         __syncthreads();
         stage_x(sh.st, x, s0, ng);
         __syncthreads();
-        for (int g = wave; g < ng; g += kWaves * kBatch) {
-            TileRegs t[kBatch];
-            TileRegs u[GATE ? kBatch : 1];
+        for (int g = wave; g < ng; g += kWaves * BATCH) {
+            TileRegs nxt[BATCH], gnxt[BATCH];
+            const int gn = g + kWaves * BATCH;
+            if (gn < ng) load_batch<GATE, BATCH>(nxt, gnxt, wt, gt, s0, gn, ng, q, a);
+            compute_batch<GATE, BATCH>(cur, gcur, sh.st, g, ng, a, acc, gacc);
 #pragma unroll
-            for (int b = 0; b < kBatch; ++b) {
-                const int gg = g + kWaves * b;
-                if (gg < ng) {
-                    t[b] = load_tile(wt + static_cast<size_t>(s0 + gg) * kTileBytes, q, a);
-                    if constexpr (GATE) u[b] = load_tile(gt + static_cast<size_t>(s0 + gg) * kTileBytes, q, a);
-                }
-            }
-#pragma unroll
-            for (int b = 0; b < kBatch; ++b) {
-                const int gg = g + kWaves * b;
-                if (gg < ng) {
-                    const float4 xl = sh.st.v[gg][a];
-                    const float4 xh = sh.st.v[gg][8 + a];
-                    const float c = sh.st.c[gg][a];
-                    tile_fma(t[b], xl, xh, c, acc);
-                    if constexpr (GATE) tile_fma(u[b], xl, xh, c, gacc);
-                }
+            for (int b = 0; b < BATCH; ++b) {
+                cur[b] = nxt[b];
+                if constexpr (GATE) gcur[b] = gnxt[b];
             }
         }
     }
@@ -206,14 +222,8 @@ __device__ __forceinline__ float epilogue(float v, float gv, const float *__rest
     return v;
 }
 
-// Workgroup b covers row tile rt and K chunk s of `split`.  Blocks are
-// remapped so the chunks of one row tile run on one XCD (the hardware deals
-// workgroups to the 8 XCDs round robin).
-__device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t n) {
-    const uint32_t xcd = b & 7u, idx = b >> 3, per = n >> 3, rem = n & 7u;
-    return xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
-}
-
+// Workgroup b covers row tile rt and K chunk s of `split`, remapped so the
+// chunks of one row tile run on one XCD.
 template <bool GATE, bool ADD>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args) {
     __shared__ Shared sh;
@@ -230,60 +240,28 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args) {
         if (threadIdx.x < 32) args.y[row] = epilogue<GATE, ADD>(v, gv, args.add, row);
         return;
     }
-    // Split K: publish this chunk, then the last workgroup of the row tile
-    // sums the chunks in chunk order.
+    // Split K: publish this chunk's partials with device-scope stores, wait
+    // for them to complete, then count arrivals; the last workgroup of the
+    // row tile sums the chunks in chunk order and resets the counter.
     if (threadIdx.x < 32) {
-        args.partial[static_cast<size_t>(s) * args.rows + row] = v;
-        if constexpr (GATE) args.partial[static_cast<size_t>(split + s) * args.rows + row] = gv;
+        store_agent(&args.partial[static_cast<size_t>(s) * args.rows + row], v);
+        if constexpr (GATE) store_agent(&args.partial[static_cast<size_t>(split + s) * args.rows + row], gv);
     }
-    __threadfence();
+    wait_stores();
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = atomicAdd(&args.counters[rt], 1u);
-        sh.last = (prev == split - 1) ? 1u : 0u;
-    }
+    if (threadIdx.x == 0) sh.last = (add_agent(&args.counters[rt], 1u) == split - 1) ? 1u : 0u;
     __syncthreads();
     if (sh.last == 0u) return;
-    __threadfence();
     if (threadIdx.x < 32) {
-        float sum = 0.f, gsum = 0.f;
-        for (uint32_t c = 0; c < split; ++c) {
-            sum = (c == 0) ? args.partial[row] : sum + args.partial[static_cast<size_t>(c) * args.rows + row];
-            if constexpr (GATE) {
-                const float p = args.partial[static_cast<size_t>(split + c) * args.rows + row];
-                gsum = (c == 0) ? p : gsum + p;
-            }
+        float sum = load_agent(&args.partial[row]);
+        float gsum = GATE ? load_agent(&args.partial[static_cast<size_t>(split) * args.rows + row]) : 0.f;
+        for (uint32_t c = 1; c < split; ++c) {
+            sum += load_agent(&args.partial[static_cast<size_t>(c) * args.rows + row]);
+            if constexpr (GATE) gsum += load_agent(&args.partial[static_cast<size_t>(split + c) * args.rows + row]);
         }
         args.y[row] = epilogue<GATE, ADD>(sum, gsum, args.add, row);
     }
-    if (threadIdx.x == 0) args.counters[rt] = 0u;
-}
-
-// Multi-tensor plan: a persistent grid sweeps work items (one row tile of one
-// GEMV, full K) in order; workgroup b takes items b, b + grid, ...
-__global__ __launch_bounds__(kThreads) void plan_kernel(const PlanDesc *__restrict__ descs,
-                                                        uint32_t count, uint32_t items) {
-    __shared__ Shared sh;
-    uint32_t d = 0;
-    for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
-        while (item >= descs[d + 1].item_begin) ++d;
-        const PlanDesc &desc = descs[d];
-        const uint32_t rt = item - desc.item_begin;
-        const uint32_t groups = desc.cols / kGroup;
-        const uint32_t row = rt * kTileRows + (threadIdx.x & 31);
-        float v = 0.f, gv = 0.f;
-        if (desc.gate != nullptr) {
-            tile_row_partial<true>(sh, desc.w, desc.gate, desc.x, desc.cols, rt, 0, groups, v, gv);
-            if (threadIdx.x < 32) {
-                if (desc.add != nullptr) v += desc.add[row];
-                desc.y[row] = v * silu(gv);
-            }
-        } else {
-            tile_row_partial<false>(sh, desc.w, nullptr, desc.x, desc.cols, rt, 0, groups, v, gv);
-            if (threadIdx.x < 32) desc.y[row] = desc.add != nullptr ? v + desc.add[row] : v;
-        }
-    }
-    (void)count;
+    if (threadIdx.x == 0) store_agent(&args.counters[rt], 0u);
 }
 
 // out[row][k] = fp32(scale) * code, one thread per code byte.
@@ -572,12 +550,6 @@ hipError_t launch_gemv(const GemvArgs &args, hipStream_t stream) {
                                : launch_gemv_t<false, false>(args, stream);
 }
 
-hipError_t launch_plan(const PlanDesc *descs, uint32_t count, uint32_t items, uint32_t workgroups,
-                       hipStream_t stream) {
-    hipLaunchKernelGGL(plan_kernel, dim3(workgroups), dim3(kThreads), 0, stream, descs, count, items);
-    return hipGetLastError();
-}
-
 hipError_t launch_dequant(const uint8_t *w, uint32_t rows, uint32_t cols, float *out, hipStream_t stream) {
     const uint64_t work = static_cast<uint64_t>(rows) * cols / 2;
     hipLaunchKernelGGL(dequant_kernel, dim3(grid_for(work, kThreads)), dim3(kThreads), 0, stream, w, rows,
@@ -592,7 +564,5 @@ hipError_t launch_pack(const float *w, uint32_t rows, uint32_t cols, int algorit
                        algorithm, tiles);
     return hipGetLastError();
 }
-
-uint32_t plan_workgroups_per_cu() { return 4; }
 
 }  // namespace q4rdna

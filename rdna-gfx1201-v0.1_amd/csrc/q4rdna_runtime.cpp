@@ -208,13 +208,14 @@ bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 constexpr uint32_t kMaxSplit = 64;
 
 uint32_t policy_split(uint32_t rows, uint32_t cols, int device) {
-    // Fill the chip with ~4 workgroups (16 waves) per CU, keeping at least
-    // two groups per wave in every K chunk.
+    // About two workgroups per CU, keeping at least 16 groups (four per wave)
+    // in every K chunk.  Measured on MI355X: 4096x4096 -> 4, 1024x4096 -> 4,
+    // 12288x4096 -> 2, 4096x12288 -> 4..8, 2048x28672 -> 8.
     const uint32_t tiles = rows / kTileRows;
     const uint32_t groups = cols / kGroup;
-    const uint32_t target = cu_count(device) * 4;
+    const uint32_t target = cu_count(device) * 2;
     uint32_t split = (target + tiles - 1) / tiles;
-    const uint32_t max_by_groups = std::max<uint32_t>(1, groups / 8);
+    const uint32_t max_by_groups = std::max<uint32_t>(1, groups / 16);
     split = std::min(split, max_by_groups);
     split = std::min(split, kMaxSplit);
     return std::max<uint32_t>(split, 1);
@@ -278,11 +279,16 @@ struct q4rdna_sidecar {
 
 struct q4rdna_plan {
     int device = 0;
-    q4rdna::PlanDesc *descs = nullptr;
+    q4rdna::PlanDesc *descs = nullptr;  // count + 1 (sentinel)
+    uint8_t *scratch = nullptr;         // activation limbs, split-K partials and counters
+    uint32_t *sched = nullptr;          // [next item, finished workgroups], zero between launches
     uint32_t count = 0;
     uint32_t items = 0;
+    uint32_t groups = 0;
     uint32_t workgroups = 0;
+    bool any_gate = false;
 };
+
 
 namespace {
 
@@ -533,16 +539,26 @@ int q4rdna_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const f
 int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device, q4rdna_plan **out) {
     if (out == nullptr || (descs == nullptr && count > 0)) return fail(Q4RDNA_ERR_ARGUMENT, "NULL descriptors or handle");
     *out = nullptr;
+    using q4rdna::kBlockRows;
+    using q4rdna::kChunkGroups;
+    using q4rdna::kPrepBytes;
     std::vector<q4rdna::PlanDesc> host(static_cast<size_t>(count) + 1);
-    uint64_t items = 0;
+    // Scratch layout: activation limbs (kPrepBytes per group), then per split
+    // GEMV its partials and per-block counters.
+    uint64_t items = 0, groups = 0, scratch = 0;
+    std::vector<uint64_t> prep_off(count), part_off(count), cnt_off(count);
     for (uint32_t i = 0; i < count; ++i) {
         const q4rdna_gemv_desc &d = descs[i];
         if (d.weight.tiles == nullptr || d.x == nullptr || d.y == nullptr)
             return fail(Q4RDNA_ERR_ARGUMENT, "descriptor %u has a NULL pointer", i);
         if (!valid_shape(d.weight.rows, d.weight.columns) || !aligned(d.weight.tiles, 16) ||
-            (d.gate_tiles != nullptr && !aligned(d.gate_tiles, 16)))
+            (d.gate_tiles != nullptr && !aligned(d.gate_tiles, 16)) || !aligned(d.x, 4) || !aligned(d.y, 4) ||
+            (d.add != nullptr && !aligned(d.add, 4)))
             return fail(Q4RDNA_ERR_ARGUMENT, "descriptor %u: invalid shape or alignment", i);
         if (d.weight.device != device) return fail(Q4RDNA_ERR_ARGUMENT, "descriptor %u lives on device %d", i, d.weight.device);
+        const uint32_t g = d.weight.columns / kGroup;
+        const uint32_t chunks = (g + kChunkGroups - 1) / kChunkGroups;
+        const uint32_t blocks = (d.weight.rows + kBlockRows - 1) / kBlockRows;
         q4rdna::PlanDesc &p = host[i];
         p.w = d.weight.tiles;
         p.gate = d.gate_tiles;
@@ -552,24 +568,64 @@ int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device
         p.rows = d.weight.rows;
         p.cols = d.weight.columns;
         p.item_begin = static_cast<uint32_t>(items);
-        items += d.weight.rows / kTileRows;
-        if (items > 0xffffffffull) return fail(Q4RDNA_ERR_ARGUMENT, "plan too large");
+        p.group_begin = static_cast<uint32_t>(groups);
+        p.chunks = chunks;
+        prep_off[i] = scratch;
+        scratch += static_cast<uint64_t>(g) * kPrepBytes;
+        if (chunks > 1) {
+            part_off[i] = scratch;
+            scratch += static_cast<uint64_t>(chunks) * d.weight.rows * (d.gate_tiles ? 2 : 1) * sizeof(float);
+            scratch = (scratch + 255) & ~uint64_t(255);
+            cnt_off[i] = scratch;
+            scratch += static_cast<uint64_t>(blocks) * sizeof(uint32_t);
+        }
+        scratch = (scratch + 255) & ~uint64_t(255);
+        items += static_cast<uint64_t>(blocks) * chunks;
+        groups += g;
+        if (items > 0xffffffffull || groups > 0xffffffffull) return fail(Q4RDNA_ERR_ARGUMENT, "plan too large");
     }
     host[count] = q4rdna::PlanDesc{};
     host[count].item_begin = static_cast<uint32_t>(items);
+    host[count].group_begin = static_cast<uint32_t>(groups);
     DeviceGuard guard(device);
     if (!guard.ok()) return fail(Q4RDNA_ERR_HIP, "hipSetDevice(%d) failed", device);
     auto plan = std::make_unique<q4rdna_plan>();
     plan->device = device;
     plan->count = count;
     plan->items = static_cast<uint32_t>(items);
-    const uint32_t resident = cu_count(device) * q4rdna::plan_workgroups_per_cu();
-    plan->workgroups = std::max<uint32_t>(1, std::min<uint32_t>(resident, plan->items));
+    plan->groups = static_cast<uint32_t>(groups);
+    for (uint32_t i = 0; i < count; ++i) plan->any_gate |= descs[i].gate_tiles != nullptr;
+    uint32_t per_cu = q4rdna::plan_workgroups_per_cu(plan->any_gate);
+    if (const char *env = std::getenv("Q4RDNA_PLAN_WG_PER_CU")) {  // tuning sweeps only
+        const int v = std::atoi(env);
+        if (v >= 1 && v <= 16) per_cu = static_cast<uint32_t>(v);
+    }
+    plan->workgroups = std::max<uint32_t>(1, std::min<uint32_t>(cu_count(device) * per_cu, plan->items));
+    auto cleanup = [&plan]() {
+        if (plan->descs) (void)hipFree(plan->descs);
+        if (plan->scratch) (void)hipFree(plan->scratch);
+        if (plan->sched) (void)hipFree(plan->sched);
+    };
     hipError_t e = hipMalloc(&plan->descs, host.size() * sizeof(q4rdna::PlanDesc));
-    if (e != hipSuccess) return fail(Q4RDNA_ERR_MEMORY, "plan table: %s", hipGetErrorString(e));
-    e = hipMemcpy(plan->descs, host.data(), host.size() * sizeof(q4rdna::PlanDesc), hipMemcpyHostToDevice);
+    if (e == hipSuccess && scratch > 0) e = hipMalloc(&plan->scratch, scratch);
+    if (e == hipSuccess) e = hipMalloc(&plan->sched, 2 * sizeof(uint32_t));
     if (e != hipSuccess) {
-        (void)hipFree(plan->descs);
+        cleanup();
+        return fail(Q4RDNA_ERR_MEMORY, "plan buffers: %s", hipGetErrorString(e));
+    }
+    for (uint32_t i = 0; i < count; ++i) {
+        host[i].prep = plan->scratch + prep_off[i];
+        if (host[i].chunks > 1) {
+            host[i].partial = reinterpret_cast<float *>(plan->scratch + part_off[i]);
+            host[i].counters = reinterpret_cast<uint32_t *>(plan->scratch + cnt_off[i]);
+        }
+    }
+    e = hipMemcpy(plan->descs, host.data(), host.size() * sizeof(q4rdna::PlanDesc), hipMemcpyHostToDevice);
+    if (e == hipSuccess && scratch > 0) e = hipMemset(plan->scratch, 0, scratch);
+    if (e == hipSuccess) e = hipMemset(plan->sched, 0, 2 * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        cleanup();
         return hip_fail(e, "plan upload");
     }
     *out = plan.release();
@@ -581,18 +637,20 @@ int q4rdna_plan_launch(q4rdna_plan *plan, void *stream) {
     if (current_device() != plan->device)
         return fail(Q4RDNA_NOT_APPLICABLE, "plan lives on device %d, current device is %d", plan->device, current_device());
     if (plan->items == 0) return Q4RDNA_OK;
-    hipError_t e = q4rdna::launch_plan(plan->descs, plan->count, plan->items, plan->workgroups,
-                                       static_cast<hipStream_t>(stream));
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = q4rdna::launch_prep(plan->descs, plan->count, plan->groups, s);
+    if (e != hipSuccess) return hip_fail(e, "plan activation launch");
+    e = q4rdna::launch_plan(plan->descs, plan->items, plan->any_gate, plan->workgroups, plan->sched, s);
     if (e != hipSuccess) return hip_fail(e, "plan launch");
     return Q4RDNA_OK;
 }
 
 void q4rdna_plan_destroy(q4rdna_plan *plan) {
     if (plan == nullptr) return;
-    if (plan->descs != nullptr) {
-        DeviceGuard guard(plan->device);
-        (void)hipFree(plan->descs);
-    }
+    DeviceGuard guard(plan->device);
+    if (plan->descs != nullptr) (void)hipFree(plan->descs);
+    if (plan->scratch != nullptr) (void)hipFree(plan->scratch);
+    if (plan->sched != nullptr) (void)hipFree(plan->sched);
     delete plan;
 }
 
