@@ -2,18 +2,27 @@
 """Q4_RDNA group-64 GEMV benchmark on one MI355X (gfx950).
 
 Workload: one decode step's weight streaming for the Qwen3-8B 36-layer stack,
-252 distinct packed tensors (q 4096x4096, k/v 1024x4096, o 4096x4096,
-gate/up 12288x4096, down 4096x12288 per layer, 3,689,938,944 packed bytes),
-swept in layer order at batch 1 with a fresh N(0,1) activation per tensor.
-Weights are N(0, 0.02) fp32 generated on the GPU and packed by the GPU packer
-(bit-identical to the reference's native packer); everything is resident in
-HBM before timing.
+252 distinct packed tensors (per layer q 4096x4096, k/v 1024x4096,
+o 4096x4096, gate/up 12288x4096, down 4096x12288; 3,689,938,944 packed
+bytes), swept in layer order at batch 1 with a fresh N(0,1) activation per
+tensor.  Weights are N(0, 0.02) fp32 generated on the GPU and packed by the
+GPU packer (bit-identical to the reference's native packer); everything is
+resident in HBM before timing.
 
-A step is one sweep of the stack by the multi-tensor plan kernel (one
-launch).  Printed: one JSON line with the step throughput over algorithmic
-bytes (17*M*K/32 + 4*K + 4*M per tensor), the per-launch roofline figures
-measured with HIP events on the launch stream, and the CPU oracle's
-sequential GEMV timed on a bounded sample of the same stack.
+A step is one sweep of the stack by a multi-tensor plan: the activation
+prepare launch plus the GEMV sweep launch.  Printed: one JSON line with
+
+  value       algorithmic bytes of the stack (17*M*K/32 + 4*K + 4*M per
+              tensor) / step time, over K timed steps between synchronizations
+  roofline    the sweep kernel alone: bytes / its mean duration from HIP events
+              on its launch stream; traffic = HBM bytes per sweep from the
+              committed PMC summary (profiles/plan_sweep_stack_traffic.json)
+  cpu_baseline  the oracle's sequential CPU GEMV (the reference bench's loop)
+              timed on host cores over a bounded sample of the same stack
+
+plus the same stack run the reference's way -- one GEMV launch per tensor --
+replayed from a HIP graph, and a full-size parity check of five tensors
+against the fp64 oracle.
 """
 from __future__ import annotations
 
@@ -29,6 +38,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "Q4g64 GEMV HBM GB/s (% of 8 TB/s peak) + µs per Qwen3-8B 252-tensor stack"
 PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "plan_sweep_stack_traffic.json")
 
 
 def algorithmic_bytes(rows: int, cols: int, n: int = 1) -> int:
@@ -40,7 +50,7 @@ def log(msg: str) -> None:
 
 
 def build_stack(layers: int, seed: int):
-    """Generate and pack the stack on the GPU; returns tensors and buffers."""
+    """Generate and pack the stack on the GPU; returns tensors and the buffer."""
     import torch
     from q4rdna import api
     from q4rdna.sidecar import layout, qwen3_8b_stack
@@ -68,49 +78,70 @@ def build_stack(layers: int, seed: int):
 
 
 def time_plan(plan, steps: int, warmup: int):
-    """Per-launch durations (ms) from HIP events on the launch stream."""
+    """Run warmup + timed steps; returns (wall ms per step, sweep ms list,
+    prepare ms list).  Events sit on the stream both launches use."""
     import torch
     stream = torch.cuda.current_stream()
+    s = stream.cuda_stream
     for _ in range(warmup):
-        plan.launch(stream.cuda_stream)
+        plan.launch(s)
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     t0 = time.perf_counter()
     for i in range(steps):
-        starts[i].record(stream)
-        plan.launch(stream.cuda_stream)
-        ends[i].record(stream)
+        ev[i][0].record(stream)
+        plan.prepare(s)
+        ev[i][1].record(stream)
+        plan.sweep(s)
+        ev[i][2].record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    return per, wall
+    wall_ms = (time.perf_counter() - t0) * 1000.0 / steps
+    prep = [e[0].elapsed_time(e[1]) for e in ev]
+    sweep = [e[1].elapsed_time(e[2]) for e in ev]
+    return wall_ms, sweep, prep
 
 
-def time_per_tensor(tensors, steps: int, warmup: int):
-    """One launch per tensor (the reference's dispatch pattern), stack time."""
+def time_per_tensor_graph(tensors, steps: int, warmup: int):
+    """The reference's dispatch pattern: one GEMV launch per tensor
+    (q4rdna_mul_mat with the shape policy), captured once into a HIP graph and
+    replayed.  Returns (us per stack, whether every replay equals the eager
+    outputs bit for bit; outputs are poisoned with NaN before each check)."""
     import torch
     from q4rdna import api
-    stream = torch.cuda.current_stream()
-    def sweep():
-        for t in tensors:
-            api.mul_mat(t["w"], t["x"], t["y"], stream=stream.cuda_stream)
-    for _ in range(warmup):
-        sweep()
+    s = torch.cuda.Stream()
+    ys_graph = [torch.empty_like(t["y"]) for t in tensors]
+
+    def sweep(outs):
+        for t, y in zip(tensors, outs):
+            api.mul_mat(t["w"], t["x"], y, stream=s.cuda_stream)
+
+    with torch.cuda.stream(s):
+        sweep(ys_graph)  # allocates the split-K workspace of this stream
     torch.cuda.synchronize()
-    a = torch.cuda.Event(enable_timing=True)
-    b = torch.cuda.Event(enable_timing=True)
-    a.record(stream)
-    for _ in range(steps):
-        sweep()
-    b.record(stream)
+    eager = [y.clone() for y in ys_graph]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        sweep(ys_graph)
+    same = True
+    with torch.cuda.stream(s):
+        for _ in range(max(warmup, 2)):
+            for y in ys_graph:
+                y.fill_(float("nan"))
+            g.replay()
+            s.synchronize()
+            same = same and all(torch.equal(y, e) for y, e in zip(ys_graph, eager))
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(s)
+        for _ in range(steps):
+            g.replay()
+        b.record(s)
     torch.cuda.synchronize()
-    return a.elapsed_time(b) / steps
+    return a.elapsed_time(b) * 1000.0 / steps, same
 
 
 def check_parity(tensors, picks):
-    """Stack outputs vs the fp64 oracle for a few tensors (full size)."""
-    import numpy as np
+    """Outputs of the last launch vs the fp64 oracle (full-size tensors)."""
     import oracle as O
     worst = 0.0
     for i in picks:
@@ -118,15 +149,14 @@ def check_parity(tensors, picks):
         tiles = t["w"].tiles.cpu().numpy()
         x = t["x"].cpu().numpy()
         y64, a64 = O.gemv_f64(tiles, t["rows"], t["cols"], x)
-        err = O.gemv_errors(t["y"].cpu().numpy(), y64, a64)
-        worst = max(worst, err["gate"])
+        worst = max(worst, O.gemv_errors(t["y"].cpu().numpy(), y64, a64)["gate"])
     return worst
 
 
 def cpu_baseline(tensors, budget_s: float):
     """The oracle's sequential fp32 GEMV (the reference bench's CPU loop,
-    source/q4rdna_gemv_bench.hip:189-211) on host cores, one thread, over the
-    stack's tensors in order until about budget_s of CPU work."""
+    source/q4rdna_gemv_bench.hip:189-211) on one host core, over the stack's
+    tensors in order until about budget_s of CPU work."""
     import oracle as O
     done_bytes, elapsed, n = 0, 0.0, 0
     for t in tensors:
@@ -139,27 +169,42 @@ def cpu_baseline(tensors, budget_s: float):
         n += 1
         if elapsed >= budget_s:
             break
+    stack = sum(algorithmic_bytes(t["rows"], t["cols"]) for t in tensors)
     return dict(value=round(done_bytes / elapsed / 1e9, 4), unit="GB/s", cores=1, kind="port",
-                sample=f"first {n} of {len(tensors)} stack tensors in layer order, {done_bytes} algorithmic bytes, "
-                       f"{elapsed:.2f}s single-thread (oracle/q4oracle.c, gcc -O2, x86-64 baseline)",
-                us_per_stack_extrapolated=round(elapsed / done_bytes * sum(
-                    algorithmic_bytes(t["rows"], t["cols"]) for t in tensors) * 1e6, 1))
+                sample=f"first {n} of {len(tensors)} stack tensors in layer order ({done_bytes} algorithmic bytes), "
+                       f"{elapsed:.2f} s on one core: oracle/q4oracle.c gcc -O2 x86-64 baseline",
+                us_per_stack=round(elapsed / done_bytes * stack * 1e6, 1))
+
+
+def load_traffic():
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
+def mean(v):
+    return sum(v) / len(v)
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--seed", type=int, default=0x51EE0000)
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-per-tensor", action="store_true")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="for rocprofv3 --pmc: five plan launches over the stack, then three plain 1 GiB "
+                         "device copies (the FETCH_SIZE calibration); prints no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (this path does not shard)",
-              file=sys.stderr)
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
+              "(this GEMV path runs on a single GPU; sharding is described in DESIGN.md)", file=sys.stderr)
         return 2
 
     import torch
@@ -169,22 +214,34 @@ def main() -> int:
     stack_bytes = sum(algorithmic_bytes(t["rows"], t["cols"]) for t in tensors)
     plan = api.Plan([(t["w"], t["x"], t["y"]) for t in tensors])
     log(f"[bench] plan: {len(tensors)} GEMVs, {plan.workgroups} workgroups")
+    if args.pmc_probe:
+        for _ in range(5):
+            plan.launch()
+        torch.cuda.synchronize()
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("[bench] pmc probe done")
+        return 0
 
-    torch.cuda.synchronize()
-    per_launch, wall = time_plan(plan, args.steps, args.warmup)
-    ms_per_step = wall * 1000.0 / args.steps
-    avg_launch_ms = sum(per_launch) / len(per_launch)
-    log(f"[bench] plan: {avg_launch_ms * 1000:.1f} us per launch (events), {ms_per_step * 1000:.1f} us per step (wall)")
+    ms_per_step, sweep_ms, prep_ms = time_plan(plan, args.steps, args.warmup)
+    sweep_us, prep_us = mean(sweep_ms) * 1000.0, mean(prep_ms) * 1000.0
+    log(f"[bench] step {ms_per_step * 1000:.1f} us (prepare {prep_us:.1f} us + sweep {sweep_us:.1f} us by events)")
     parity = check_parity(tensors, [0, 1, 4, 6, len(tensors) - 1])
-    log(f"[bench] parity vs fp64 oracle on 5 tensors: gate {parity:.2e}")
+    log(f"[bench] parity vs fp64 oracle on 5 full-size tensors: gate {parity:.2e}")
 
-    per_tensor_us = None
+    per_tensor = None
     if not args.no_per_tensor:
-        per_tensor_us = time_per_tensor(tensors, max(3, args.steps // 10), 2) * 1000.0
-        log(f"[bench] per-tensor launches: {per_tensor_us:.1f} us per stack")
+        us, same = time_per_tensor_graph(tensors, max(5, args.steps // 5), 3)
+        per_tensor = dict(us_per_stack=round(us, 2), gb_per_s=round(stack_bytes / us / 1e3, 1),
+                          graph_replays_equal_eager=same)
+        log(f"[bench] one launch per tensor (graph replay): {us:.1f} us per stack, replays equal eager: {same}")
 
     value = stack_bytes / (ms_per_step / 1000.0) / 1e9
-    achieved = stack_bytes / (avg_launch_ms / 1000.0) / 1e9
+    achieved = stack_bytes / (sweep_us / 1e6) / 1e9
+    traffic = load_traffic()
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -198,15 +255,18 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": f"qwen3-8b {args.layers}-layer stack, {len(tensors)} Q4_RDNA group-64 tensors, "
-                               "batch 1, fresh x per tensor, one multi-tensor launch per step",
+        "config": {"workload": f"qwen3-8b {args.layers}-layer stack: {len(tensors)} Q4_RDNA group-64 GEMVs at batch 1, "
+                               "layer order, fresh x per tensor, one multi-tensor plan per step",
                    "tensors": len(tensors), "algorithmic_bytes_per_step": stack_bytes, "batch": 1},
-        "us_per_stack": round(avg_launch_ms * 1000.0, 2),
-        "pct_of_peak": round(100.0 * achieved / PEAK_GBS, 2),
-        "per_tensor_launches_us_per_stack": None if per_tensor_us is None else round(per_tensor_us, 2),
+        "us_per_stack": round(ms_per_step * 1000.0, 2),
+        "pct_of_peak": round(100.0 * value / PEAK_GBS, 2),
+        "prepare_us": round(prep_us, 2),
+        "sweep_us": round(sweep_us, 2),
+        "per_tensor_launches": per_tensor,
         "parity_gate_max": parity,
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_GBS, 4), "traffic": None},
+        "roofline": {"bound": "hbm", "kernel": "plan sweep", "achieved": round(achieved, 2), "peak": PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
+                     "traffic": None if traffic is None else traffic.get("bytes_per_sweep")},
         "cpu_baseline": None,
     }
     if not args.no_cpu:

@@ -165,8 +165,14 @@ typedef struct q4rdna_plan q4rdna_plan;
 /* Build a plan for `count` descriptors (uploads the descriptor table once). */
 int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device,
                        q4rdna_plan **out);
-/* Launch the whole plan on `stream`; allocates nothing. */
+/* Launch the whole plan on `stream` (prepare + sweep); allocates nothing. */
 int q4rdna_plan_launch(q4rdna_plan *plan, void *stream);
+/* The two launches of q4rdna_plan_launch, for callers that time or overlap
+ * them: prepare converts every activation x into the plan's int8 digit
+ * buffers; sweep runs the GEMVs and must follow a prepare of the same x on
+ * the same stream. */
+int q4rdna_plan_prepare(q4rdna_plan *plan, void *stream);
+int q4rdna_plan_sweep(q4rdna_plan *plan, void *stream);
 void q4rdna_plan_destroy(q4rdna_plan *plan);
 /* Workgroups the plan launches (persistent grid). */
 uint32_t q4rdna_plan_workgroups(const q4rdna_plan *plan);

@@ -632,17 +632,39 @@ int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device
     return Q4RDNA_OK;
 }
 
-int q4rdna_plan_launch(q4rdna_plan *plan, void *stream) {
+namespace {
+
+int plan_check(const q4rdna_plan *plan) {
     if (plan == nullptr) return fail(Q4RDNA_ERR_ARGUMENT, "NULL plan");
     if (current_device() != plan->device)
         return fail(Q4RDNA_NOT_APPLICABLE, "plan lives on device %d, current device is %d", plan->device, current_device());
-    if (plan->items == 0) return Q4RDNA_OK;
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    hipError_t e = q4rdna::launch_prep(plan->descs, plan->count, plan->groups, s);
-    if (e != hipSuccess) return hip_fail(e, "plan activation launch");
-    e = q4rdna::launch_plan(plan->descs, plan->items, plan->any_gate, plan->workgroups, plan->sched, s);
-    if (e != hipSuccess) return hip_fail(e, "plan launch");
     return Q4RDNA_OK;
+}
+
+}  // namespace
+
+int q4rdna_plan_prepare(q4rdna_plan *plan, void *stream) {
+    int rc = plan_check(plan);
+    if (rc != Q4RDNA_OK) return rc;
+    hipError_t e = q4rdna::launch_prep(plan->descs, plan->count, plan->groups, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "plan prepare launch");
+    return Q4RDNA_OK;
+}
+
+int q4rdna_plan_sweep(q4rdna_plan *plan, void *stream) {
+    int rc = plan_check(plan);
+    if (rc != Q4RDNA_OK) return rc;
+    if (plan->items == 0) return Q4RDNA_OK;
+    hipError_t e = q4rdna::launch_plan(plan->descs, plan->items, plan->any_gate, plan->workgroups, plan->sched,
+                                       static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "plan sweep launch");
+    return Q4RDNA_OK;
+}
+
+int q4rdna_plan_launch(q4rdna_plan *plan, void *stream) {
+    int rc = q4rdna_plan_prepare(plan, stream);
+    if (rc != Q4RDNA_OK) return rc;
+    return q4rdna_plan_sweep(plan, stream);
 }
 
 void q4rdna_plan_destroy(q4rdna_plan *plan) {

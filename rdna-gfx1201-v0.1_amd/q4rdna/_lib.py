@@ -37,7 +37,8 @@ EXPORTS = (
     "q4rdna_sidecar_open_memory", "q4rdna_sidecar_close", "q4rdna_sidecar_count", "q4rdna_sidecar_entry",
     "q4rdna_find", "q4rdna_weight_from_device", "q4rdna_default_sidecar", "q4rdna_scope_allows",
     "q4rdna_mul_mat", "q4rdna_mul_mat_add", "q4rdna_mul_mat_glu", "q4rdna_mul_mat_ex",
-    "q4rdna_policy_split_k", "q4rdna_plan_create", "q4rdna_plan_launch", "q4rdna_plan_destroy",
+    "q4rdna_policy_split_k", "q4rdna_plan_create", "q4rdna_plan_launch", "q4rdna_plan_prepare",
+    "q4rdna_plan_sweep", "q4rdna_plan_destroy",
     "q4rdna_plan_workgroups", "q4rdna_pack", "q4rdna_dequantize",
 )
 
@@ -99,6 +100,8 @@ def load() -> ctypes.CDLL:
         "q4rdna_policy_split_k": (u32, [u32, u32, i32]),
         "q4rdna_plan_create": (i32, [ctypes.POINTER(GemvDesc), u32, i32, ctypes.POINTER(vp)]),
         "q4rdna_plan_launch": (i32, [vp, vp]),
+        "q4rdna_plan_prepare": (i32, [vp, vp]),
+        "q4rdna_plan_sweep": (i32, [vp, vp]),
         "q4rdna_plan_destroy": (None, [vp]),
         "q4rdna_plan_workgroups": (u32, [vp]),
         "q4rdna_pack": (i32, [vp, u32, u32, i32, vp, vp]),

@@ -245,8 +245,19 @@ class Plan:
         return load().q4rdna_plan_workgroups(self._h)
 
     def launch(self, stream: int | None = None) -> bool:
+        """prepare() + sweep() on one stream."""
         s = _stream(self.device) if stream is None else stream
         return check(load().q4rdna_plan_launch(self._h, s))
+
+    def prepare(self, stream: int | None = None) -> bool:
+        """Convert every activation into the plan's int8 digit buffers."""
+        s = _stream(self.device) if stream is None else stream
+        return check(load().q4rdna_plan_prepare(self._h, s))
+
+    def sweep(self, stream: int | None = None) -> bool:
+        """Run the GEMVs (after a prepare of the same activations)."""
+        s = _stream(self.device) if stream is None else stream
+        return check(load().q4rdna_plan_sweep(self._h, s))
 
     def close(self) -> None:
         if self._h is not None and self._h.value:
