@@ -29,11 +29,12 @@ struct GemvArgs {
 };
 
 // Device-side descriptor of one GEMV in a multi-tensor plan.  Work items are
-// (64-row block, K chunk of up to kChunkGroups groups), numbered from
-// item_begin in block-major order.  The activation is first converted into
-// int8 limbs (kPrepBytes per 64-element group) in `prep`.  With chunks > 1
-// the chunks of a block meet in partial[chunk][rows] (and a second such array
-// for the SwiGLU gate) through counters[block], zero between launches.
+// (64-row block, stream, K chunk of up to kChunkGroups groups), numbered from
+// item_begin block-major, then stream (0 = w, 1 = the SwiGLU gate), then
+// chunk.  The activation is first converted into int8 digits (kPrepBytes per
+// 64-element group) in `prep`.  When a block has more than one item
+// (streams * chunks > 1) its items meet in partial[stream][chunk][rows]
+// through counters[block], zero between launches.
 struct PlanDesc {
     const uint8_t *w;
     const uint8_t *gate;
@@ -48,7 +49,7 @@ struct PlanDesc {
     uint32_t item_begin;
     uint32_t group_begin;
     uint32_t chunks;
-    uint32_t pad;
+    uint32_t streams;
 };
 
 constexpr uint32_t kPrepBytes = 272;
@@ -61,7 +62,7 @@ hipError_t launch_gemv(const GemvArgs &args, hipStream_t stream);
 // sweeps the items.  sched holds two zeroed counters owned by the plan (left
 // zero after every launch).
 hipError_t launch_prep(const PlanDesc *descs, uint32_t count, uint32_t groups, hipStream_t stream);
-hipError_t launch_plan(const PlanDesc *descs, uint32_t items, bool any_gate, uint32_t workgroups, uint32_t *sched,
+hipError_t launch_plan(const PlanDesc *descs, uint32_t items, uint32_t workgroups, uint32_t *sched,
                        hipStream_t stream);
 hipError_t launch_dequant(const uint8_t *w, uint32_t rows, uint32_t cols, float *out,
                           hipStream_t stream);
@@ -69,8 +70,8 @@ hipError_t launch_pack(const float *w, uint32_t rows, uint32_t cols, int algorit
                        hipStream_t stream);
 
 // Workgroups of 256 threads the kernels are built for, and the number the
-// plan kernel keeps resident per CU (two measured best on MI355X).
+// plan kernel launches per CU.
 constexpr uint32_t kThreads = 256;
-uint32_t plan_workgroups_per_cu(bool any_gate);
+uint32_t plan_workgroups_per_cu();
 
 }  // namespace q4rdna

@@ -15,31 +15,33 @@
 //    A = a0 + 256*a1 + 65536*a2.  x_k = A_k * 2^(E-22) to within 2^-23 of the
 //    group maximum, so the GEMV keeps fp32-level accuracy.
 //
-//  * v_mfma_i32_16x16x64_i8: D[i][j] = sum_k A[i][k] B[k][j] with A = the three
-//    digit rows of x (row 3 zero) and B = 16 weight rows, one group (64 k) per
-//    instruction; |D| <= 64 * 128 * 128 = 2^20, exact in int32.  Lane l
-//    supplies A row l%16 and B column l%16 for k-slot l/16 (16 bytes each) and
-//    receives D[4*(l/16) + v][l%16] -- checked on the device against a CPU
-//    product.  Per (row, group) the result is
+//  * v_mfma_i32_16x16x64_i8: D[i][j] = sum_k A[i][k] B[k][j] with A = digit
+//    rows of x and B = 16 weight rows, one group (64 k) per instruction;
+//    |D| <= 64 * 128 * 128 = 2^20, exact in int32.  Lane l supplies 16 bytes
+//    of A row l%16 and of B column l%16 for k-slot l/16 and receives
+//    D[4*(l/16) + v][l%16] in element v -- checked on the device against a
+//    CPU product.  Per (row, group) the result is
 //    scale * 2^(E-26) * (D0 + 256*D1 + 65536*D2) (2^-4 undoes the 16*q).
 //
-//  * Layout.  A wave takes a 64-row block (two 32-row tiles) and one group per
-//    step.  Lane (kslot = l/16, j = l%16) loads, from tile j/8, the eight code
-//    dwords of rows 4(j%8)..+3 at k-pairs 4c + kslot, c = 0..7 (so each load
-//    instruction reads 128 contiguous bytes of each tile), transposes the two
-//    4x4 byte blocks (c = 0..3, 4..7) with v_perm_b32 so each dword holds one
-//    row's four k-pairs, and splits nibbles: the four B operands of rows
-//    4j+0..3 for four MFMAs.  Element e of a lane's operand is
-//    k = 2*(16*(e/8) + 4*(e%4) + kslot) + (e/4)%2 within the group; the
+//  * Operand order.  A lane's 16 operand bytes for k-slot kslot are, for
+//    e = 0..15, k = 2*(16*(e/8) + 4*(e%4) + kslot) + (e/4)%2 within the group:
+//    the low and high nibbles of k-pairs kslot + 4c, c = 0..7, which is what
+//    a 4x4 byte transpose (v_perm_b32) of four code dwords -- four rows at
+//    one k-pair each -- followed by the nibble split produces.  The
 //    activation digits are stored in the same order.
 //
-// About 38 VALU instructions per 2048-weight tile instead of ~99.
+// The sweep kernel's lane mapping is described at the kernel below.
 #include "q4rdna_device.h"
 
 namespace q4rdna {
 namespace {
 
 constexpr int kWaves = 4;
+#ifndef Q4RDNA_PLAN_DEPTH
+#define Q4RDNA_PLAN_DEPTH 2
+#endif
+// Groups in flight per wave (register sets that rotate) on a full chunk.
+constexpr int kPlanDepth = Q4RDNA_PLAN_DEPTH;
 
 // Position of element k (0..63) of a group in the operand order above:
 // returns the byte index e (0..15) and the k-slot.
@@ -112,172 +114,262 @@ __device__ __forceinline__ void transpose4(const uint32_t d0, const uint32_t d1,
 __device__ __forceinline__ uint32_t low_nibbles_x16(uint32_t t) { return (t << 4) & 0xf0f0f0f0u; }
 __device__ __forceinline__ uint32_t high_nibbles_x16(uint32_t t) { return t & 0xf0f0f0f0u; }
 
-struct StepRegs {
-    uint32_t d[8];
-    u32x2 s;
-    i32x4 a;  // activation digits (operand A) of the group
-    float f;  // group factor 2^(E-26)
+// ---- sweep kernel ---------------------------------------------------------
+//
+// An item is (64-row block, stream, K chunk of up to 64 groups), taken by one
+// workgroup.  Its four waves read the block's two row tiles side by side: in
+// workgroup step s, wave w takes groups g0 + 4w .. g0 + 4w + 3 with
+// g0 = chunk start + 16s, so the workgroup streams two contiguous runs of 16
+// tiles.
+//
+// Loads.  Per step a wave reads eight tiles (4 groups x 2 row tiles).  Load
+// instruction c reads the whole 1024-byte code area of tile (group c/2, row
+// tile c%2), 16 contiguous bytes per lane -- long contiguous runs per
+// instruction stream markedly faster than short ones -- and the wave
+// restages it in LDS, where each lane picks up its operand bytes.  The LDS
+// copy of tile c starts at 1056*c: the 32-byte skew keeps both the stores and
+// the operand reads free of bank conflicts.
+//
+// Operands.  Lane l = 16*kslot + j with j = 4*gB + r4 and r4 = 2*T + h:
+//  * B: from the copy of tile (gB, T) the lane reads rows 16h..16h+15 at
+//    k-pairs kslot + 4c, c = 0..7 (eight 16-byte LDS reads).  Dword m of read
+//    c holds rows 16h + 4m..+3 of k-pair kslot + 4c, so the 4x4 transposes
+//    above give, for row n = 4m + q, the operand of MFMA n (16 MFMAs per
+//    step, one per row).
+//  * A: digit (j & 3) of group g0 + 4w + gB at k-slot kslot, so rows
+//    4s'..4s'+3 of A hold group g0 + 4w + s'.
+//  * D: lane l holds D rows 4*(l/16)..+3 of column j: group kslot's digits
+//    times column j's rows of group gB.  Meaningful when gB == kslot -- lanes
+//    20*gB + r4, which accumulate rows 32T + 16h + n, with the fp16 scales of
+//    those rows loaded by the same lane; the 16 (wave, gB) partial sums of
+//    each row meet in LDS at the item's end.
+constexpr int kStepGroups = 4;                         // groups per wave step
+constexpr int kWgStepGroups = kWaves * kStepGroups;    // groups per workgroup step
+constexpr int kItemSteps = kChunkGroups / kWgStepGroups;
+constexpr int kStageStride = 1056;                     // LDS bytes per staged tile (1024 + skew)
+constexpr int kStageBytes = 8 * kStageStride;          // per wave
+
+struct WaveRegs {
+    i32x4 code[8];  // tile c's 16 bytes at 16*lane (global), then the operand bytes (LDS)
+    i32x4 sc[2];    // the lane's 16 rows' fp16 scales
+    i32x4 a;        // activation digits
+    float f;        // group factor of the lane's D rows
 };
 
-// Code dwords and scales of one group for this lane (see the layout above).
-__device__ __forceinline__ StepRegs load_step(const uint8_t *__restrict__ tile, int kslot, int q) {
-    StepRegs r;
-    const uint8_t *codes = tile + 64 + 32 * kslot + 4 * q;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) r.d[c] = __builtin_nontemporal_load((gptr_u32)(codes + 128 * c));
-    r.s = __builtin_nontemporal_load((gptr_u32x2)(tile + 8 * q));
+struct LaneRole {
+    int kslot, gB, T, h;
+    uint32_t a_offset;   // digit bytes within a prep group
+    uint32_t lds_read;   // byte offset of the lane's first operand read in a staged step
+    bool useful;         // gB == kslot
+};
+
+__device__ __forceinline__ LaneRole lane_role(int lane) {
+    LaneRole r;
+    r.kslot = lane >> 4;
+    const int j = lane & 15;
+    r.gB = j >> 2;
+    r.T = (j >> 1) & 1;
+    r.h = j & 1;
+    r.a_offset = 16u * (4u * r.kslot + (j & 3));
+    r.lds_read = kStageStride * (2 * r.gB + r.T) + 32 * r.kslot + 16 * r.h;
+    r.useful = r.gB == r.kslot;
     return r;
 }
 
-// acc[m] += scale(row 4j+m) * f * (D0 + 256 D1 + 65536 D2) for the four
-// MFMAs of one step (meaningful in lanes 0..15).  D0 + 256*D1 is exact in
-// int32 (|D| <= 2^20); the 65536*D2 term joins in fp32.
-__device__ __forceinline__ void step_mfma(const StepRegs &r, const i32x4 a, const float f, float (&acc)[4]) {
-    uint32_t t[8];
-    transpose4(r.d[0], r.d[1], r.d[2], r.d[3], t[0], t[1], t[2], t[3]);
-    transpose4(r.d[4], r.d[5], r.d[6], r.d[7], t[4], t[5], t[6], t[7]);
+// Tiles of one wave step: t0 / t1 = group g of row tiles 2*block and
+// 2*block + 1; the lane's scales come from its own tile (gB, T).
+__device__ __forceinline__ void load_wave(WaveRegs &r, const uint8_t *t0, const uint8_t *t1, const uint8_t *pa,
+                                          const uint8_t *pf, const LaneRole &ln, int lane) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const uint8_t *tile = ((c & 1) ? t1 : t0) + (c >> 1) * kTileBytes;
+        r.code[c] = __builtin_nontemporal_load((gptr_i32x4)(tile + 64 + 16 * lane));
+    }
+    const uint8_t *own = (ln.T ? t1 : t0) + ln.gB * kTileBytes + 32 * ln.h;
+    r.sc[0] = __builtin_nontemporal_load((gptr_i32x4)own);
+    r.sc[1] = __builtin_nontemporal_load((gptr_i32x4)(own + 16));
+    r.a = *(gptr_i32x4)pa;
+    r.f = *(gptr_cf32)pf;
+}
+
+// Through this wave's LDS stage: store the eight tiles, read the operand
+// bytes back in their place.  LDS operations of one wave complete in order,
+// so the reads see the stores and the next step's stores follow the reads.
+__device__ __forceinline__ void restage(WaveRegs &r, uint8_t *stage, const LaneRole &ln, int lane) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) *reinterpret_cast<i32x4 *>(stage + kStageStride * c + 16 * lane) = r.code[c];
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int c = 0; c < 8; ++c) r.code[c] = *reinterpret_cast<const i32x4 *>(stage + ln.lds_read + 128 * c);
+}
+
+// acc[n] += scale(row n) * f * (D0 + 256 D1 + 65536 D2) for the 16 MFMAs of
+// one step (meaningful in the useful lanes).  D0 + 256*D1 is exact in int32
+// (|D| <= 2^20); the 65536*D2 term joins in fp32.  MASK: skip the update
+// where the lane's D group lies past the chunk.
+template <bool MASK>
+__device__ __forceinline__ void compute_wave(const WaveRegs &r, float (&acc)[16], bool valid) {
     const i32x4 zero = {0, 0, 0, 0};
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-        i32x4 b;
-        b[0] = static_cast<int>(low_nibbles_x16(t[m]));
-        b[1] = static_cast<int>(high_nibbles_x16(t[m]));
-        b[2] = static_cast<int>(low_nibbles_x16(t[4 + m]));
-        b[3] = static_cast<int>(high_nibbles_x16(t[4 + m]));
-        const i32x4 dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, zero, 0, 0, 0);
-        const int d01 = dm[0] + (dm[1] << 8);
-        const float v = fmaf(static_cast<float>(dm[2]), 65536.0f, static_cast<float>(d01));
-        const uint32_t sbits = (m < 2) ? r.s.x : r.s.y;
-        const float sf = half_bits_to_float((m & 1) ? (sbits >> 16) : sbits) * f;
-        acc[m] = fmaf(sf, v, acc[m]);
+        uint32_t t[8];
+        transpose4(r.code[0][m], r.code[1][m], r.code[2][m], r.code[3][m], t[0], t[1], t[2], t[3]);
+        transpose4(r.code[4][m], r.code[5][m], r.code[6][m], r.code[7][m], t[4], t[5], t[6], t[7]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int n = 4 * m + q;
+            i32x4 b;
+            b[0] = static_cast<int>(low_nibbles_x16(t[q]));
+            b[1] = static_cast<int>(high_nibbles_x16(t[q]));
+            b[2] = static_cast<int>(low_nibbles_x16(t[4 + q]));
+            b[3] = static_cast<int>(high_nibbles_x16(t[4 + q]));
+            const i32x4 dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(r.a, b, zero, 0, 0, 0);
+            const int d01 = dm[0] + (dm[1] << 8);
+            const float v = fmaf(static_cast<float>(dm[2]), 65536.0f, static_cast<float>(d01));
+            const uint32_t word = static_cast<uint32_t>(r.sc[n >> 3][(n >> 1) & 3]);
+            const float sf = half_bits_to_float((n & 1) ? (word >> 16) : word) * r.f;
+            const float upd = fmaf(sf, v, acc[n]);
+            acc[n] = (!MASK || valid) ? upd : acc[n];
+        }
     }
 }
 
 struct Shared {
-    float red[2][kWaves][kBlockRows];
+    uint8_t stage[kWaves][kStageBytes];
+    float red[kWaves][kStepGroups][kBlockRows];
     uint32_t next_item[2];
     uint32_t last;
 };
 
-// Partial sums of a 64-row block over groups [g_begin, g_end): wave w takes
-// groups g_begin + w, + 4, ...; threads 0..63 return rows 0..63 of the block.
-template <bool GATE>
-__device__ __forceinline__ void block_partial(Shared &sh, const PlanDesc &d, uint32_t block, uint32_t g_begin,
-                                              uint32_t g_end, float &out, float &gout) {
-    const uint32_t groups = d.cols / kGroup;
-    const uint32_t tiles = d.rows / kTileRows;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int kslot = lane >> 4, j = lane & 15, q = j & 7;
-    // The second tile of a block past the last row tile re-reads the first
-    // (its rows are never written).
-    uint32_t tile = 2 * block + (j >> 3);
-    if (tile >= tiles) tile = tiles - 1;
-    const uint8_t *wt = d.w + static_cast<size_t>(tile) * groups * kTileBytes;
-    const uint8_t *gt = GATE ? d.gate + static_cast<size_t>(tile) * groups * kTileBytes : nullptr;
-    const uint8_t *prep = d.prep;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f}, gacc[4] = {0.f, 0.f, 0.f, 0.f};
-
-    // Two register sets alternate (no copies): while one group is converted
-    // and multiplied, the next group's loads are in flight.
-    // The activation digits and group factor travel with the weights, one
-    // step ahead of their use.
-    // sched_barrier keeps the scheduler from sinking a prefetch below the
-    // conversion of the previous group (which would expose its latency).
-    auto load = [&](uint32_t g, StepRegs &r, StepRegs &gr) {
-        r = load_step(wt + static_cast<size_t>(g) * kTileBytes, kslot, q);
-        if constexpr (GATE) gr = load_step(gt + static_cast<size_t>(g) * kTileBytes, kslot, q);
-        const uint8_t *pg = prep + static_cast<size_t>(g) * kPrepBytes;
-        r.a = *(gptr_i32x4)(pg + 16 * (4 * kslot + (j & 3)));
-        r.f = *(gptr_cf32)(pg + 256);
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    auto compute = [&](const StepRegs &r, const StepRegs &gr) {
-        step_mfma(r, r.a, r.f, acc);
-        if constexpr (GATE) step_mfma(gr, r.a, r.f, gacc);
-    };
-    // A full chunk (16 groups per wave) runs as straight-line code: the
-    // waitcnt pass then counts outstanding loads exactly and each step waits
-    // only for its own group while the next one is in flight.  In a runtime
-    // loop it cannot track the loop-carried loads and waits for all of them
-    // (vmcnt(0)), prefetch included.
-    const uint32_t first = g_begin + wave;
-    if (g_end - g_begin == kChunkGroups) {
-        constexpr int kSteps = kChunkGroups / kWaves;
-        StepRegs r[2], gr[2];
-        load(first, r[0], gr[0]);
+// The wave's steps of one item: rt0 / rt1 = the block's two row tiles.
+template <bool FULL>
+__device__ __forceinline__ void item_steps(const uint8_t *rt0, const uint8_t *rt1, const uint8_t *prep,
+                                           uint32_t g_begin, uint32_t g_end, int wave, int lane, const LaneRole &ln,
+                                           uint8_t *stage, float (&acc)[16]) {
+    if constexpr (FULL) {
+        // Straight-line code: the waitcnt pass then counts outstanding loads
+        // exactly, and each step waits only for its own loads while the
+        // next kPlanDepth-1 steps' are in flight.  sched_barrier keeps a
+        // prefetch from sinking below the previous step's arithmetic.
+        constexpr int D = kPlanDepth;
+        WaveRegs r[D];
+        auto load = [&](int s, WaveRegs &rr) {
+            const uint32_t g = g_begin + kWgStepGroups * s + kStepGroups * wave;
+            load_wave(rr, rt0 + static_cast<size_t>(g) * kTileBytes, rt1 + static_cast<size_t>(g) * kTileBytes,
+                      prep + static_cast<size_t>(g + ln.gB) * kPrepBytes + ln.a_offset,
+                      prep + static_cast<size_t>(g + ln.kslot) * kPrepBytes + 256, ln, lane);
+            __builtin_amdgcn_sched_barrier(0);
+        };
 #pragma unroll
-        for (int s = 0; s < kSteps; ++s) {
-            if (s + 1 < kSteps) load(first + (s + 1) * kWaves, r[(s + 1) & 1], gr[(s + 1) & 1]);
-            compute(r[s & 1], gr[s & 1]);
+        for (int p = 0; p + 1 < D; ++p) load(p, r[p]);
+#pragma unroll
+        for (int s = 0; s < kItemSteps; ++s) {
+            if (s + D - 1 < kItemSteps) load(s + D - 1, r[(s + D - 1) % D]);
+            restage(r[s % D], stage, ln, lane);
+            compute_wave<false>(r[s % D], acc, true);
         }
     } else {
-        for (uint32_t g = first; g < g_end; g += kWaves) {
-            StepRegs r, gr;
-            load(g, r, gr);
-            compute(r, gr);
-        }
-    }
-    if (lane < 16) {
+        // A short last chunk: the step's four groups are clamped to the
+        // chunk for the loads, and those past its end are masked out.
+        for (uint32_t g = g_begin + kStepGroups * wave; g < g_end; g += kWgStepGroups) {
+            const uint32_t gb = min(g + ln.gB, g_end - 1);
+            const uint32_t gf = g + ln.kslot;
+            WaveRegs rr;
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            sh.red[0][wave][4 * j + m] = acc[m];
-            if constexpr (GATE) sh.red[1][wave][4 * j + m] = gacc[m];
+            for (int c = 0; c < 8; ++c) {
+                const uint32_t gc = min(g + (c >> 1), g_end - 1);
+                const uint8_t *tile = ((c & 1) ? rt1 : rt0) + static_cast<size_t>(gc) * kTileBytes;
+                rr.code[c] = __builtin_nontemporal_load((gptr_i32x4)(tile + 64 + 16 * lane));
+            }
+            const uint8_t *own = (ln.T ? rt1 : rt0) + static_cast<size_t>(gb) * kTileBytes + 32 * ln.h;
+            rr.sc[0] = __builtin_nontemporal_load((gptr_i32x4)own);
+            rr.sc[1] = __builtin_nontemporal_load((gptr_i32x4)(own + 16));
+            rr.a = *(gptr_i32x4)(prep + static_cast<size_t>(gb) * kPrepBytes + ln.a_offset);
+            rr.f = *(gptr_cf32)(prep + static_cast<size_t>(min(gf, g_end - 1)) * kPrepBytes + 256);
+            restage(rr, stage, ln, lane);
+            compute_wave<true>(rr, acc, gf < g_end);
         }
-    }
-    __syncthreads();
-    if (threadIdx.x < kBlockRows) {
-        const int t = threadIdx.x;
-        out = ((sh.red[0][0][t] + sh.red[0][1][t]) + sh.red[0][2][t]) + sh.red[0][3][t];
-        if constexpr (GATE) gout = ((sh.red[1][0][t] + sh.red[1][1][t]) + sh.red[1][2][t]) + sh.red[1][3][t];
     }
 }
 
-template <bool GATE>
-__device__ __forceinline__ void run_item(Shared &sh, const PlanDesc &d, uint32_t local) {
+__device__ __forceinline__ void run_item(Shared &sh, const PlanDesc &d, uint32_t local, const LaneRole &ln, int lane,
+                                         int wave) {
     const uint32_t groups = d.cols / kGroup;
-    const uint32_t block = local / d.chunks, chunk = local % d.chunks;
+    const uint32_t tiles = d.rows / kTileRows;
+    const uint32_t per = d.streams * d.chunks;  // items of one 64-row block
+    const uint32_t block = local / per, part = local - block * per;
+    const uint32_t stream = part / d.chunks, chunk = part - stream * d.chunks;
     const uint32_t g_begin = chunk * kChunkGroups;
     const uint32_t g_end = min(groups, g_begin + kChunkGroups);
-    float v = 0.f, gv = 0.f;
-    block_partial<GATE>(sh, d, block, g_begin, g_end, v, gv);
+    // The second row tile of a block past the last one re-reads the last
+    // (its rows are never written).
+    const size_t row_tile_bytes = static_cast<size_t>(groups) * kTileBytes;
+    const uint8_t *rt0 = (stream != 0 ? d.gate : d.w) + static_cast<size_t>(2 * block) * row_tile_bytes;
+    const uint8_t *rt1 = 2 * block + 1 < tiles ? rt0 + row_tile_bytes : rt0;
+    float acc[16];
+#pragma unroll
+    for (int n = 0; n < 16; ++n) acc[n] = 0.0f;
+    if (g_end - g_begin == kChunkGroups)
+        item_steps<true>(rt0, rt1, d.prep, g_begin, g_end, wave, lane, ln, sh.stage[wave], acc);
+    else
+        item_steps<false>(rt0, rt1, d.prep, g_begin, g_end, wave, lane, ln, sh.stage[wave], acc);
+
+    // The useful lanes publish their 16 rows; thread t < 64 then sums row t's
+    // 16 (wave, group) partials in a fixed order.
+    if (ln.useful) {
+        float *dst = &sh.red[wave][ln.gB][32 * ln.T + 16 * ln.h];
+#pragma unroll
+        for (int n = 0; n < 16; ++n) dst[n] = acc[n];
+    }
+    __syncthreads();
     const uint32_t row = block * kBlockRows + threadIdx.x;
     const bool mine = threadIdx.x < kBlockRows && row < d.rows;
-    if (d.chunks > 1) {
-        // Publish this chunk; the last of the block's chunks to arrive sums
-        // them in chunk order (device-scope stores, waited on before the
-        // arrival count, so the summing workgroup sees them).
-        if (mine) {
-            store_agent(&d.partial[static_cast<size_t>(chunk) * d.rows + row], v);
-            if constexpr (GATE) store_agent(&d.partial[static_cast<size_t>(d.chunks + chunk) * d.rows + row], gv);
-        }
-        wait_stores();
-        __syncthreads();
-        if (threadIdx.x == 0) sh.last = (add_agent(&d.counters[block], 1u) == d.chunks - 1) ? 1u : 0u;
-        __syncthreads();
-        if (sh.last == 0u) return;
-        if (mine) {
-            v = load_agent(&d.partial[row]);
-            if constexpr (GATE) gv = load_agent(&d.partial[static_cast<size_t>(d.chunks) * d.rows + row]);
-            for (uint32_t c = 1; c < d.chunks; ++c) {
-                v += load_agent(&d.partial[static_cast<size_t>(c) * d.rows + row]);
-                if constexpr (GATE) gv += load_agent(&d.partial[static_cast<size_t>(d.chunks + c) * d.rows + row]);
-            }
-        }
-        if (threadIdx.x == 0) store_agent(&d.counters[block], 0u);
+    float v = 0.0f;
+    if (threadIdx.x < kBlockRows) {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w)
+#pragma unroll
+            for (int g = 0; g < kStepGroups; ++g) v += sh.red[w][g][threadIdx.x];
     }
+    if (per == 1) {
+        if (mine) {
+            if (d.add != nullptr) v += ((gptr_cf32)d.add)[row];
+            ((gptr_f32)d.y)[row] = v;
+        }
+        return;
+    }
+    // Publish this part; the block's last part to arrive sums the chunks in
+    // chunk order (device-scope stores, drained before the arrival count, so
+    // the summing workgroup sees them) and applies the epilogue.
+    if (mine) store_agent(&d.partial[static_cast<size_t>(part) * d.rows + row], v);
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) sh.last = (add_agent(&d.counters[block], 1u) == per - 1) ? 1u : 0u;
+    __syncthreads();
+    if (sh.last == 0u) return;
     if (mine) {
-        if (d.add != nullptr) v += ((gptr_cf32)d.add)[row];
-        if constexpr (GATE) v *= silu(gv);
-        ((gptr_f32)d.y)[row] = v;
+        float u = load_agent(&d.partial[row]);
+        for (uint32_t c = 1; c < d.chunks; ++c) u += load_agent(&d.partial[static_cast<size_t>(c) * d.rows + row]);
+        if (d.add != nullptr) u += ((gptr_cf32)d.add)[row];
+        if (d.streams > 1) {
+            const float *gp = d.partial + static_cast<size_t>(d.chunks) * d.rows;
+            float g = load_agent(&gp[row]);
+            for (uint32_t c = 1; c < d.chunks; ++c) g += load_agent(&gp[static_cast<size_t>(c) * d.rows + row]);
+            u *= silu(g);
+        }
+        ((gptr_f32)d.y)[row] = u;
     }
+    if (threadIdx.x == 0) store_agent(&d.counters[block], 0u);
 }
 
-// Persistent grid: items are taken in sweep order from sched[0]; sched[1]
-// counts finished workgroups and the last one resets both.
-template <bool ANY_GATE>
+// Persistent grid: items are taken in sweep order from sched[0] (the next
+// one is fetched while the current one runs); sched[1] counts finished
+// workgroups and the last one resets both.
 __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ descs, uint32_t items,
                                                    uint32_t *__restrict__ sched) {
     __shared__ Shared sh;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const LaneRole ln = lane_role(lane);
     if (threadIdx.x == 0) sh.next_item[0] = add_agent(&sched[0], 1u);
     __syncthreads();
     uint32_t item = sh.next_item[0];
@@ -286,11 +378,7 @@ __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ 
     while (item < items) {
         if (threadIdx.x == 0) sh.next_item[slot ^ 1] = add_agent(&sched[0], 1u);
         while (item >= descs[d + 1].item_begin) ++d;
-        const PlanDesc &desc = descs[d];
-        if (ANY_GATE && desc.gate != nullptr)
-            run_item<true>(sh, desc, item - desc.item_begin);
-        else
-            run_item<false>(sh, desc, item - desc.item_begin);
+        run_item(sh, descs[d], item - descs[d].item_begin, ln, lane, wave);
         __syncthreads();
         slot ^= 1;
         item = sh.next_item[slot];
@@ -309,15 +397,12 @@ hipError_t launch_prep(const PlanDesc *descs, uint32_t count, uint32_t groups, h
     return hipGetLastError();
 }
 
-hipError_t launch_plan(const PlanDesc *descs, uint32_t items, bool any_gate, uint32_t workgroups, uint32_t *sched,
+hipError_t launch_plan(const PlanDesc *descs, uint32_t items, uint32_t workgroups, uint32_t *sched,
                        hipStream_t stream) {
-    if (any_gate)
-        hipLaunchKernelGGL(plan_kernel<true>, dim3(workgroups), dim3(256), 0, stream, descs, items, sched);
-    else
-        hipLaunchKernelGGL(plan_kernel<false>, dim3(workgroups), dim3(256), 0, stream, descs, items, sched);
+    hipLaunchKernelGGL(plan_kernel, dim3(workgroups), dim3(256), 0, stream, descs, items, sched);
     return hipGetLastError();
 }
 
-uint32_t plan_workgroups_per_cu(bool any_gate) { return any_gate ? 2 : 2; }
+uint32_t plan_workgroups_per_cu() { return 2; }
 
 }  // namespace q4rdna

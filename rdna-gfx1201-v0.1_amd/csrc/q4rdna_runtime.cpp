@@ -280,13 +280,12 @@ struct q4rdna_sidecar {
 struct q4rdna_plan {
     int device = 0;
     q4rdna::PlanDesc *descs = nullptr;  // count + 1 (sentinel)
-    uint8_t *scratch = nullptr;         // activation limbs, split-K partials and counters
-    uint32_t *sched = nullptr;          // [next item, finished workgroups], zero between launches
+    uint8_t *scratch = nullptr;         // activation digits, split-K partials and counters
+    uint32_t *sched = nullptr;          // [next item, finished waves], zero between launches
     uint32_t count = 0;
     uint32_t items = 0;
     uint32_t groups = 0;
     uint32_t workgroups = 0;
-    bool any_gate = false;
 };
 
 
@@ -559,6 +558,7 @@ int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device
         const uint32_t g = d.weight.columns / kGroup;
         const uint32_t chunks = (g + kChunkGroups - 1) / kChunkGroups;
         const uint32_t blocks = (d.weight.rows + kBlockRows - 1) / kBlockRows;
+        const uint32_t streams = d.gate_tiles != nullptr ? 2u : 1u;
         q4rdna::PlanDesc &p = host[i];
         p.w = d.weight.tiles;
         p.gate = d.gate_tiles;
@@ -570,17 +570,18 @@ int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device
         p.item_begin = static_cast<uint32_t>(items);
         p.group_begin = static_cast<uint32_t>(groups);
         p.chunks = chunks;
+        p.streams = streams;
         prep_off[i] = scratch;
         scratch += static_cast<uint64_t>(g) * kPrepBytes;
-        if (chunks > 1) {
+        if (chunks * streams > 1) {
             part_off[i] = scratch;
-            scratch += static_cast<uint64_t>(chunks) * d.weight.rows * (d.gate_tiles ? 2 : 1) * sizeof(float);
+            scratch += static_cast<uint64_t>(chunks) * streams * d.weight.rows * sizeof(float);
             scratch = (scratch + 255) & ~uint64_t(255);
             cnt_off[i] = scratch;
             scratch += static_cast<uint64_t>(blocks) * sizeof(uint32_t);
         }
         scratch = (scratch + 255) & ~uint64_t(255);
-        items += static_cast<uint64_t>(blocks) * chunks;
+        items += static_cast<uint64_t>(blocks) * chunks * streams;
         groups += g;
         if (items > 0xffffffffull || groups > 0xffffffffull) return fail(Q4RDNA_ERR_ARGUMENT, "plan too large");
     }
@@ -594,8 +595,7 @@ int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device
     plan->count = count;
     plan->items = static_cast<uint32_t>(items);
     plan->groups = static_cast<uint32_t>(groups);
-    for (uint32_t i = 0; i < count; ++i) plan->any_gate |= descs[i].gate_tiles != nullptr;
-    uint32_t per_cu = q4rdna::plan_workgroups_per_cu(plan->any_gate);
+    uint32_t per_cu = q4rdna::plan_workgroups_per_cu();
     if (const char *env = std::getenv("Q4RDNA_PLAN_WG_PER_CU")) {  // tuning sweeps only
         const int v = std::atoi(env);
         if (v >= 1 && v <= 16) per_cu = static_cast<uint32_t>(v);
@@ -615,7 +615,7 @@ int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device
     }
     for (uint32_t i = 0; i < count; ++i) {
         host[i].prep = plan->scratch + prep_off[i];
-        if (host[i].chunks > 1) {
+        if (host[i].chunks * host[i].streams > 1) {
             host[i].partial = reinterpret_cast<float *>(plan->scratch + part_off[i]);
             host[i].counters = reinterpret_cast<uint32_t *>(plan->scratch + cnt_off[i]);
         }
@@ -655,7 +655,7 @@ int q4rdna_plan_sweep(q4rdna_plan *plan, void *stream) {
     int rc = plan_check(plan);
     if (rc != Q4RDNA_OK) return rc;
     if (plan->items == 0) return Q4RDNA_OK;
-    hipError_t e = q4rdna::launch_plan(plan->descs, plan->items, plan->any_gate, plan->workgroups, plan->sched,
+    hipError_t e = q4rdna::launch_plan(plan->descs, plan->items, plan->workgroups, plan->sched,
                                        static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "plan sweep launch");
     return Q4RDNA_OK;

@@ -237,8 +237,12 @@ def test_sidecar_open_find_and_gemv(cuda, golden, tmp_path):
 # ----------------------------------------------------------------- multi-tensor plan
 
 def test_plan_matches_oracle(cuda):
+    # Short and full 64-group chunks, several chunks with a short last one,
+    # odd row-tile counts, and the add / SwiGLU epilogues over one and
+    # several chunks.
     shapes = [(128, 512, None), (32, 512, None), (32, 512, "add"), (128, 512, None), (384, 512, "glu"),
-              (128, 1536, None), (4096, 4096, None), (1024, 4096, "add")]
+              (128, 1536, None), (4096, 4096, None), (1024, 4096, "add"), (96, 4736, None),
+              (160, 8192, "glu"), (96, 12288, "add"), (32, 4096, "glu"), (224, 28672, None)]
     items, checks = [], []
     for i, (rows, cols, kind) in enumerate(shapes):
         t = random_tiles(rows, cols, 100 + i)
@@ -258,9 +262,15 @@ def test_plan_matches_oracle(cuda):
         checks.append((t, gt, x, add_np if kind == "add" else None, rows, cols, y))
     plan = api.Plan(items)
     assert plan.workgroups >= 1
-    for _ in range(2):
-        assert plan.launch()
+    assert plan.launch()
     torch.cuda.synchronize()
+    first = [c[-1].clone() for c in checks]
+    for c in checks:
+        c[-1].fill_(np.nan)
+    assert plan.prepare() and plan.sweep()
+    torch.cuda.synchronize()
+    for f, c in zip(first, checks):  # the counters were left clean: a second sweep repeats the first
+        assert torch.equal(f, c[-1])
     for t, gt, x, add_np, rows, cols, y in checks:
         yh = y.cpu().numpy().astype(np.float64)
         y64, a64 = O.gemv_f64(t, rows, cols, x)
@@ -273,4 +283,26 @@ def test_plan_matches_oracle(cuda):
             want = y64
         rms = np.sqrt(np.mean(want ** 2))
         assert (np.abs(yh - want) / np.maximum(np.abs(want), 0.01 * rms)).max() <= GATE_TOL, (rows, cols)
+    plan.close()
+
+
+@pytest.mark.gpu
+def test_plan_nonfinite_activation(cuda):
+    """A NaN in x makes every row NaN, as in the fp32 reference.  An infinity
+    makes every row non-finite (the reference gives +-inf or NaN per row
+    depending on the weight it meets; the digit path gives NaN).  The other
+    GEMVs of the plan are unaffected."""
+    rows, cols = 64, 4096
+    t = random_tiles(rows, cols, 7)
+    w = api.QWeight.from_tiles(dev_u8(t), rows, cols)
+    xs = [O.gaussian_x(cols, 8 + i) for i in range(3)]
+    xs[0][100] = np.nan
+    xs[1][4000] = np.inf
+    ys = [torch.zeros(rows, device="cuda") for _ in xs]
+    plan = api.Plan([(w, dev_f32(x), y) for x, y in zip(xs, ys)])
+    assert plan.launch()
+    torch.cuda.synchronize()
+    assert torch.isnan(ys[0]).all() and not torch.isfinite(ys[1]).any()
+    y64, a64 = O.gemv_f64(t, rows, cols, xs[2])
+    assert O.gemv_errors(ys[2].cpu().numpy(), y64, a64)["gate"] <= GATE_TOL
     plan.close()
