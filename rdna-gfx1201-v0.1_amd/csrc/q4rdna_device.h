@@ -12,6 +12,7 @@ namespace q4rdna {
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Global-address-space views.  Pointers read from a descriptor table are
 // generic; without the cast their loads become flat loads, which also count
@@ -20,6 +21,7 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) const unsigned int *gptr_u32;
 typedef __attribute__((address_space(1))) const u32x2 *gptr_u32x2;
 typedef __attribute__((address_space(1))) const i32x4 *gptr_i32x4;
+typedef __attribute__((address_space(1))) const f32x4 *gptr_f32x4;
 typedef __attribute__((address_space(1))) const float *gptr_cf32;
 typedef __attribute__((address_space(1))) float *gptr_f32;
 typedef __attribute__((address_space(1))) uint8_t *gptr_u8;

@@ -37,11 +37,9 @@ namespace q4rdna {
 namespace {
 
 constexpr int kWaves = 4;
-#ifndef Q4RDNA_PLAN_DEPTH
-#define Q4RDNA_PLAN_DEPTH 2
-#endif
-// Groups in flight per wave (register sets that rotate) on a full chunk.
-constexpr int kPlanDepth = Q4RDNA_PLAN_DEPTH;
+// Wave steps in flight per wave (register sets that rotate) on a full chunk;
+// deeper pipelines measured no faster.
+constexpr int kPlanDepth = 2;
 
 // Position of element k (0..63) of a group in the operand order above:
 // returns the byte index e (0..15) and the k-slot.
@@ -52,46 +50,78 @@ __device__ __forceinline__ int operand_index(int k, int &kslot) {
     return 4 * (2 * (c >> 2) + h) + (c & 3);
 }
 
-// One wave per 64-element activation group: block exponent, three int8
-// digits per element in operand order, and the group factor 2^(E-26).
-// Prep layout per group (kPrepBytes = 272): byte (kslot*4 + digit)*16 + e for
+// Activation digits.  A wave converts four 64-element groups, 16 lanes per
+// group and four elements per lane: block exponent E of the group's max |x|
+// (frexp), three balanced int8 digits per element in operand order, and the
+// group factor 2^(E-26); a non-finite element makes the factor NaN.
+// Layout per group (kPrepBytes = 272): byte (kslot*4 + digit)*16 + e for
 // digit 0..2, digit slot 3 zero; float factor at 256; zero padding to 272.
-__global__ __launch_bounds__(256) void prep_kernel(const PlanDesc *__restrict__ descs, uint32_t count,
-                                                   uint32_t total_groups) {
-    const uint32_t gid = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (gid >= total_groups) return;
-    uint32_t lo = 0, hi = count;  // descs[lo].group_begin <= gid < descs[hi].group_begin
-    while (hi - lo > 1) {
-        const uint32_t mid = (lo + hi) >> 1;
-        if (descs[mid].group_begin <= gid) lo = mid; else hi = mid;
-    }
-    const PlanDesc &d = descs[lo];
-    const uint32_t g = gid - d.group_begin;
-    const int k = threadIdx.x & 63;
-    const float xv = ((gptr_cf32)d.x)[static_cast<size_t>(g) * kGroup + k];
-    const bool bad = __any(!isfinite(xv));
-    float m = isfinite(xv) ? fabsf(xv) : 0.0f;
+// A lane's four elements k = 4q..4q+3 (q = lane % 16) land, for each k-slot
+// and digit, in two byte pairs (e, e+1) and (e+4, e+5).
+template <typename OutPtr>
+__device__ __forceinline__ void prep_group_quarter(const f32x4 xv, int q, bool valid_group, OutPtr out,
+                                                   bool &bad, int &e_out) {
+    const float xs[4] = {xv[0], xv[1], xv[2], xv[3]};
+    float m = 0.0f;
+    bool nonfinite = false;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    for (int i = 0; i < 4; ++i) {
+        nonfinite |= !isfinite(xs[i]);
+        m = fmaxf(m, isfinite(xs[i]) ? fabsf(xs[i]) : 0.0f);
+    }
+    // Max over the group's 16 lanes (xor within aligned 16-lane blocks).
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    int nf = nonfinite ? 1 : 0;
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) nf |= __shfl_xor(nf, o);
     int e = 0;
     if (m > 0.0f) (void)frexpf(m, &e);
     if (e < -100) e = -100;
-    const int A = isfinite(xv) ? static_cast<int>(rintf(ldexpf(xv, 22 - e))) : 0;
-    const int a0 = ((A + 128) & 255) - 128;
-    const int A1 = (A - a0) >> 8;
-    const int a1 = ((A1 + 128) & 255) - 128;
-    const int a2 = (A1 - a1) >> 8;
-    int kslot;
-    const int idx = operand_index(k, kslot);
+    bad = nf != 0;
+    e_out = e;
+    int dig[4][3];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int A = isfinite(xs[i]) ? static_cast<int>(rintf(ldexpf(xs[i], 22 - e))) : 0;
+        const int a0 = ((A + 128) & 255) - 128;
+        const int A1 = (A - a0) >> 8;
+        const int a1 = ((A1 + 128) & 255) - 128;
+        dig[i][0] = a0;
+        dig[i][1] = a1;
+        dig[i][2] = (A1 - a1) >> 8;
+    }
+    if (!valid_group) return;
+    // Elements 4q + i: k-pair 2q + (i >> 1), half i & 1.  For k-pair p:
+    // kslot = p & 3, c = p >> 2, e = 4*(2*(c >> 2) + half) + (c & 3).
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int k = 4 * q + i;
+        int kslot;
+        const int idx = operand_index(k, kslot);
+#pragma unroll
+        for (int dgt = 0; dgt < 3; ++dgt) out[(kslot * 4 + dgt) * 16 + idx] = static_cast<uint8_t>(dig[i][dgt]);
+        out[(kslot * 4 + 3) * 16 + idx] = 0;
+    }
+}
+
+// owner[g] = descriptor of global group g (built by the host).
+__global__ __launch_bounds__(256) void prep_kernel(const PlanDesc *__restrict__ descs,
+                                                   const uint32_t *__restrict__ owner, uint32_t total_groups) {
+    const int lane = threadIdx.x & 63, q = lane & 15;
+    const uint32_t gid = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+    const bool valid = gid < total_groups;
+    const uint32_t gq = valid ? gid : total_groups - 1;
+    const PlanDesc &d = descs[owner[gq]];
+    const uint32_t g = gq - d.group_begin;
+    const f32x4 xv = *(gptr_f32x4)(d.x + static_cast<size_t>(g) * kGroup + 4 * q);
     gptr_u8 out = (gptr_u8)(d.prep + static_cast<size_t>(g) * kPrepBytes);
-    out[(kslot * 4 + 0) * 16 + idx] = static_cast<uint8_t>(a0);
-    out[(kslot * 4 + 1) * 16 + idx] = static_cast<uint8_t>(a1);
-    out[(kslot * 4 + 2) * 16 + idx] = static_cast<uint8_t>(a2);
-    out[(kslot * 4 + 3) * 16 + idx] = 0;
-    if (k < 16) {
+    bool bad;
+    int e;
+    prep_group_quarter(xv, q, valid, out, bad, e);
+    if (valid && q < 4) {
         const float f = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 26);
-        const uint32_t bits = __float_as_uint(f);
-        out[256 + k] = k < 4 ? static_cast<uint8_t>(bits >> (8 * k)) : 0;
+        *(gptr_f32)(out + 256 + 4 * q) = q == 0 ? f : 0.0f;
     }
 }
 
@@ -234,6 +264,67 @@ __device__ __forceinline__ void compute_wave(const WaveRegs &r, float (&acc)[16]
     }
 }
 
+// Where an item's 64 sums go: y directly when the block has one item, else
+// part `part` of the block's per = streams * chunks parts.
+struct ItemOut {
+    const float *add;
+    float *y;
+    float *partial;
+    uint32_t *counters;
+    uint32_t rows, block, part, per, chunks, streams;
+};
+
+// The useful lanes publish their 16 rows; thread t < 64 then sums row t's 16
+// (wave, group) partials in a fixed order and finishes the item: y = sum
+// (+ add), or the part is published and the block's last part to arrive sums
+// the parts in chunk order (device-scope stores, drained before the arrival
+// count, so the summing workgroup sees them) and applies the epilogue.
+template <class SH>
+__device__ __forceinline__ void finish_item(SH &sh, const ItemOut &o, const float (&acc)[16], const LaneRole &ln,
+                                            int wave) {
+    if (ln.useful) {
+        float *dst = &sh.red[wave][ln.gB][32 * ln.T + 16 * ln.h];
+#pragma unroll
+        for (int n = 0; n < 16; ++n) dst[n] = acc[n];
+    }
+    __syncthreads();
+    const uint32_t row = o.block * kBlockRows + threadIdx.x;
+    const bool mine = threadIdx.x < kBlockRows && row < o.rows;
+    float v = 0.0f;
+    if (threadIdx.x < kBlockRows) {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w)
+#pragma unroll
+            for (int g = 0; g < kStepGroups; ++g) v += sh.red[w][g][threadIdx.x];
+    }
+    if (o.per == 1) {
+        if (mine) {
+            if (o.add != nullptr) v += ((gptr_cf32)o.add)[row];
+            ((gptr_f32)o.y)[row] = v;
+        }
+        return;
+    }
+    if (mine) store_agent(&o.partial[static_cast<size_t>(o.part) * o.rows + row], v);
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) sh.last = (add_agent(&o.counters[o.block], 1u) == o.per - 1) ? 1u : 0u;
+    __syncthreads();
+    if (sh.last == 0u) return;
+    if (mine) {
+        float u = load_agent(&o.partial[row]);
+        for (uint32_t k = 1; k < o.chunks; ++k) u += load_agent(&o.partial[static_cast<size_t>(k) * o.rows + row]);
+        if (o.add != nullptr) u += ((gptr_cf32)o.add)[row];
+        if (o.streams > 1) {
+            const float *gp = o.partial + static_cast<size_t>(o.chunks) * o.rows;
+            float g = load_agent(&gp[row]);
+            for (uint32_t k = 1; k < o.chunks; ++k) g += load_agent(&gp[static_cast<size_t>(k) * o.rows + row]);
+            u *= silu(g);
+        }
+        ((gptr_f32)o.y)[row] = u;
+    }
+    if (threadIdx.x == 0) store_agent(&o.counters[o.block], 0u);
+}
+
 struct Shared {
     uint8_t stage[kWaves][kStageBytes];
     float red[kWaves][kStepGroups][kBlockRows];
@@ -314,52 +405,8 @@ __device__ __forceinline__ void run_item(Shared &sh, const PlanDesc &d, uint32_t
     else
         item_steps<false>(rt0, rt1, d.prep, g_begin, g_end, wave, lane, ln, sh.stage[wave], acc);
 
-    // The useful lanes publish their 16 rows; thread t < 64 then sums row t's
-    // 16 (wave, group) partials in a fixed order.
-    if (ln.useful) {
-        float *dst = &sh.red[wave][ln.gB][32 * ln.T + 16 * ln.h];
-#pragma unroll
-        for (int n = 0; n < 16; ++n) dst[n] = acc[n];
-    }
-    __syncthreads();
-    const uint32_t row = block * kBlockRows + threadIdx.x;
-    const bool mine = threadIdx.x < kBlockRows && row < d.rows;
-    float v = 0.0f;
-    if (threadIdx.x < kBlockRows) {
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w)
-#pragma unroll
-            for (int g = 0; g < kStepGroups; ++g) v += sh.red[w][g][threadIdx.x];
-    }
-    if (per == 1) {
-        if (mine) {
-            if (d.add != nullptr) v += ((gptr_cf32)d.add)[row];
-            ((gptr_f32)d.y)[row] = v;
-        }
-        return;
-    }
-    // Publish this part; the block's last part to arrive sums the chunks in
-    // chunk order (device-scope stores, drained before the arrival count, so
-    // the summing workgroup sees them) and applies the epilogue.
-    if (mine) store_agent(&d.partial[static_cast<size_t>(part) * d.rows + row], v);
-    wait_stores();
-    __syncthreads();
-    if (threadIdx.x == 0) sh.last = (add_agent(&d.counters[block], 1u) == per - 1) ? 1u : 0u;
-    __syncthreads();
-    if (sh.last == 0u) return;
-    if (mine) {
-        float u = load_agent(&d.partial[row]);
-        for (uint32_t c = 1; c < d.chunks; ++c) u += load_agent(&d.partial[static_cast<size_t>(c) * d.rows + row]);
-        if (d.add != nullptr) u += ((gptr_cf32)d.add)[row];
-        if (d.streams > 1) {
-            const float *gp = d.partial + static_cast<size_t>(d.chunks) * d.rows;
-            float g = load_agent(&gp[row]);
-            for (uint32_t c = 1; c < d.chunks; ++c) g += load_agent(&gp[static_cast<size_t>(c) * d.rows + row]);
-            u *= silu(g);
-        }
-        ((gptr_f32)d.y)[row] = u;
-    }
-    if (threadIdx.x == 0) store_agent(&d.counters[block], 0u);
+    ItemOut o{d.add, d.y, d.partial, d.counters, d.rows, block, part, per, d.chunks, d.streams};
+    finish_item(sh, o, acc, ln, wave);
 }
 
 // Persistent grid: items are taken in sweep order from sched[0] (the next
@@ -391,9 +438,9 @@ __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ 
 
 }  // namespace
 
-hipError_t launch_prep(const PlanDesc *descs, uint32_t count, uint32_t groups, hipStream_t stream) {
+hipError_t launch_prep(const PlanDesc *descs, const uint32_t *owner, uint32_t groups, hipStream_t stream) {
     if (groups == 0) return hipSuccess;
-    hipLaunchKernelGGL(prep_kernel, dim3((groups + 3) / 4), dim3(256), 0, stream, descs, count, groups);
+    hipLaunchKernelGGL(prep_kernel, dim3((groups + 15) / 16), dim3(256), 0, stream, descs, owner, groups);
     return hipGetLastError();
 }
 

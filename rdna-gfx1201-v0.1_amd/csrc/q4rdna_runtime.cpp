@@ -184,7 +184,10 @@ int get_workspace(int device, hipStream_t stream, size_t partial_floats, size_t 
             (void)hipFree(p);
             return fail(Q4RDNA_ERR_MEMORY, "split-K counters: %s", hipGetErrorString(e));
         }
+        // Zeroed once, complete before any launch uses them (launches on
+        // non-blocking streams are not ordered after the null stream).
         e = hipMemset(c, 0, cc * sizeof(uint32_t));
+        if (e == hipSuccess) e = hipDeviceSynchronize();
         if (e != hipSuccess) {
             (void)hipFree(p);
             (void)hipFree(c);
@@ -281,7 +284,8 @@ struct q4rdna_plan {
     int device = 0;
     q4rdna::PlanDesc *descs = nullptr;  // count + 1 (sentinel)
     uint8_t *scratch = nullptr;         // activation digits, split-K partials and counters
-    uint32_t *sched = nullptr;          // [next item, finished waves], zero between launches
+    uint32_t *sched = nullptr;          // [next item, finished workgroups], zero between launches
+    uint32_t *owner = nullptr;          // descriptor index of every activation group (in scratch)
     uint32_t count = 0;
     uint32_t items = 0;
     uint32_t groups = 0;
@@ -588,6 +592,13 @@ int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device
     host[count] = q4rdna::PlanDesc{};
     host[count].item_begin = static_cast<uint32_t>(items);
     host[count].group_begin = static_cast<uint32_t>(groups);
+    // Owner table of the prep launch: descriptor index per activation group.
+    std::vector<uint32_t> owner(groups);
+    for (uint32_t i = 0; i < count; ++i)
+        for (uint32_t g = host[i].group_begin; g < host[i + 1].group_begin; ++g) owner[g] = i;
+    const uint64_t owner_off = scratch;
+    scratch += groups * sizeof(uint32_t);
+    scratch = (scratch + 255) & ~uint64_t(255);
     DeviceGuard guard(device);
     if (!guard.ok()) return fail(Q4RDNA_ERR_HIP, "hipSetDevice(%d) failed", device);
     auto plan = std::make_unique<q4rdna_plan>();
@@ -620,8 +631,11 @@ int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device
             host[i].counters = reinterpret_cast<uint32_t *>(plan->scratch + cnt_off[i]);
         }
     }
+    plan->owner = reinterpret_cast<uint32_t *>(plan->scratch + owner_off);
     e = hipMemcpy(plan->descs, host.data(), host.size() * sizeof(q4rdna::PlanDesc), hipMemcpyHostToDevice);
     if (e == hipSuccess && scratch > 0) e = hipMemset(plan->scratch, 0, scratch);
+    if (e == hipSuccess && groups > 0)
+        e = hipMemcpy(plan->owner, owner.data(), groups * sizeof(uint32_t), hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemset(plan->sched, 0, 2 * sizeof(uint32_t));
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
@@ -646,7 +660,7 @@ int plan_check(const q4rdna_plan *plan) {
 int q4rdna_plan_prepare(q4rdna_plan *plan, void *stream) {
     int rc = plan_check(plan);
     if (rc != Q4RDNA_OK) return rc;
-    hipError_t e = q4rdna::launch_prep(plan->descs, plan->count, plan->groups, static_cast<hipStream_t>(stream));
+    hipError_t e = q4rdna::launch_prep(plan->descs, plan->owner, plan->groups, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "plan prepare launch");
     return Q4RDNA_OK;
 }
