@@ -155,25 +155,37 @@ def check_parity(tensors, picks):
 
 def cpu_baseline(tensors, budget_s: float):
     """The oracle's sequential fp32 GEMV (the reference bench's CPU loop,
-    source/q4rdna_gemv_bench.hip:189-211) on one host core, over the stack's
-    tensors in order until about budget_s of CPU work."""
+    source/q4rdna_gemv_bench.hip:189-211) over the stack's tensors in layer
+    order until about budget_s of CPU work: once on all host threads (OpenMP
+    over rows, each row in sequential order) and once on one core."""
     import oracle as O
-    done_bytes, elapsed, n = 0, 0.0, 0
-    for t in tensors:
-        tiles = t["w"].tiles.cpu().numpy()
-        x = t["x"].cpu().numpy()
-        t0 = time.perf_counter()
-        O.gemv_seq_f32(tiles, t["rows"], t["cols"], x)
-        elapsed += time.perf_counter() - t0
-        done_bytes += algorithmic_bytes(t["rows"], t["cols"])
-        n += 1
-        if elapsed >= budget_s:
-            break
     stack = sum(algorithmic_bytes(t["rows"], t["cols"]) for t in tensors)
-    return dict(value=round(done_bytes / elapsed / 1e9, 4), unit="GB/s", cores=1, kind="port",
-                sample=f"first {n} of {len(tensors)} stack tensors in layer order ({done_bytes} algorithmic bytes), "
-                       f"{elapsed:.2f} s on one core: oracle/q4oracle.c gcc -O2 x86-64 baseline",
-                us_per_stack=round(elapsed / done_bytes * stack * 1e6, 1))
+
+    def run(threads):
+        done_bytes, elapsed, n, used = 0, 0.0, 0, 1
+        for t in tensors:
+            tiles = t["w"].tiles.cpu().numpy()
+            x = t["x"].cpu().numpy()
+            t0 = time.perf_counter()
+            if threads == 1:
+                O.gemv_seq_f32(tiles, t["rows"], t["cols"], x)
+            else:
+                _, used = O.gemv_seq_f32_mt(tiles, t["rows"], t["cols"], x)
+            elapsed += time.perf_counter() - t0
+            done_bytes += algorithmic_bytes(t["rows"], t["cols"])
+            n += 1
+            if elapsed >= budget_s:
+                break
+        return done_bytes, elapsed, n, used
+
+    mb, me, mn, used = run(0)
+    sb, se, sn, _ = run(1)
+    return dict(value=round(mb / me / 1e9, 4), unit="GB/s", cores=used, kind="port",
+                sample=f"first {mn} of {len(tensors)} stack tensors in layer order ({mb} algorithmic bytes), "
+                       f"{me:.2f} s on {used} OpenMP threads: oracle/q4oracle.c (gcc -O2, x86-64 baseline ISA)",
+                us_per_stack=round(me / mb * stack * 1e6, 1),
+                single_core=dict(value=round(sb / se / 1e9, 4), unit="GB/s", cores=1,
+                                 sample=f"first {sn} tensors, {se:.2f} s", us_per_stack=round(se / sb * stack * 1e6, 1)))
 
 
 def load_traffic():
@@ -186,6 +198,73 @@ def load_traffic():
 
 def mean(v):
     return sum(v) / len(v)
+
+
+def outlier_weights(rows: int, cols: int, seed: int, frac: float = 0.01, factor: float = 20.0):
+    """N(0, 0.02) fp32 on the GPU with `frac` of the (row, group) pairs --
+    an exact count chosen by a seeded shuffle -- scaled by `factor`."""
+    import torch
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    w = torch.randn(rows, cols, generator=gen, device="cuda", dtype=torch.float32).mul_(0.02)
+    groups = cols // 64
+    count = round(frac * rows * groups)
+    if count:
+        cpu = torch.Generator()
+        cpu.manual_seed(seed)
+        pick = torch.randperm(rows * groups, generator=cpu)[:count].cuda()
+        w.view(rows * groups, 64)[pick] *= factor
+    return w
+
+
+def time_tensor(rows: int, cols: int, split: int, seed: int, reps: int = 40):
+    """Mean us of one q4rdna_mul_mat_ex launch (split 0 = the shape policy),
+    back to back, rotating over >= 1 GiB of weight copies so the 256 MB
+    Infinity Cache cannot serve them."""
+    import torch
+    from q4rdna import api
+    size = api.packed_size(rows, cols)
+    copies = max(4, min(128, (1 << 30) // size + 1))
+    tiles = api.pack(outlier_weights(rows, cols, seed))
+    buf = tiles.unsqueeze(0).repeat(copies, 1)
+    ws = [api.QWeight.from_tiles(buf[c], rows, cols) for c in range(copies)]
+    x = torch.randn(cols, device="cuda")
+    y = torch.empty(rows, device="cuda")
+    for i in range(3):
+        api.mul_mat_ex(ws[i % copies], x, y, split_k=split)
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(reps):
+        api.mul_mat_ex(ws[i % copies], x, y, split_k=split)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1000.0 / reps, copies
+
+
+def tensor_table(seed: int):
+    """Per-tensor figures: the seven projection shapes and lm_head at the
+    shape policy, and the long-K split sweep (S = 1..32) with 1% outlier
+    groups."""
+    from q4rdna import api
+    rows_out = []
+    shapes = [("q/o_proj", 4096, 4096), ("k/v_proj", 1024, 4096), ("gate/up_proj", 12288, 4096),
+              ("down_proj", 4096, 12288), ("lm_head", 151936, 4096)]
+    for name, r, c in shapes:
+        us, copies = time_tensor(r, c, 0, seed)
+        gbs = algorithmic_bytes(r, c) / us / 1e3
+        rows_out.append(dict(kind="policy", name=name, rows=r, cols=c, split=api.policy_split_k(r, c), us=round(us, 2),
+                             gb_per_s=round(gbs, 1), copies=copies))
+        log(f"[tensors] {name} {r}x{c}: {us:.2f} us {gbs:.0f} GB/s")
+    for r, c in [(4096, 12288), (2048, 28672)]:
+        for split in (1, 2, 3, 4, 6, 8, 12, 16, 24, 32):
+            us, copies = time_tensor(r, c, split, seed + split)
+            gbs = algorithmic_bytes(r, c) / us / 1e3
+            rows_out.append(dict(kind="split_sweep", rows=r, cols=c, split=split, us=round(us, 2),
+                                 gb_per_s=round(gbs, 1), copies=copies))
+            log(f"[tensors] split sweep {r}x{c} S={split}: {us:.2f} us {gbs:.0f} GB/s")
+    return rows_out
 
 
 def main() -> int:
@@ -201,6 +280,9 @@ def main() -> int:
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc: five plan launches over the stack, then three plain 1 GiB "
                          "device copies (the FETCH_SIZE calibration); prints no JSON")
+    ap.add_argument("--tensors", action="store_true",
+                    help="per-tensor launch figures (projection shapes, lm_head, long-K split sweep with "
+                         "outlier groups); prints one JSON line with the table instead of the stack bench")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
@@ -209,6 +291,10 @@ def main() -> int:
 
     import torch
     from q4rdna import api
+
+    if args.tensors:
+        print(json.dumps({"per_tensor": tensor_table(args.seed)}), flush=True)
+        return 0
 
     tensors, _data = build_stack(args.layers, args.seed)
     stack_bytes = sum(algorithmic_bytes(t["rows"], t["cols"]) for t in tensors)

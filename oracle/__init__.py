@@ -68,6 +68,8 @@ def lib() -> ctypes.CDLL:
         L.q4o_dequant.argtypes = [u8p, u32, u32, f32p]
         L.q4o_dequant_ref_cpu.argtypes = [u8p, u32, u32, f32p]
         L.q4o_gemv_seq_f32.argtypes = [u8p, u32, u32, f32p, f32p, u32, u32, ctypes.c_int]
+        L.q4o_gemv_seq_f32_mt.argtypes = [u8p, u32, u32, f32p, f32p, ctypes.c_int]
+        L.q4o_gemv_seq_f32_mt.restype = ctypes.c_int
         L.q4o_gemv_f64.argtypes = [u8p, u32, u32, f32p, f64p, f64p]
         L.q4o_silu.argtypes = [ctypes.c_double]
         L.q4o_silu.restype = ctypes.c_double
@@ -142,6 +144,18 @@ def gemv_seq_f32(tiles: np.ndarray, rows: int, cols: int, x: np.ndarray,
     lib().q4o_gemv_seq_f32(_ptr(tiles, ctypes.c_uint8), rows, cols, _ptr(x, ctypes.c_float),
                            _ptr(y, ctypes.c_float), row_begin, row_end, int(ref_cpu_decode))
     return y
+
+
+def gemv_seq_f32_mt(tiles: np.ndarray, rows: int, cols: int, x: np.ndarray, threads: int = 0):
+    """q4o_gemv_seq_f32 over all rows with OpenMP threads (0 = the OpenMP
+    default); returns (y, threads used)."""
+    tiles = np.ascontiguousarray(tiles, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert x.shape == (cols,)
+    y = np.zeros(rows, dtype=np.float32)
+    used = lib().q4o_gemv_seq_f32_mt(_ptr(tiles, ctypes.c_uint8), rows, cols, _ptr(x, ctypes.c_float),
+                                     _ptr(y, ctypes.c_float), threads)
+    return y, used
 
 
 def gemv_f64(tiles: np.ndarray, rows: int, cols: int, x: np.ndarray):

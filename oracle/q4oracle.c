@@ -22,16 +22,21 @@
  *   q4o_pack                   same as the scale selectors (tile placement)
  *   q4o_dequant                exhaustive closed form fp32(s)*q incl. signed zero
  *   q4o_gemv_seq_f32           vs fp64 brute force + planted-mistake checks
+ *   q4o_gemv_seq_f32_mt        bit-identical to q4o_gemv_seq_f32 (tests)
  *   q4o_gemv_f64               vs numpy float64 matmul of the dequantized matrix
  *   q4o_silu                   vs long-double textbook g/(1+exp(-g)); the
  *                              reference's epilogue (llama.cpp unary.cuh) is not
  *                              vendored, so epilogue parity is "parity unpinned"
  *                              beyond the mathematics.
  *
- * Build: gcc -O2 -std=c11 -ffp-contract=off -fPIC -shared (no FMA contraction,
- * matching an x86-64 build of the reference without FMA instructions).
+ * Build: gcc -O2 -std=c11 -ffp-contract=off -fopenmp -fPIC -shared (no FMA
+ * contraction, matching an x86-64 build of the reference without FMA
+ * instructions; OpenMP only spreads independent rows over threads).
  */
 #include <fenv.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -455,6 +460,32 @@ void q4o_gemv_seq_f32(const uint8_t *tiles, uint32_t rows, uint32_t cols, const 
         }
         y[r] = sum;
     }
+}
+
+/* The same loop, row tiles spread over OpenMP threads (each row keeps its
+ * sequential order, so the result is identical); the CPU baseline's
+ * all-cores variant.  Returns the number of threads used. */
+int q4o_gemv_seq_f32_mt(const uint8_t *tiles, uint32_t rows, uint32_t cols, const float *x, float *y,
+                        int threads)
+{
+    int used = 1;
+    int64_t tiles_n = rows / Q4O_TILE_ROWS;
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel
+    {
+#pragma omp single
+        used = omp_get_num_threads();
+#pragma omp for schedule(static)
+        for (int64_t t = 0; t < tiles_n; ++t)
+            q4o_gemv_seq_f32(tiles, rows, cols, x, y, (uint32_t)t * Q4O_TILE_ROWS,
+                             (uint32_t)(t + 1) * Q4O_TILE_ROWS, 0);
+    }
+#else
+    (void)threads;
+    q4o_gemv_seq_f32(tiles, rows, cols, x, y, 0, rows, 0);
+#endif
+    return used;
 }
 
 /* fp64 GEMV over the exactly dequantized weights (products are exact in

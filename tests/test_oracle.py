@@ -251,6 +251,14 @@ def test_gemv_seq_f32_is_sequential_fma():
     assert np.array_equal(y, want)
 
 
+def test_gemv_seq_f32_threads_match_one_thread():
+    tiles, x = small_problem(256, 512, 9)
+    y1 = O.gemv_seq_f32(tiles, 256, 512, x)
+    ym, used = O.gemv_seq_f32_mt(tiles, 256, 512, x, threads=4)
+    assert used >= 1
+    assert np.array_equal(y1, ym)
+
+
 def test_gemv_gates_accept_oracle_and_catch_planted_mistakes():
     tiles, x = small_problem(256, 1024, 8)
     rows, cols = 256, 1024
