@@ -243,6 +243,48 @@ def time_tensor(rows: int, cols: int, split: int, seed: int, reps: int = 40):
     return a.elapsed_time(b) * 1000.0 / reps, copies
 
 
+def batch_table(tensors, batches, steps: int, warmup: int, seed: int):
+    """The stack's 252 GEMVs with N activation vectors each (the small-batch
+    decode shapes): one batched plan per N over the same weights, timed like
+    the main bench; parity of every vector of three tensors vs the oracle."""
+    import torch
+    import oracle as O
+    from q4rdna import api
+    out = []
+    gen = torch.Generator(device="cuda")
+    for n in batches:
+        items = []
+        for i, t in enumerate(tensors):
+            gen.manual_seed(seed + 0x4000 + 1000 * n + i)
+            x = torch.randn(n, t["cols"], generator=gen, device="cuda", dtype=torch.float32)
+            y = torch.empty(n, t["rows"], device="cuda", dtype=torch.float32)
+            items.append((t["w"], x, y))
+        plan = api.Plan(items, batch=n)
+        ms_per_step, sweep_ms, prep_ms = time_plan(plan, steps, warmup)
+        step_bytes = sum(algorithmic_bytes(t["rows"], t["cols"], n) for t in tensors)
+        worst = 0.0
+        for i in (0, 4, len(tensors) - 1):
+            t = tensors[i]
+            tiles = t["w"].tiles.cpu().numpy()
+            xs = items[i][1].cpu().numpy()
+            ys = items[i][2].cpu().numpy()
+            for v in range(n):
+                y64, a64 = O.gemv_f64(tiles, t["rows"], t["cols"], xs[v])
+                worst = max(worst, O.gemv_errors(ys[v], y64, a64)["gate"])
+        layers = len(tensors) / 7
+        row = dict(batch=n, us_per_stack=round(ms_per_step * 1000, 2), us_per_layer=round(ms_per_step * 1000 / layers, 2),
+                   sweep_us=round(mean(sweep_ms) * 1000, 2), prepare_us=round(mean(prep_ms) * 1000, 2),
+                   gb_per_s=round(step_bytes / ms_per_step / 1e6, 1),
+                   sweep_gb_per_s=round(step_bytes / mean(sweep_ms) / 1e6, 1),
+                   tflops=round(sum(2 * t["rows"] * t["cols"] * n for t in tensors) / ms_per_step / 1e9, 3),
+                   parity_gate_max=worst)
+        log(f"[batch] N={n}: {row}")
+        out.append(row)
+        plan.close()
+        del items
+    return out
+
+
 def tensor_table(seed: int):
     """Per-tensor figures: the seven projection shapes and lm_head at the
     shape policy, and the long-K split sweep (S = 1..32) with 1% outlier
@@ -257,6 +299,22 @@ def tensor_table(seed: int):
         rows_out.append(dict(kind="policy", name=name, rows=r, cols=c, split=api.policy_split_k(r, c), us=round(us, 2),
                              gb_per_s=round(gbs, 1), copies=copies))
         log(f"[tensors] {name} {r}x{c}: {us:.2f} us {gbs:.0f} GB/s")
+    # lm_head through a plan: four distinct copies (1.3 GB) swept per step.
+    import torch
+    r, c = 151936, 4096
+    tiles = api.pack(outlier_weights(r, c, seed, frac=0.0))
+    copies = [tiles.clone() for _ in range(4)]
+    items = [(api.QWeight.from_tiles(cp, r, c), torch.randn(c, device="cuda"), torch.empty(r, device="cuda"))
+             for cp in copies]
+    plan = api.Plan(items)
+    ms, sweep_ms, prep_ms = time_plan(plan, 20, 5)
+    us = ms * 1000 / len(items)
+    rows_out.append(dict(kind="plan", name="lm_head", rows=r, cols=c, us=round(us, 2),
+                         sweep_us=round(mean(sweep_ms) * 1000 / len(items), 2),
+                         gb_per_s=round(algorithmic_bytes(r, c) / us / 1e3, 1), copies=len(items)))
+    log(f"[tensors] lm_head via a 4-copy plan: {us:.2f} us per lm_head")
+    plan.close()
+    del items, copies, tiles
     for r, c in [(4096, 12288), (2048, 28672)]:
         for split in (1, 2, 3, 4, 6, 8, 12, 16, 24, 32):
             us, copies = time_tensor(r, c, split, seed + split)
@@ -280,6 +338,9 @@ def main() -> int:
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc: five plan launches over the stack, then three plain 1 GiB "
                          "device copies (the FETCH_SIZE calibration); prints no JSON")
+    ap.add_argument("--batches", type=str, default="",
+                    help="comma-separated batch sizes (e.g. 2,4,8): time the stack with that many activation "
+                         "vectors per GEMV and print one JSON line with the table instead of the stack bench")
     ap.add_argument("--tensors", action="store_true",
                     help="per-tensor launch figures (projection shapes, lm_head, long-K split sweep with "
                          "outlier groups); prints one JSON line with the table instead of the stack bench")
@@ -298,6 +359,10 @@ def main() -> int:
 
     tensors, _data = build_stack(args.layers, args.seed)
     stack_bytes = sum(algorithmic_bytes(t["rows"], t["cols"]) for t in tensors)
+    if args.batches:
+        sizes = [int(v) for v in args.batches.split(",") if v]
+        print(json.dumps({"batched": batch_table(tensors, sizes, args.steps, args.warmup, args.seed)}), flush=True)
+        return 0
     plan = api.Plan([(t["w"], t["x"], t["y"]) for t in tensors])
     log(f"[bench] plan: {len(tensors)} GEMVs, {plan.workgroups} workgroups")
     if args.pmc_probe:

@@ -165,6 +165,14 @@ typedef struct q4rdna_plan q4rdna_plan;
 /* Build a plan for `count` descriptors (uploads the descriptor table once). */
 int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device,
                        q4rdna_plan **out);
+/* Batched plan: every descriptor's x holds n activation vectors of
+ * `columns` floats one after another ([n][columns]), y and add hold n
+ * results of `rows` floats ([n][rows]); n = 1..Q4RDNA_MAX_BATCH (the
+ * small-batch decode shapes).  No reference counterpart: the reference's
+ * hooks decline batches above 1 (source/q4rdna.cu:722,754,777). */
+#define Q4RDNA_MAX_BATCH 8
+int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint32_t n, int device,
+                             q4rdna_plan **out);
 /* Launch the whole plan on `stream` (prepare + sweep); allocates nothing. */
 int q4rdna_plan_launch(q4rdna_plan *plan, void *stream);
 /* The two launches of q4rdna_plan_launch, for callers that time or overlap

@@ -65,6 +65,16 @@ hipError_t launch_gemv(const GemvArgs &args, hipStream_t stream);
 hipError_t launch_prep(const PlanDesc *descs, const uint32_t *owner, uint32_t groups, hipStream_t stream);
 hipError_t launch_plan(const PlanDesc *descs, uint32_t items, uint32_t workgroups, uint32_t *sched,
                        hipStream_t stream);
+// Batched plans (n = 2..8 activation vectors per GEMV; x [n][cols],
+// y and add [n][rows]): items are 256-row blocks, prep holds
+// kBatchQuadBytesHost per (group, quad of 4 vectors).
+constexpr uint32_t kBatchQuadBytesHost = 1040;
+constexpr uint32_t kBatchBlockRows = 256;
+constexpr uint32_t kBatchChunkGroups = 64;  // K chunk of a batched item (smaller chunks measured slower)
+hipError_t launch_prep_batch(const PlanDesc *descs, const uint32_t *owner, uint32_t groups, uint32_t n,
+                             hipStream_t stream);
+hipError_t launch_plan_batch(const PlanDesc *descs, uint32_t items, uint32_t n, uint32_t workgroups, uint32_t *sched,
+                             hipStream_t stream);
 hipError_t launch_dequant(const uint8_t *w, uint32_t rows, uint32_t cols, float *out,
                           hipStream_t stream);
 hipError_t launch_pack(const float *w, uint32_t rows, uint32_t cols, int algorithm, uint8_t *tiles,

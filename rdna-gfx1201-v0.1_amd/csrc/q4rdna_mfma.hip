@@ -436,6 +436,290 @@ __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ 
     }
 }
 
+// ---- batched sweep (N = 2..8 activation vectors) ---------------------------
+//
+// With several activation vectors the A operand's rows carry the vectors
+// instead of groups: one MFMA multiplies 16 row sets of ONE group by the
+// three digits of up to four vectors (rows 4n + d of A, d = 3 zero), so
+// every lane of D is useful for N = 4 and a second vector quad costs one more
+// MFMA per operand, not more loads or transposes.
+//  * Item: (256-row block = 8 row tiles, stream, K chunk of up to 64
+//    groups); wave w takes groups chunk start + w + 4s, one per step.
+//  * Loads per step: load instruction c reads the whole code area of row
+//    tile c at the step's group (1 KB contiguous), restaged through LDS as in
+//    the single-vector sweep; lane (kslot, j) then reads rows 16h..16h+15 of
+//    row tile T = j/2, h = j%2, at k-pairs kslot + 4c.
+//  * D: lane l holds D rows 4*(l/16)..+3 of column j = l%16, i.e. vector
+//    l/16 of the quad, digits 0..2, for the 16 rows of column j; it loads
+//    those rows' scales and the vector's group factor itself.
+// Prep layout per (group, vector quad), kBatchQuadBytes = 1040: digit d of
+// vector n at byte kslot*256 + (4n + d)*16 + e (the operand order above),
+// then the four vectors' group factors at 1024.
+constexpr int kBatchRows = 256;
+constexpr uint32_t kBatchQuadBytes = 1040;
+
+// One 16-lane quarter of a wave converts one (group, vector): digits at
+// `quad` + kslot*256 + (4*slot + d)*16 + e and the factor at quad + 1024 + 4*slot.
+template <typename OutPtr>
+__device__ __forceinline__ void prep_batch_quarter(const f32x4 xv, int q, bool valid, OutPtr quad, int slot) {
+    const float xs[4] = {xv[0], xv[1], xv[2], xv[3]};
+    float m = 0.0f;
+    bool nonfinite = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        nonfinite |= !isfinite(xs[i]);
+        m = fmaxf(m, isfinite(xs[i]) ? fabsf(xs[i]) : 0.0f);
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    int nf = nonfinite ? 1 : 0;
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) nf |= __shfl_xor(nf, o);
+    int e = 0;
+    if (m > 0.0f) (void)frexpf(m, &e);
+    if (e < -100) e = -100;
+    if (!valid) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int A = isfinite(xs[i]) ? static_cast<int>(rintf(ldexpf(xs[i], 22 - e))) : 0;
+        const int a0 = ((A + 128) & 255) - 128;
+        const int A1 = (A - a0) >> 8;
+        const int a1 = ((A1 + 128) & 255) - 128;
+        const int a2 = (A1 - a1) >> 8;
+        int kslot;
+        const int idx = operand_index(4 * q + i, kslot);
+        OutPtr row = quad + kslot * 256 + (4 * slot) * 16 + idx;
+        row[0] = static_cast<uint8_t>(a0);
+        row[16] = static_cast<uint8_t>(a1);
+        row[32] = static_cast<uint8_t>(a2);
+        row[48] = 0;
+    }
+    if (q == 0) {
+        const float f = nf ? __builtin_nanf("") : ldexpf(1.0f, e - 26);
+        *(gptr_f32)(quad + 1024 + 4 * slot) = f;
+    }
+}
+
+// One quarter wave per (group, vector): pairs p = g * n + vector.
+__global__ __launch_bounds__(256) void prep_batch_kernel(const PlanDesc *__restrict__ descs,
+                                                         const uint32_t *__restrict__ owner, uint32_t total_groups,
+                                                         uint32_t n) {
+    const int lane = threadIdx.x & 63, q = lane & 15;
+    const uint32_t pair = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+    const bool valid = pair < total_groups * n;
+    const uint32_t pq = valid ? pair : total_groups * n - 1;
+    const uint32_t gid = pq / n, vec = pq - gid * n;
+    const PlanDesc &d = descs[owner[gid]];
+    const uint32_t g = gid - d.group_begin;
+    const uint32_t quads = (n + 3) / 4;
+    const f32x4 xv = *(gptr_f32x4)(d.x + static_cast<size_t>(vec) * d.cols + static_cast<size_t>(g) * kGroup + 4 * q);
+    gptr_u8 quad = (gptr_u8)(d.prep + (static_cast<size_t>(g) * quads + vec / 4) * kBatchQuadBytes);
+    prep_batch_quarter(xv, q, valid, quad, static_cast<int>(vec & 3));
+}
+
+constexpr int kBatchWaves = 4;  // eight waves per workgroup measured slower
+
+// A wave's stage also receives its partial sums at the item's end (after
+// its last step, so the two uses never overlap): 4*NQ x 256 floats <= 8 KB.
+template <int NQ>
+struct BatchShared {
+    uint8_t stage[kBatchWaves][kStageBytes];
+    uint32_t next_item[2];
+    uint32_t last;
+};
+static_assert(8 * kBatchRows * sizeof(float) <= kStageBytes, "partials must fit a wave's stage");
+
+struct BatchRegs {
+    i32x4 code[8];
+    i32x4 sc[2];
+};
+
+template <int NQ>
+__device__ __forceinline__ void compute_batch(const BatchRegs &r, const i32x4 (&a)[NQ], const float (&f)[NQ],
+                                              float (&acc)[NQ][16]) {
+    const i32x4 zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        uint32_t t[8];
+        transpose4(r.code[0][m], r.code[1][m], r.code[2][m], r.code[3][m], t[0], t[1], t[2], t[3]);
+        transpose4(r.code[4][m], r.code[5][m], r.code[6][m], r.code[7][m], t[4], t[5], t[6], t[7]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int n = 4 * m + q;
+            i32x4 b;
+            b[0] = static_cast<int>(low_nibbles_x16(t[q]));
+            b[1] = static_cast<int>(high_nibbles_x16(t[q]));
+            b[2] = static_cast<int>(low_nibbles_x16(t[4 + q]));
+            b[3] = static_cast<int>(high_nibbles_x16(t[4 + q]));
+            const uint32_t word = static_cast<uint32_t>(r.sc[n >> 3][(n >> 1) & 3]);
+            const float s = half_bits_to_float((n & 1) ? (word >> 16) : word);
+#pragma unroll
+            for (int vq = 0; vq < NQ; ++vq) {
+                const i32x4 dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[vq], b, zero, 0, 0, 0);
+                const int d01 = dm[0] + (dm[1] << 8);
+                const float v = fmaf(static_cast<float>(dm[2]), 65536.0f, static_cast<float>(d01));
+                acc[vq][n] = fmaf(s * f[vq], v, acc[vq][n]);
+            }
+        }
+    }
+}
+
+template <int NQ>
+__device__ __forceinline__ void run_batch_item(BatchShared<NQ> &sh, const PlanDesc &d, uint32_t local, uint32_t nvec,
+                                               int lane, int wave) {
+    const uint32_t groups = d.cols / kGroup;
+    const uint32_t tiles = d.rows / kTileRows;
+    const uint32_t per = d.streams * d.chunks;
+    const uint32_t block = local / per, part = local - block * per;
+    const uint32_t stream = part / d.chunks, chunk = part - stream * d.chunks;
+    const uint32_t g_begin = chunk * kBatchChunkGroups;
+    const uint32_t g_end = min(groups, g_begin + kBatchChunkGroups);
+    const size_t row_tile_bytes = static_cast<size_t>(groups) * kTileBytes;
+    const uint8_t *base = stream != 0 ? d.gate : d.w;
+    const int kslot = lane >> 4, j = lane & 15, T = j >> 1, h = j & 1;
+    const uint32_t lds_read = kStageStride * T + 32 * kslot + 16 * h;
+    // The block's eight row tiles; those past the last re-read the last
+    // (their rows are never written).
+    const uint8_t *rt[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) rt[c] = base + static_cast<size_t>(min(8 * block + c, tiles - 1)) * row_tile_bytes;
+    const size_t prep_stride = static_cast<size_t>(NQ) * kBatchQuadBytes;
+    float acc[NQ][16];
+#pragma unroll
+    for (int vq = 0; vq < NQ; ++vq)
+#pragma unroll
+        for (int n = 0; n < 16; ++n) acc[vq][n] = 0.0f;
+
+    auto load = [&](uint32_t g, BatchRegs &r) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            r.code[c] = __builtin_nontemporal_load((gptr_i32x4)(rt[c] + static_cast<size_t>(g) * kTileBytes + 64 + 16 * lane));
+        const uint8_t *own = rt[T] + static_cast<size_t>(g) * kTileBytes + 32 * h;
+        r.sc[0] = __builtin_nontemporal_load((gptr_i32x4)own);
+        r.sc[1] = __builtin_nontemporal_load((gptr_i32x4)(own + 16));
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto step = [&](uint32_t g, BatchRegs &r) {
+        i32x4 a[NQ];
+        float f[NQ];
+        const uint8_t *pg = d.prep + static_cast<size_t>(g) * prep_stride;
+#pragma unroll
+        for (int vq = 0; vq < NQ; ++vq) {
+            a[vq] = *(gptr_i32x4)(pg + vq * kBatchQuadBytes + 256 * kslot + 16 * j);
+            f[vq] = *(gptr_cf32)(pg + vq * kBatchQuadBytes + 1024 + 4 * kslot);
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) *reinterpret_cast<i32x4 *>(sh.stage[wave] + kStageStride * c + 16 * lane) = r.code[c];
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int c = 0; c < 8; ++c) r.code[c] = *reinterpret_cast<const i32x4 *>(sh.stage[wave] + lds_read + 128 * c);
+        compute_batch<NQ>(r, a, f, acc);
+    };
+    if (g_end - g_begin == kBatchChunkGroups) {
+        constexpr int kSteps = kBatchChunkGroups / kBatchWaves;
+        BatchRegs r[2];
+        load(g_begin + wave, r[0]);
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            if (s + 1 < kSteps) load(g_begin + wave + kBatchWaves * (s + 1), r[(s + 1) & 1]);
+            step(g_begin + wave + kBatchWaves * s, r[s & 1]);
+        }
+    } else {
+        for (uint32_t g = g_begin + wave; g < g_end; g += kBatchWaves) {
+            BatchRegs r;
+            load(g, r);
+            step(g, r);
+        }
+    }
+
+    // Lane (kslot, j) holds vector 4*vq + kslot, rows 32T + 16h + n; the
+    // wave's partials go to red[vector][row] in its own stage.
+    float *red = reinterpret_cast<float *>(sh.stage[wave]);
+#pragma unroll
+    for (int vq = 0; vq < NQ; ++vq) {
+        const uint32_t vec = 4 * vq + kslot;
+        if (vec < nvec) {
+            float *dst = red + (4 * vq + kslot) * kBatchRows + 32 * T + 16 * h;
+#pragma unroll
+            for (int n = 0; n < 16; ++n) dst[n] = acc[vq][n];
+        }
+    }
+    __syncthreads();
+    // Threads split the block's rows; each sums its rows' partials over the
+    // waves in wave order.
+    auto total = [&](uint32_t vec, uint32_t r) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kBatchWaves; ++w) v += reinterpret_cast<const float *>(sh.stage[w])[vec * kBatchRows + r];
+        return v;
+    };
+    const size_t M = d.rows;
+    if (per == 1) {
+        for (uint32_t r = threadIdx.x; r < kBatchRows; r += blockDim.x) {
+            const uint32_t row = block * kBatchRows + r;
+            if (row >= d.rows) break;
+            for (uint32_t vec = 0; vec < nvec; ++vec) {
+                float v = total(vec, r);
+                if (d.add != nullptr) v += ((gptr_cf32)d.add)[vec * M + row];
+                ((gptr_f32)d.y)[vec * M + row] = v;
+            }
+        }
+        return;
+    }
+    for (uint32_t r = threadIdx.x; r < kBatchRows; r += blockDim.x) {
+        const uint32_t row = block * kBatchRows + r;
+        if (row >= d.rows) break;
+        for (uint32_t vec = 0; vec < nvec; ++vec)
+            store_agent(&d.partial[(static_cast<size_t>(part) * nvec + vec) * M + row], total(vec, r));
+    }
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) sh.last = (add_agent(&d.counters[block], 1u) == per - 1) ? 1u : 0u;
+    __syncthreads();
+    if (sh.last == 0u) return;
+    for (uint32_t r = threadIdx.x; r < kBatchRows; r += blockDim.x) {
+        const uint32_t row = block * kBatchRows + r;
+        if (row >= d.rows) break;
+        for (uint32_t vec = 0; vec < nvec; ++vec) {
+            float u = load_agent(&d.partial[static_cast<size_t>(vec) * M + row]);
+            for (uint32_t k = 1; k < d.chunks; ++k) u += load_agent(&d.partial[(static_cast<size_t>(k) * nvec + vec) * M + row]);
+            if (d.add != nullptr) u += ((gptr_cf32)d.add)[vec * M + row];
+            if (d.streams > 1) {
+                float g = load_agent(&d.partial[(static_cast<size_t>(d.chunks) * nvec + vec) * M + row]);
+                for (uint32_t k = 1; k < d.chunks; ++k)
+                    g += load_agent(&d.partial[(static_cast<size_t>(d.chunks + k) * nvec + vec) * M + row]);
+                u *= silu(g);
+            }
+            ((gptr_f32)d.y)[vec * M + row] = u;
+        }
+    }
+    if (threadIdx.x == 0) store_agent(&d.counters[block], 0u);
+}
+
+template <int NQ>
+__global__ __launch_bounds__(64 * kBatchWaves) void plan_batch_kernel(const PlanDesc *__restrict__ descs, uint32_t items,
+                                                         uint32_t nvec, uint32_t *__restrict__ sched) {
+    __shared__ BatchShared<NQ> sh;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (threadIdx.x == 0) sh.next_item[0] = add_agent(&sched[0], 1u);
+    __syncthreads();
+    uint32_t item = sh.next_item[0];
+    uint32_t d = 0;
+    int slot = 0;
+    while (item < items) {
+        if (threadIdx.x == 0) sh.next_item[slot ^ 1] = add_agent(&sched[0], 1u);
+        while (item >= descs[d + 1].item_begin) ++d;
+        run_batch_item<NQ>(sh, descs[d], item - descs[d].item_begin, nvec, lane, wave);
+        __syncthreads();
+        slot ^= 1;
+        item = sh.next_item[slot];
+    }
+    if (threadIdx.x == 0 && add_agent(&sched[1], 1u) == gridDim.x - 1) {
+        store_agent(&sched[0], 0u);
+        store_agent(&sched[1], 0u);
+    }
+}
+
 }  // namespace
 
 hipError_t launch_prep(const PlanDesc *descs, const uint32_t *owner, uint32_t groups, hipStream_t stream) {
@@ -447,6 +731,23 @@ hipError_t launch_prep(const PlanDesc *descs, const uint32_t *owner, uint32_t gr
 hipError_t launch_plan(const PlanDesc *descs, uint32_t items, uint32_t workgroups, uint32_t *sched,
                        hipStream_t stream) {
     hipLaunchKernelGGL(plan_kernel, dim3(workgroups), dim3(256), 0, stream, descs, items, sched);
+    return hipGetLastError();
+}
+
+hipError_t launch_prep_batch(const PlanDesc *descs, const uint32_t *owner, uint32_t groups, uint32_t n,
+                             hipStream_t stream) {
+    if (groups == 0) return hipSuccess;
+    hipLaunchKernelGGL(prep_batch_kernel, dim3((groups * n + 15) / 16), dim3(256), 0, stream, descs, owner, groups, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_plan_batch(const PlanDesc *descs, uint32_t items, uint32_t n, uint32_t workgroups, uint32_t *sched,
+                             hipStream_t stream) {
+    const dim3 block(64 * kBatchWaves);
+    if (n <= 4)
+        hipLaunchKernelGGL(plan_batch_kernel<1>, dim3(workgroups), block, 0, stream, descs, items, n, sched);
+    else
+        hipLaunchKernelGGL(plan_batch_kernel<2>, dim3(workgroups), block, 0, stream, descs, items, n, sched);
     return hipGetLastError();
 }
 

@@ -290,6 +290,7 @@ struct q4rdna_plan {
     uint32_t items = 0;
     uint32_t groups = 0;
     uint32_t workgroups = 0;
+    uint32_t batch = 1;  // activation vectors per GEMV
 };
 
 
@@ -540,14 +541,23 @@ int q4rdna_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const f
 }
 
 int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device, q4rdna_plan **out) {
+    return q4rdna_plan_create_batch(descs, count, 1, device, out);
+}
+
+int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint32_t n, int device,
+                             q4rdna_plan **out) {
     if (out == nullptr || (descs == nullptr && count > 0)) return fail(Q4RDNA_ERR_ARGUMENT, "NULL descriptors or handle");
     *out = nullptr;
-    using q4rdna::kBlockRows;
+    if (n < 1 || n > Q4RDNA_MAX_BATCH) return fail(Q4RDNA_ERR_ARGUMENT, "batch %u is outside 1..%d", n, Q4RDNA_MAX_BATCH);
     using q4rdna::kChunkGroups;
-    using q4rdna::kPrepBytes;
+    // Single vectors: 64-row blocks, kPrepBytes per group.  Batches: 256-row
+    // blocks, one kBatchQuadBytesHost record per (group, quad of vectors).
+    const uint32_t block_rows = n == 1 ? q4rdna::kBlockRows : q4rdna::kBatchBlockRows;
+    const uint64_t prep_per_group =
+        n == 1 ? q4rdna::kPrepBytes : static_cast<uint64_t>((n + 3) / 4) * q4rdna::kBatchQuadBytesHost;
     std::vector<q4rdna::PlanDesc> host(static_cast<size_t>(count) + 1);
-    // Scratch layout: activation limbs (kPrepBytes per group), then per split
-    // GEMV its partials and per-block counters.
+    // Scratch layout: activation digits (prep_per_group per group), then per
+    // GEMV with several items per block its partials and per-block counters.
     uint64_t items = 0, groups = 0, scratch = 0;
     std::vector<uint64_t> prep_off(count), part_off(count), cnt_off(count);
     for (uint32_t i = 0; i < count; ++i) {
@@ -560,8 +570,9 @@ int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device
             return fail(Q4RDNA_ERR_ARGUMENT, "descriptor %u: invalid shape or alignment", i);
         if (d.weight.device != device) return fail(Q4RDNA_ERR_ARGUMENT, "descriptor %u lives on device %d", i, d.weight.device);
         const uint32_t g = d.weight.columns / kGroup;
-        const uint32_t chunks = (g + kChunkGroups - 1) / kChunkGroups;
-        const uint32_t blocks = (d.weight.rows + kBlockRows - 1) / kBlockRows;
+        const uint32_t chunk_groups = n == 1 ? kChunkGroups : q4rdna::kBatchChunkGroups;
+        const uint32_t chunks = (g + chunk_groups - 1) / chunk_groups;
+        const uint32_t blocks = (d.weight.rows + block_rows - 1) / block_rows;
         const uint32_t streams = d.gate_tiles != nullptr ? 2u : 1u;
         q4rdna::PlanDesc &p = host[i];
         p.w = d.weight.tiles;
@@ -576,10 +587,10 @@ int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device
         p.chunks = chunks;
         p.streams = streams;
         prep_off[i] = scratch;
-        scratch += static_cast<uint64_t>(g) * kPrepBytes;
+        scratch += static_cast<uint64_t>(g) * prep_per_group;
         if (chunks * streams > 1) {
             part_off[i] = scratch;
-            scratch += static_cast<uint64_t>(chunks) * streams * d.weight.rows * sizeof(float);
+            scratch += static_cast<uint64_t>(chunks) * streams * n * d.weight.rows * sizeof(float);
             scratch = (scratch + 255) & ~uint64_t(255);
             cnt_off[i] = scratch;
             scratch += static_cast<uint64_t>(blocks) * sizeof(uint32_t);
@@ -603,6 +614,7 @@ int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device
     if (!guard.ok()) return fail(Q4RDNA_ERR_HIP, "hipSetDevice(%d) failed", device);
     auto plan = std::make_unique<q4rdna_plan>();
     plan->device = device;
+    plan->batch = n;
     plan->count = count;
     plan->items = static_cast<uint32_t>(items);
     plan->groups = static_cast<uint32_t>(groups);
@@ -660,7 +672,10 @@ int plan_check(const q4rdna_plan *plan) {
 int q4rdna_plan_prepare(q4rdna_plan *plan, void *stream) {
     int rc = plan_check(plan);
     if (rc != Q4RDNA_OK) return rc;
-    hipError_t e = q4rdna::launch_prep(plan->descs, plan->owner, plan->groups, static_cast<hipStream_t>(stream));
+    hipError_t e = plan->batch == 1
+                       ? q4rdna::launch_prep(plan->descs, plan->owner, plan->groups, static_cast<hipStream_t>(stream))
+                       : q4rdna::launch_prep_batch(plan->descs, plan->owner, plan->groups, plan->batch,
+                                                   static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "plan prepare launch");
     return Q4RDNA_OK;
 }
@@ -669,8 +684,11 @@ int q4rdna_plan_sweep(q4rdna_plan *plan, void *stream) {
     int rc = plan_check(plan);
     if (rc != Q4RDNA_OK) return rc;
     if (plan->items == 0) return Q4RDNA_OK;
-    hipError_t e = q4rdna::launch_plan(plan->descs, plan->items, plan->workgroups, plan->sched,
-                                       static_cast<hipStream_t>(stream));
+    hipError_t e = plan->batch == 1
+                       ? q4rdna::launch_plan(plan->descs, plan->items, plan->workgroups, plan->sched,
+                                             static_cast<hipStream_t>(stream))
+                       : q4rdna::launch_plan_batch(plan->descs, plan->items, plan->batch, plan->workgroups,
+                                                   plan->sched, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "plan sweep launch");
     return Q4RDNA_OK;
 }

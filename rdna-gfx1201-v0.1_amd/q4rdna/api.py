@@ -221,8 +221,11 @@ def scope_allows(scope: str | None, name: str) -> bool:
 class Plan:
     """A multi-tensor GEMV sweep launched as one kernel."""
 
-    def __init__(self, items: Sequence[tuple], device: int = 0):
-        """items: (weight, x, y) or (weight, x, y, gate_weight_or_None, add_or_None)."""
+    def __init__(self, items: Sequence[tuple], device: int = 0, batch: int = 1):
+        """items: (weight, x, y) or (weight, x, y, gate_weight_or_None, add_or_None).
+
+        batch > 1: each x holds `batch` activation vectors ([batch, cols],
+        contiguous), y and add hold [batch, rows]."""
         descs = (GemvDesc * len(items))()
         self._keep = []
         for i, it in enumerate(items):
@@ -236,9 +239,10 @@ class Plan:
             descs[i].y = y.data_ptr()
             self._keep.append(it)
         h = ctypes.c_void_p()
-        check(load().q4rdna_plan_create(descs, len(items), device, ctypes.byref(h)))
+        check(load().q4rdna_plan_create_batch(descs, len(items), batch, device, ctypes.byref(h)))
         self._h = h
         self.device = device
+        self.batch = batch
 
     @property
     def workgroups(self) -> int:

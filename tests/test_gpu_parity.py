@@ -306,3 +306,68 @@ def test_plan_nonfinite_activation(cuda):
     y64, a64 = O.gemv_f64(t, rows, cols, xs[2])
     assert O.gemv_errors(ys[2].cpu().numpy(), y64, a64)["gate"] <= GATE_TOL
     plan.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batch", [2, 3, 4, 5, 8])
+def test_batched_plan_matches_oracle(cuda, batch):
+    """Every vector of a batched plan against the fp64 oracle: short and
+    full chunks, several chunks, odd row-tile counts, row counts that are not
+    a multiple of 256, add and SwiGLU epilogues."""
+    shapes = [(256, 4096, None), (96, 512, None), (1024, 4096, "add"), (160, 8192, "glu"),
+              (4096, 4096, None), (288, 12288, "add"), (32, 4736, "glu"), (512, 1536, None)]
+    items, checks = [], []
+    for i, (rows, cols, kind) in enumerate(shapes):
+        t = random_tiles(rows, cols, 500 + 17 * batch + i)
+        xs = np.stack([O.gaussian_x(cols, 600 + 31 * batch + 7 * i + v) for v in range(batch)])
+        w = api.QWeight.from_tiles(dev_u8(t), rows, cols)
+        y = torch.full((batch, rows), np.nan, device="cuda")
+        gate = add = None
+        gt = add_np = None
+        if kind == "glu":
+            gt = random_tiles(rows, cols, 700 + i)
+            gate = api.QWeight.from_tiles(dev_u8(gt), rows, cols)
+        if kind == "add":
+            add_np = np.stack([O.gaussian_x(rows, 800 + i + v) for v in range(batch)])
+            add = dev_f32(add_np)
+        items.append((w, dev_f32(xs), y, gate, add))
+        checks.append((t, gt, xs, add_np, rows, cols, y))
+    plan = api.Plan(items, batch=batch)
+    for _ in range(2):
+        assert plan.launch()
+    torch.cuda.synchronize()
+    for t, gt, xs, add_np, rows, cols, y in checks:
+        yh = y.cpu().numpy().astype(np.float64)
+        for v in range(batch):
+            y64, _ = O.gemv_f64(t, rows, cols, xs[v])
+            if gt is not None:
+                g64, _ = O.gemv_f64(gt, rows, cols, xs[v])
+                want = y64 * O.silu(g64)
+            elif add_np is not None:
+                want = y64 + add_np[v]
+            else:
+                want = y64
+            rms = np.sqrt(np.mean(want ** 2))
+            err = (np.abs(yh[v] - want) / np.maximum(np.abs(want), 0.01 * rms)).max()
+            assert err <= GATE_TOL, (rows, cols, kind, v, err)
+    plan.close()
+
+
+@pytest.mark.gpu
+def test_batched_plan_rows_are_independent_of_batch(cuda):
+    """A vector's result depends only on that vector: the batch-4 result of
+    vector v equals the batch-8 result of the same vector bit for bit (both
+    run the same digits and the same per-row summation order)."""
+    rows, cols = 512, 4096
+    t = random_tiles(rows, cols, 901)
+    w = api.QWeight.from_tiles(dev_u8(t), rows, cols)
+    xs = np.stack([O.gaussian_x(cols, 910 + v) for v in range(8)])
+    y4 = torch.empty((4, rows), device="cuda")
+    y8 = torch.empty((8, rows), device="cuda")
+    p4 = api.Plan([(w, dev_f32(xs[:4]), y4)], batch=4)
+    p8 = api.Plan([(w, dev_f32(xs), y8)], batch=8)
+    assert p4.launch() and p8.launch()
+    torch.cuda.synchronize()
+    assert torch.equal(y4, y8[:4])
+    p4.close()
+    p8.close()
