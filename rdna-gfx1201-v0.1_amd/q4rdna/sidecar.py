@@ -82,3 +82,56 @@ def write_sidecar(path_or_file, tensors: Iterable[tuple[str, int, int, bytes]]) 
         if own:
             f.close()
     return end
+
+
+class SidecarWriter:
+    """Streams a sidecar to disk: header and index first, then each tensor's
+    packed tiles in index order (same bytes as :func:`write_sidecar`)."""
+
+    def __init__(self, path, tensors: Iterable[tuple[str, int, int]]):
+        self.data_offset, self.entries, self.end = layout(tensors)
+        self._f = open(path, "wb")
+        self._next = 0
+        self._f.write(HEADER.pack(MAGIC, 1, len(self.entries), GROUP, TILE_ROWS, TILE_BYTES, 0, self.data_offset,
+                                  self.end - self.data_offset))
+        for name, rows, cols, off, size in self.entries:
+            self._f.write(ENTRY.pack(name.encode("ascii"), rows, cols, off, size, 0))
+        self._pos = HEADER.size + ENTRY.size * len(self.entries)
+
+    def add(self, name: str, data) -> None:
+        """Append the next tensor's packed bytes (index order)."""
+        if self._next >= len(self.entries):
+            raise ValueError("more tensors than the index holds")
+        ename, rows, cols, off, size = self.entries[self._next]
+        if name != ename:
+            raise ValueError(f"expected {ename}, got {name}")
+        data = memoryview(data).cast("B")
+        if data.nbytes != size:
+            raise ValueError(f"{name}: {data.nbytes} bytes, expected {size}")
+        self._f.write(bytes(off - self._pos))
+        self._f.write(data)
+        self._pos = off + size
+        self._next += 1
+
+    def close(self) -> int:
+        if self._f is None:
+            return self.end
+        try:
+            if self._next != len(self.entries):
+                raise ValueError(f"{len(self.entries) - self._next} tensors were not written")
+            self._f.write(bytes(self.end - self._pos))
+        finally:
+            self._f.close()
+            self._f = None
+        return self.end
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        if exc[0] is None:
+            self.close()
+        elif self._f is not None:
+            self._f.close()
+            self._f = None
+        return False
