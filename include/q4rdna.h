@@ -155,7 +155,7 @@ uint32_t q4rdna_policy_split_k(uint32_t rows, uint32_t columns, int device);
 typedef struct q4rdna_gemv_desc {
     q4rdna_weight weight;      /* W (the up projection for SwiGLU) */
     const uint8_t *gate_tiles; /* SwiGLU gate tiles of the same shape, or NULL */
-    const float *x;            /* [columns] */
+    const float *x;            /* [columns], 16-byte aligned */
     const float *add;          /* [rows] or NULL */
     float *y;                  /* [rows] */
 } q4rdna_gemv_desc;

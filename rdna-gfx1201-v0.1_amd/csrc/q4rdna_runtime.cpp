@@ -565,7 +565,7 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
         if (d.weight.tiles == nullptr || d.x == nullptr || d.y == nullptr)
             return fail(Q4RDNA_ERR_ARGUMENT, "descriptor %u has a NULL pointer", i);
         if (!valid_shape(d.weight.rows, d.weight.columns) || !aligned(d.weight.tiles, 16) ||
-            (d.gate_tiles != nullptr && !aligned(d.gate_tiles, 16)) || !aligned(d.x, 4) || !aligned(d.y, 4) ||
+            (d.gate_tiles != nullptr && !aligned(d.gate_tiles, 16)) || !aligned(d.x, 16) || !aligned(d.y, 4) ||
             (d.add != nullptr && !aligned(d.add, 4)))
             return fail(Q4RDNA_ERR_ARGUMENT, "descriptor %u: invalid shape or alignment", i);
         if (d.weight.device != device) return fail(Q4RDNA_ERR_ARGUMENT, "descriptor %u lives on device %d", i, d.weight.device);

@@ -371,3 +371,67 @@ def test_batched_plan_rows_are_independent_of_batch(cuda):
     assert torch.equal(y4, y8[:4])
     p4.close()
     p8.close()
+
+
+@pytest.mark.gpu
+def test_plan_and_mul_mat_replay_from_a_hip_graph(cuda):
+    """A plan launch and per-tensor launches captured into one HIP graph (the
+    plan allocates nothing per launch; the per-tensor workspace is allocated
+    by an eager call first).  Replayed several times with new activations and
+    eager work in between; every replay must equal the eager results bit for
+    bit."""
+    rows, cols = 1024, 4096
+    tiles = [random_tiles(rows, cols, 1200 + i) for i in range(3)]
+    ws = [api.QWeight.from_tiles(dev_u8(t), rows, cols) for t in tiles]
+    xs = [torch.empty(cols, device="cuda") for _ in ws]
+    ys_plan = [torch.empty(rows, device="cuda") for _ in ws]
+    y_single = torch.empty(rows, device="cuda")
+    s = torch.cuda.Stream()
+    plan = api.Plan([(w, x, y) for w, x, y in zip(ws, xs, ys_plan)])
+
+    def work():
+        assert plan.launch(s.cuda_stream)
+        api.mul_mat(ws[0], xs[1], y_single, stream=s.cuda_stream)
+
+    with torch.cuda.stream(s):
+        for x in xs:
+            x.normal_()
+        work()  # allocates the per-tensor split-K workspace of stream s
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        work()
+    for rep in range(4):
+        with torch.cuda.stream(s):
+            for x in xs:
+                x.normal_()
+            work()
+        s.synchronize()
+        eager = [y.clone() for y in ys_plan] + [y_single.clone()]
+        for y in ys_plan + [y_single]:
+            y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+        s.synchronize()
+        for got, want in zip(ys_plan + [y_single], eager):
+            assert torch.equal(got, want), rep
+        # and the replay is right, not just repeatable
+        y64, a64 = O.gemv_f64(tiles[2], rows, cols, xs[2].cpu().numpy())
+        assert O.gemv_errors(ys_plan[2].cpu().numpy(), y64, a64)["gate"] <= GATE_TOL
+    plan.close()
+
+
+@pytest.mark.gpu
+def test_plan_rejects_bad_descriptors(cuda):
+    """Argument errors raise (negative status) and create nothing."""
+    t = random_tiles(64, 128, 5)
+    w = api.QWeight.from_tiles(dev_u8(t), 64, 128)
+    x = torch.zeros(128, device="cuda")
+    y = torch.zeros(64, device="cuda")
+    with pytest.raises(api.Q4RdnaError):
+        api.Plan([(w, x, y)], batch=9)
+    with pytest.raises(api.Q4RdnaError):
+        api.Plan([(w, x, y)], batch=0)
+    with pytest.raises(api.Q4RdnaError):
+        api.Plan([(w, x[1:], y)])  # misaligned activation
