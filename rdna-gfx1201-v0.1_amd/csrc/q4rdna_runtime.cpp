@@ -211,12 +211,13 @@ bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 constexpr uint32_t kMaxSplit = 64;
 
 uint32_t policy_split(uint32_t rows, uint32_t cols, int device) {
-    // About two workgroups per CU, keeping at least 16 groups (four per wave)
-    // in every K chunk.  Measured on MI355X: 4096x4096 -> 4, 1024x4096 -> 4,
-    // 12288x4096 -> 2, 4096x12288 -> 4..8, 2048x28672 -> 8.
+    // About three workgroups per CU, keeping at least 16 groups (four per
+    // wave) in every K chunk.  Measured on MI355X (split sweep): 4096x4096
+    // best at 4, 1024x4096 at 4, 12288x4096 at 2, 4096x12288 at 6,
+    // 2048x28672 at 8 (12 within 4 %).
     const uint32_t tiles = rows / kTileRows;
     const uint32_t groups = cols / kGroup;
-    const uint32_t target = cu_count(device) * 2;
+    const uint32_t target = cu_count(device) * 3;
     uint32_t split = (target + tiles - 1) / tiles;
     const uint32_t max_by_groups = std::max<uint32_t>(1, groups / 16);
     split = std::min(split, max_by_groups);
