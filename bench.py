@@ -188,6 +188,51 @@ def cpu_baseline(tensors, budget_s: float):
                                  sample=f"first {sn} tensors, {se:.2f} s", us_per_stack=round(se / sb * stack * 1e6, 1)))
 
 
+def host_description() -> str:
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return f"{os.cpu_count()} logical CPUs, {model or 'unknown model'}"
+
+
+def pack_figures(seed: int, sample_rows: int = 1024):
+    """Quantize + pack of one 4096x4096 N(0, 0.02) tensor with the sidecar
+    search: the GPU packer on the whole tensor, the oracle's C restatement of
+    the native packer (source/q4rdna_sidecar_pack.cpp:126-179) on one thread
+    over the first `sample_rows` rows, extrapolated; and whether the two
+    agree byte for byte on the sample."""
+    import numpy as np
+    import torch
+    import oracle as O
+    from q4rdna import api
+    rows = cols = 4096
+    w = outlier_weights(rows, cols, seed, frac=0.0)
+    api.pack(w)
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    tiles = api.pack(w)
+    b.record()
+    torch.cuda.synchronize()
+    gpu_ms = a.elapsed_time(b)
+    sample = w[:sample_rows].cpu().numpy()
+    t0 = time.perf_counter()
+    ref = O.pack(sample, O.ALGO_SIDECAR)
+    cpu_s = time.perf_counter() - t0
+    same = bool(np.array_equal(ref, tiles[:ref.size].cpu().numpy()))
+    return dict(shape="4096x4096", algorithm="sidecar (10 starts x 12 LSQ iterations)", gpu_ms=round(gpu_ms, 3),
+                cpu_s=round(cpu_s * rows / sample_rows, 2), cpu_threads=1,
+                cpu_sample=f"first {sample_rows} rows, {cpu_s:.2f} s, extrapolated to 4096 rows",
+                gpu_matches_oracle_on_sample=same)
+
+
 def load_traffic():
     try:
         with open(TRAFFIC_FILE) as f:
@@ -299,8 +344,42 @@ def tensor_table(seed: int):
         rows_out.append(dict(kind="policy", name=name, rows=r, cols=c, split=api.policy_split_k(r, c), us=round(us, 2),
                              gb_per_s=round(gbs, 1), copies=copies))
         log(f"[tensors] {name} {r}x{c}: {us:.2f} us {gbs:.0f} GB/s")
-    # lm_head through a plan: four distinct copies (1.3 GB) swept per step.
+    # The reference's fused sites: SwiGLU gate/up (two weight streams) and
+    # the bias add, one launch each.
     import torch
+    for name, r, c, kind in [("gate+up SwiGLU", 12288, 4096, "glu"), ("o_proj + add", 4096, 4096, "add")]:
+        size = api.packed_size(r, c)
+        copies = max(4, min(128, (1 << 30) // (2 * size) + 1))
+        up = api.pack(outlier_weights(r, c, seed + 1))
+        gt = api.pack(outlier_weights(r, c, seed + 2))
+        ups = [api.QWeight.from_tiles(t, r, c) for t in up.unsqueeze(0).repeat(copies, 1)]
+        gates = [api.QWeight.from_tiles(t, r, c) for t in gt.unsqueeze(0).repeat(copies, 1)]
+        x = torch.randn(c, device="cuda")
+        add = torch.randn(r, device="cuda")
+        y = torch.empty(r, device="cuda")
+
+        def launch(i):
+            if kind == "glu":
+                api.mul_mat_glu(ups[i % copies], gates[i % copies], x, y)
+            else:
+                api.mul_mat_add(ups[i % copies], x, add, y)
+        for i in range(3):
+            launch(i)
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(40):
+            launch(i)
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1000 / 40
+        nbytes = algorithmic_bytes(r, c) + (17 * r * c // 32 if kind == "glu" else 4 * r)
+        rows_out.append(dict(kind="fused", name=name, rows=r, cols=c, us=round(us, 2),
+                             gb_per_s=round(nbytes / us / 1e3, 1), copies=copies))
+        log(f"[tensors] {name} {r}x{c}: {us:.2f} us {nbytes / us / 1e3:.0f} GB/s")
+        del ups, gates, up, gt
+    # lm_head through a plan: four distinct copies (1.3 GB) swept per step.
     r, c = 151936, 4096
     tiles = api.pack(outlier_weights(r, c, seed, frac=0.0))
     copies = [tiles.clone() for _ in range(4)]
@@ -422,6 +501,8 @@ def main() -> int:
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(tensors, args.cpu_budget)
+        out["cpu_baseline"]["host"] = host_description()
+        out["pack"] = pack_figures(args.seed)
     print(json.dumps(out), flush=True)
     return 0
 
