@@ -58,11 +58,12 @@ constexpr uint32_t kBlockRows = 64;
 
 hipError_t launch_gemv(const GemvArgs &args, hipStream_t stream);
 // descs[count] plus a sentinel whose item_begin / group_begin are the totals.
-// The prep launch converts every activation into digits (owner[g] = the
-// descriptor of global group g); the plan launch then sweeps the items.
-// sched holds two zeroed counters owned by the plan (left zero after every
-// launch).
-hipError_t launch_prep(const PlanDesc *descs, const uint32_t *owner, uint32_t groups, hipStream_t stream);
+// The prep launch converts every activation into digits: group g of the
+// plan (global numbering) reads its 64 floats at group_x[g] and writes
+// kPrepBytes at prep + g * kPrepBytes.  The plan launch then sweeps the
+// items.  sched holds two zeroed counters owned by the plan (left zero after
+// every launch).
+hipError_t launch_prep(const float *const *group_x, uint8_t *prep, uint32_t groups, hipStream_t stream);
 hipError_t launch_plan(const PlanDesc *descs, uint32_t items, uint32_t workgroups, uint32_t *sched,
                        hipStream_t stream);
 // Batched plans (n = 2..8 activation vectors per GEMV; x [n][cols],

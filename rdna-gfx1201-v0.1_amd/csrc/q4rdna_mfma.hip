@@ -105,17 +105,17 @@ __device__ __forceinline__ void prep_group_quarter(const f32x4 xv, int q, bool v
     }
 }
 
-// owner[g] = descriptor of global group g (built by the host).
-__global__ __launch_bounds__(256) void prep_kernel(const PlanDesc *__restrict__ descs,
-                                                   const uint32_t *__restrict__ owner, uint32_t total_groups) {
+// group_x[g] = address of global group g's 64 activations (built by the
+// host); the digits go to prep + g * kPrepBytes.
+__global__ __launch_bounds__(256) void prep_kernel(const float *const *__restrict__ group_x,
+                                                   uint8_t *__restrict__ prep, uint32_t total_groups) {
     const int lane = threadIdx.x & 63, q = lane & 15;
     const uint32_t gid = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
     const bool valid = gid < total_groups;
     const uint32_t gq = valid ? gid : total_groups - 1;
-    const PlanDesc &d = descs[owner[gq]];
-    const uint32_t g = gq - d.group_begin;
-    const f32x4 xv = *(gptr_f32x4)(d.x + static_cast<size_t>(g) * kGroup + 4 * q);
-    gptr_u8 out = (gptr_u8)(d.prep + static_cast<size_t>(g) * kPrepBytes);
+    const float *x = group_x[gq];
+    const f32x4 xv = *(gptr_f32x4)(x + 4 * q);
+    gptr_u8 out = (gptr_u8)(prep + static_cast<size_t>(gq) * kPrepBytes);
     bool bad;
     int e;
     prep_group_quarter(xv, q, valid, out, bad, e);
@@ -722,9 +722,9 @@ __global__ __launch_bounds__(64 * kBatchWaves) void plan_batch_kernel(const Plan
 
 }  // namespace
 
-hipError_t launch_prep(const PlanDesc *descs, const uint32_t *owner, uint32_t groups, hipStream_t stream) {
+hipError_t launch_prep(const float *const *group_x, uint8_t *prep, uint32_t groups, hipStream_t stream) {
     if (groups == 0) return hipSuccess;
-    hipLaunchKernelGGL(prep_kernel, dim3((groups + 15) / 16), dim3(256), 0, stream, descs, owner, groups);
+    hipLaunchKernelGGL(prep_kernel, dim3((groups + 15) / 16), dim3(256), 0, stream, group_x, prep, groups);
     return hipGetLastError();
 }
 

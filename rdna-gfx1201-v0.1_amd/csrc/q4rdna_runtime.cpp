@@ -286,7 +286,7 @@ struct q4rdna_plan {
     q4rdna::PlanDesc *descs = nullptr;  // count + 1 (sentinel)
     uint8_t *scratch = nullptr;         // activation digits, split-K partials and counters
     uint32_t *sched = nullptr;          // [next item, finished workgroups], zero between launches
-    uint32_t *owner = nullptr;          // descriptor index of every activation group (in scratch)
+    uint8_t *table = nullptr;           // prep launch's group table (in scratch)
     uint32_t count = 0;
     uint32_t items = 0;
     uint32_t groups = 0;
@@ -557,10 +557,12 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
     const uint64_t prep_per_group =
         n == 1 ? q4rdna::kPrepBytes : static_cast<uint64_t>((n + 3) / 4) * q4rdna::kBatchQuadBytesHost;
     std::vector<q4rdna::PlanDesc> host(static_cast<size_t>(count) + 1);
-    // Scratch layout: activation digits (prep_per_group per group), then per
-    // GEMV with several items per block its partials and per-block counters.
+    // Scratch layout: activation digits of every group in global group order
+    // (prep_per_group each), the prep launch's group table, then per GEMV
+    // with several items per block its partials and per-block counters
+    // (offsets below are relative to the end of the first two regions).
     uint64_t items = 0, groups = 0, scratch = 0;
-    std::vector<uint64_t> prep_off(count), part_off(count), cnt_off(count);
+    std::vector<uint64_t> part_off(count), cnt_off(count);
     for (uint32_t i = 0; i < count; ++i) {
         const q4rdna_gemv_desc &d = descs[i];
         if (d.weight.tiles == nullptr || d.x == nullptr || d.y == nullptr)
@@ -587,8 +589,6 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
         p.group_begin = static_cast<uint32_t>(groups);
         p.chunks = chunks;
         p.streams = streams;
-        prep_off[i] = scratch;
-        scratch += static_cast<uint64_t>(g) * prep_per_group;
         if (chunks * streams > 1) {
             part_off[i] = scratch;
             scratch += static_cast<uint64_t>(chunks) * streams * n * d.weight.rows * sizeof(float);
@@ -604,13 +604,21 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
     host[count] = q4rdna::PlanDesc{};
     host[count].item_begin = static_cast<uint32_t>(items);
     host[count].group_begin = static_cast<uint32_t>(groups);
-    // Owner table of the prep launch: descriptor index per activation group.
-    std::vector<uint32_t> owner(groups);
+    // Group table of the prep launch: single vectors get each group's
+    // activation address (one load, no descriptor lookup); batches the
+    // descriptor index of each group.
+    const uint64_t table_off = (groups * prep_per_group + 255) & ~uint64_t(255);
+    const uint64_t table_bytes = groups * (n == 1 ? sizeof(uint64_t) : sizeof(uint32_t));
+    const uint64_t tail_off = (table_off + table_bytes + 255) & ~uint64_t(255);
+    std::vector<uint64_t> table(n == 1 ? groups : (groups + 1) / 2);
     for (uint32_t i = 0; i < count; ++i)
-        for (uint32_t g = host[i].group_begin; g < host[i + 1].group_begin; ++g) owner[g] = i;
-    const uint64_t owner_off = scratch;
-    scratch += groups * sizeof(uint32_t);
-    scratch = (scratch + 255) & ~uint64_t(255);
+        for (uint32_t g = host[i].group_begin; g < host[i + 1].group_begin; ++g) {
+            if (n == 1)
+                table[g] = reinterpret_cast<uint64_t>(descs[i].x + static_cast<size_t>(g - host[i].group_begin) * kGroup);
+            else
+                reinterpret_cast<uint32_t *>(table.data())[g] = i;
+        }
+    scratch += tail_off;
     DeviceGuard guard(device);
     if (!guard.ok()) return fail(Q4RDNA_ERR_HIP, "hipSetDevice(%d) failed", device);
     auto plan = std::make_unique<q4rdna_plan>();
@@ -638,17 +646,17 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
         return fail(Q4RDNA_ERR_MEMORY, "plan buffers: %s", hipGetErrorString(e));
     }
     for (uint32_t i = 0; i < count; ++i) {
-        host[i].prep = plan->scratch + prep_off[i];
+        host[i].prep = plan->scratch + static_cast<uint64_t>(host[i].group_begin) * prep_per_group;
         if (host[i].chunks * host[i].streams > 1) {
-            host[i].partial = reinterpret_cast<float *>(plan->scratch + part_off[i]);
-            host[i].counters = reinterpret_cast<uint32_t *>(plan->scratch + cnt_off[i]);
+            host[i].partial = reinterpret_cast<float *>(plan->scratch + tail_off + part_off[i]);
+            host[i].counters = reinterpret_cast<uint32_t *>(plan->scratch + tail_off + cnt_off[i]);
         }
     }
-    plan->owner = reinterpret_cast<uint32_t *>(plan->scratch + owner_off);
+    plan->table = plan->scratch + table_off;
     e = hipMemcpy(plan->descs, host.data(), host.size() * sizeof(q4rdna::PlanDesc), hipMemcpyHostToDevice);
     if (e == hipSuccess && scratch > 0) e = hipMemset(plan->scratch, 0, scratch);
     if (e == hipSuccess && groups > 0)
-        e = hipMemcpy(plan->owner, owner.data(), groups * sizeof(uint32_t), hipMemcpyHostToDevice);
+        e = hipMemcpy(plan->table, table.data(), table_bytes, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemset(plan->sched, 0, 2 * sizeof(uint32_t));
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
@@ -674,8 +682,10 @@ int q4rdna_plan_prepare(q4rdna_plan *plan, void *stream) {
     int rc = plan_check(plan);
     if (rc != Q4RDNA_OK) return rc;
     hipError_t e = plan->batch == 1
-                       ? q4rdna::launch_prep(plan->descs, plan->owner, plan->groups, static_cast<hipStream_t>(stream))
-                       : q4rdna::launch_prep_batch(plan->descs, plan->owner, plan->groups, plan->batch,
+                       ? q4rdna::launch_prep(reinterpret_cast<const float *const *>(plan->table), plan->scratch,
+                                             plan->groups, static_cast<hipStream_t>(stream))
+                       : q4rdna::launch_prep_batch(plan->descs, reinterpret_cast<const uint32_t *>(plan->table),
+                                                   plan->groups, plan->batch,
                                                    static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "plan prepare launch");
     return Q4RDNA_OK;
