@@ -436,7 +436,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
-              "(this GEMV path runs on a single GPU; sharding is described in DESIGN.md)", file=sys.stderr)
+              "(this GEMV path runs on a single GPU; it is not sharded across GPUs)", file=sys.stderr)
         return 2
 
     import torch
