@@ -12,6 +12,7 @@ namespace q4rdna {
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Global-address-space views.  Pointers read from a descriptor table are
@@ -21,10 +22,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) const unsigned int *gptr_u32;
 typedef __attribute__((address_space(1))) const u32x2 *gptr_u32x2;
 typedef __attribute__((address_space(1))) const i32x4 *gptr_i32x4;
+typedef __attribute__((address_space(1))) const f32x2 *gptr_f32x2;
 typedef __attribute__((address_space(1))) const f32x4 *gptr_f32x4;
 typedef __attribute__((address_space(1))) const float *gptr_cf32;
 typedef __attribute__((address_space(1))) float *gptr_f32;
 typedef __attribute__((address_space(1))) uint8_t *gptr_u8;
+typedef __attribute__((address_space(1))) i32x4 *gptr_wi32x4;
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
     return __half2float(__ushort_as_half(static_cast<unsigned short>(bits & 0xffffu)));
@@ -34,18 +37,22 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
 // Device-scope (agent) relaxed atomics: on gfx950 these are single sc1
 // loads/stores and a plain atomic add, coherent across the XCDs' L2s without
-// the whole-L2 write-back/invalidate that release/acquire fences emit.
+// the whole-L2 write-back/invalidate that release/acquire fences emit.  Every
+// pointer passed here is device memory; the global address space keeps them
+// global_* instructions: a flat access also counts against lgkmcnt, so the
+// next wait for an LDS read would wait for the store's acknowledgement too.
+typedef __attribute__((address_space(1))) uint32_t *gptr_au32;
 __device__ __forceinline__ void store_agent(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((gptr_f32)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void store_agent(uint32_t *p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((gptr_au32)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ float load_agent(const float *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load((gptr_cf32)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint32_t add_agent(uint32_t *p, uint32_t v) {
-    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_fetch_add((gptr_au32)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Wait until this wave's stores have completed (visible at device scope for
 // sc1 stores); the memory clobber keeps the compiler from moving memory

@@ -41,88 +41,83 @@ constexpr int kWaves = 4;
 // deeper pipelines measured no faster.
 constexpr int kPlanDepth = 2;
 
-// Position of element k (0..63) of a group in the operand order above:
-// returns the byte index e (0..15) and the k-slot.
-__device__ __forceinline__ int operand_index(int k, int &kslot) {
-    const int i = k >> 1, h = k & 1;
-    kslot = i & 3;
-    const int c = i >> 2;
-    return 4 * (2 * (c >> 2) + h) + (c & 3);
-}
-
-// Activation digits.  A wave converts four 64-element groups, 16 lanes per
-// group and four elements per lane: block exponent E of the group's max |x|
-// (frexp), three balanced int8 digits per element in operand order, and the
-// group factor 2^(E-26); a non-finite element makes the factor NaN.
-// Layout per group (kPrepBytes = 272): byte (kslot*4 + digit)*16 + e for
-// digit 0..2, digit slot 3 zero; float factor at 256; zero padding to 272.
-// A lane's four elements k = 4q..4q+3 (q = lane % 16) land, for each k-slot
-// and digit, in two byte pairs (e, e+1) and (e+4, e+5).
-template <typename OutPtr>
-__device__ __forceinline__ void prep_group_quarter(const f32x4 xv, int q, bool valid_group, OutPtr out,
-                                                   bool &bad, int &e_out) {
-    const float xs[4] = {xv[0], xv[1], xv[2], xv[3]};
+// Activation digits.  One lane takes one k-slot of a 64-element group: the
+// 16 elements 2*(kslot + 4c) + h (c = 0..7, h = 0..1), i.e. its operand bytes
+// e = 8*(c/4) + 4*h + c%4.  The group's block exponent E (frexp of max |x|)
+// and non-finite flag are reduced over the four lanes holding its k-slots
+// (lanes 4p .. 4p+3 of the wave); each element becomes A = rint(x*2^(22-E)),
+// split into three balanced int8 digits.  The lane writes the three digit
+// rows and a zero row as 64 contiguous bytes (row d at out + 16*d): the
+// single-vector and batched layouts both keep a k-slot's rows together.
+// `have` false: the lane reads nothing and writes nothing (its group lies
+// past the end); its three sibling lanes are in the same state.
+__device__ __forceinline__ void prep_kslot(const float *x, int kslot, bool have, gptr_u8 out, bool &bad, int &e_out) {
+    float xs[16];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        f32x2 v = {0.0f, 0.0f};
+        if (have) v = *(gptr_f32x2)(x + 2 * (kslot + 4 * c));
+        xs[8 * (c >> 2) + (c & 3)] = v[0];
+        xs[8 * (c >> 2) + 4 + (c & 3)] = v[1];
+    }
     float m = 0.0f;
     bool nonfinite = false;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 16; ++i) {
         nonfinite |= !isfinite(xs[i]);
         m = fmaxf(m, isfinite(xs[i]) ? fabsf(xs[i]) : 0.0f);
     }
-    // Max over the group's 16 lanes (xor within aligned 16-lane blocks).
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = fmaxf(m, __shfl_xor(m, 1));
+    m = fmaxf(m, __shfl_xor(m, 2));
     int nf = nonfinite ? 1 : 0;
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) nf |= __shfl_xor(nf, o);
+    nf |= __shfl_xor(nf, 1);
+    nf |= __shfl_xor(nf, 2);
     int e = 0;
     if (m > 0.0f) (void)frexpf(m, &e);
     if (e < -100) e = -100;
     bad = nf != 0;
     e_out = e;
-    int dig[4][3];
+    if (!have) return;
+    uint32_t row[3][4] = {};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 16; ++i) {
         const int A = isfinite(xs[i]) ? static_cast<int>(rintf(ldexpf(xs[i], 22 - e))) : 0;
         const int a0 = ((A + 128) & 255) - 128;
         const int A1 = (A - a0) >> 8;
         const int a1 = ((A1 + 128) & 255) - 128;
-        dig[i][0] = a0;
-        dig[i][1] = a1;
-        dig[i][2] = (A1 - a1) >> 8;
+        const int a2 = (A1 - a1) >> 8;
+        const int sh = 8 * (i & 3);
+        row[0][i >> 2] |= (static_cast<uint32_t>(a0) & 255u) << sh;
+        row[1][i >> 2] |= (static_cast<uint32_t>(a1) & 255u) << sh;
+        row[2][i >> 2] |= (static_cast<uint32_t>(a2) & 255u) << sh;
     }
-    if (!valid_group) return;
-    // Elements 4q + i: k-pair 2q + (i >> 1), half i & 1.  For k-pair p:
-    // kslot = p & 3, c = p >> 2, e = 4*(2*(c >> 2) + half) + (c & 3).
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int k = 4 * q + i;
-        int kslot;
-        const int idx = operand_index(k, kslot);
-#pragma unroll
-        for (int dgt = 0; dgt < 3; ++dgt) out[(kslot * 4 + dgt) * 16 + idx] = static_cast<uint8_t>(dig[i][dgt]);
-        out[(kslot * 4 + 3) * 16 + idx] = 0;
+    for (int d = 0; d < 3; ++d) {
+        const i32x4 v = {static_cast<int>(row[d][0]), static_cast<int>(row[d][1]), static_cast<int>(row[d][2]),
+                         static_cast<int>(row[d][3])};
+        *(gptr_wi32x4)(out + 16 * d) = v;
     }
+    const i32x4 zero = {0, 0, 0, 0};
+    *(gptr_wi32x4)(out + 48) = zero;
 }
 
-// group_x[g] = address of global group g's 64 activations (built by the
-// host); the digits go to prep + g * kPrepBytes.
+// Single-vector layout per group (kPrepBytes = 272): byte (kslot*4 + d)*16 + e
+// for digit d (d = 3 zero), the float factor 2^(E-26) at 256 (NaN for a
+// non-finite group).  Lane 4p + kslot of a wave converts k-slot kslot of the
+// wave's group p (16 groups per wave); group_x[g] is the address of global
+// group g's 64 activations (built by the host); its digits go to
+// prep + g * kPrepBytes.
 __global__ __launch_bounds__(256) void prep_kernel(const float *const *__restrict__ group_x,
                                                    uint8_t *__restrict__ prep, uint32_t total_groups) {
-    const int lane = threadIdx.x & 63, q = lane & 15;
-    const uint32_t gid = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+    const int lane = threadIdx.x & 63, kslot = lane & 3;
+    const uint32_t gid = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + (lane >> 2);
     const bool valid = gid < total_groups;
-    const uint32_t gq = valid ? gid : total_groups - 1;
-    const float *x = group_x[gq];
-    const f32x4 xv = *(gptr_f32x4)(x + 4 * q);
-    gptr_u8 out = (gptr_u8)(prep + static_cast<size_t>(gq) * kPrepBytes);
+    const float *x = valid ? group_x[gid] : nullptr;
+    gptr_u8 out = (gptr_u8)(prep + static_cast<size_t>(valid ? gid : 0) * kPrepBytes);
     bool bad;
     int e;
-    prep_group_quarter(xv, q, valid, out, bad, e);
-    if (valid && q < 4) {
-        const float f = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 26);
-        *(gptr_f32)(out + 256 + 4 * q) = q == 0 ? f : 0.0f;
-    }
+    prep_kslot(x, kslot, valid, out + 64 * kslot, bad, e);
+    if (valid && kslot == 0) *(gptr_f32)(out + 256) = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 26);
 }
 
 // 4x4 byte transpose: d[c] holds k-pair c for rows 0..3 (one byte each);
@@ -300,7 +295,7 @@ __device__ __forceinline__ void finish_item(SH &sh, const ItemOut &o, const floa
     if (o.per == 1) {
         if (mine) {
             if (o.add != nullptr) v += ((gptr_cf32)o.add)[row];
-            ((gptr_f32)o.y)[row] = v;
+            __builtin_nontemporal_store(v, (gptr_f32)o.y + row);
         }
         return;
     }
@@ -320,7 +315,7 @@ __device__ __forceinline__ void finish_item(SH &sh, const ItemOut &o, const floa
             for (uint32_t k = 1; k < o.chunks; ++k) g += load_agent(&gp[static_cast<size_t>(k) * o.rows + row]);
             u *= silu(g);
         }
-        ((gptr_f32)o.y)[row] = u;
+        __builtin_nontemporal_store(u, (gptr_f32)o.y + row);
     }
     if (threadIdx.x == 0) store_agent(&o.counters[o.block], 0u);
 }
@@ -458,63 +453,26 @@ __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ 
 constexpr int kBatchRows = 256;
 constexpr uint32_t kBatchQuadBytes = 1040;
 
-// One 16-lane quarter of a wave converts one (group, vector): digits at
-// `quad` + kslot*256 + (4*slot + d)*16 + e and the factor at quad + 1024 + 4*slot.
-template <typename OutPtr>
-__device__ __forceinline__ void prep_batch_quarter(const f32x4 xv, int q, bool valid, OutPtr quad, int slot) {
-    const float xs[4] = {xv[0], xv[1], xv[2], xv[3]};
-    float m = 0.0f;
-    bool nonfinite = false;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        nonfinite |= !isfinite(xs[i]);
-        m = fmaxf(m, isfinite(xs[i]) ? fabsf(xs[i]) : 0.0f);
-    }
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    int nf = nonfinite ? 1 : 0;
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) nf |= __shfl_xor(nf, o);
-    int e = 0;
-    if (m > 0.0f) (void)frexpf(m, &e);
-    if (e < -100) e = -100;
-    if (!valid) return;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int A = isfinite(xs[i]) ? static_cast<int>(rintf(ldexpf(xs[i], 22 - e))) : 0;
-        const int a0 = ((A + 128) & 255) - 128;
-        const int A1 = (A - a0) >> 8;
-        const int a1 = ((A1 + 128) & 255) - 128;
-        const int a2 = (A1 - a1) >> 8;
-        int kslot;
-        const int idx = operand_index(4 * q + i, kslot);
-        OutPtr row = quad + kslot * 256 + (4 * slot) * 16 + idx;
-        row[0] = static_cast<uint8_t>(a0);
-        row[16] = static_cast<uint8_t>(a1);
-        row[32] = static_cast<uint8_t>(a2);
-        row[48] = 0;
-    }
-    if (q == 0) {
-        const float f = nf ? __builtin_nanf("") : ldexpf(1.0f, e - 26);
-        *(gptr_f32)(quad + 1024 + 4 * slot) = f;
-    }
-}
-
-// One quarter wave per (group, vector): pairs p = g * n + vector.
+// Lane 4p + kslot of a wave converts k-slot kslot of the wave's (group,
+// vector) pair p (16 pairs per wave, pair = g * n + vector).  Slots past n in
+// the last quad are never written and stay zero from the plan's creation.
 __global__ __launch_bounds__(256) void prep_batch_kernel(const PlanDesc *__restrict__ descs,
                                                          const uint32_t *__restrict__ owner, uint32_t total_groups,
                                                          uint32_t n) {
-    const int lane = threadIdx.x & 63, q = lane & 15;
-    const uint32_t pair = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+    const int lane = threadIdx.x & 63, kslot = lane & 3;
+    const uint32_t pair = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + (lane >> 2);
     const bool valid = pair < total_groups * n;
-    const uint32_t pq = valid ? pair : total_groups * n - 1;
+    const uint32_t pq = valid ? pair : 0;
     const uint32_t gid = pq / n, vec = pq - gid * n;
     const PlanDesc &d = descs[owner[gid]];
     const uint32_t g = gid - d.group_begin;
-    const uint32_t quads = (n + 3) / 4;
-    const f32x4 xv = *(gptr_f32x4)(d.x + static_cast<size_t>(vec) * d.cols + static_cast<size_t>(g) * kGroup + 4 * q);
+    const uint32_t quads = (n + 3) / 4, slot = vec & 3;
+    const float *x = d.x + static_cast<size_t>(vec) * d.cols + static_cast<size_t>(g) * kGroup;
     gptr_u8 quad = (gptr_u8)(d.prep + (static_cast<size_t>(g) * quads + vec / 4) * kBatchQuadBytes);
-    prep_batch_quarter(xv, q, valid, quad, static_cast<int>(vec & 3));
+    bool bad;
+    int e;
+    prep_kslot(x, kslot, valid, quad + 256 * kslot + 64 * slot, bad, e);
+    if (valid && kslot == 0) *(gptr_f32)(quad + 1024 + 4 * slot) = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 26);
 }
 
 constexpr int kBatchWaves = 4;  // eight waves per workgroup measured slower
@@ -661,7 +619,7 @@ __device__ __forceinline__ void run_batch_item(BatchShared<NQ> &sh, const PlanDe
             for (uint32_t vec = 0; vec < nvec; ++vec) {
                 float v = total(vec, r);
                 if (d.add != nullptr) v += ((gptr_cf32)d.add)[vec * M + row];
-                ((gptr_f32)d.y)[vec * M + row] = v;
+                __builtin_nontemporal_store(v, (gptr_f32)d.y + vec * M + row);
             }
         }
         return;
@@ -690,7 +648,7 @@ __device__ __forceinline__ void run_batch_item(BatchShared<NQ> &sh, const PlanDe
                     g += load_agent(&d.partial[(static_cast<size_t>(d.chunks + k) * nvec + vec) * M + row]);
                 u *= silu(g);
             }
-            ((gptr_f32)d.y)[vec * M + row] = u;
+            __builtin_nontemporal_store(u, (gptr_f32)d.y + vec * M + row);
         }
     }
     if (threadIdx.x == 0) store_agent(&d.counters[block], 0u);
@@ -724,7 +682,7 @@ __global__ __launch_bounds__(64 * kBatchWaves) void plan_batch_kernel(const Plan
 
 hipError_t launch_prep(const float *const *group_x, uint8_t *prep, uint32_t groups, hipStream_t stream) {
     if (groups == 0) return hipSuccess;
-    hipLaunchKernelGGL(prep_kernel, dim3((groups + 15) / 16), dim3(256), 0, stream, group_x, prep, groups);
+    hipLaunchKernelGGL(prep_kernel, dim3((groups + 63) / 64), dim3(256), 0, stream, group_x, prep, groups);
     return hipGetLastError();
 }
 
@@ -737,7 +695,7 @@ hipError_t launch_plan(const PlanDesc *descs, uint32_t items, uint32_t workgroup
 hipError_t launch_prep_batch(const PlanDesc *descs, const uint32_t *owner, uint32_t groups, uint32_t n,
                              hipStream_t stream) {
     if (groups == 0) return hipSuccess;
-    hipLaunchKernelGGL(prep_batch_kernel, dim3((groups * n + 15) / 16), dim3(256), 0, stream, descs, owner, groups, n);
+    hipLaunchKernelGGL(prep_batch_kernel, dim3((groups * n + 63) / 64), dim3(256), 0, stream, descs, owner, groups, n);
     return hipGetLastError();
 }
 

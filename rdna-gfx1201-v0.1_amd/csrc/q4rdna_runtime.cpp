@@ -599,7 +599,7 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
         scratch = (scratch + 255) & ~uint64_t(255);
         items += static_cast<uint64_t>(blocks) * chunks * streams;
         groups += g;
-        if (items > 0xffffffffull || groups > 0xffffffffull) return fail(Q4RDNA_ERR_ARGUMENT, "plan too large");
+        if (items > 0xffffffffull || groups * n > 0xffffffffull) return fail(Q4RDNA_ERR_ARGUMENT, "plan too large");
     }
     host[count] = q4rdna::PlanDesc{};
     host[count].item_begin = static_cast<uint32_t>(items);
