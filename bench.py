@@ -272,30 +272,50 @@ def outlier_weights(rows: int, cols: int, seed: int, frac: float = 0.01, factor:
     return w
 
 
+def time_launches(launch, count: int, replays: int = 5) -> float:
+    """Mean us per launch of launch(0) .. launch(count - 1), captured once
+    into a HIP graph and replayed, so the host's per-call launch overhead
+    (ctypes, stream lookup: several us) is not what gets timed."""
+    import torch
+    # The split-K workspace belongs to a stream: an eager call on the capture
+    # stream allocates it before the capture starts.
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for i in range(min(count, 3)):
+            launch(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(count):
+            launch(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(replays):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    del graph
+    return a.elapsed_time(b) * 1000.0 / (replays * count)
+
+
 def time_tensor(rows: int, cols: int, split: int, seed: int, reps: int = 40):
     """Mean us of one q4rdna_mul_mat_ex launch (split 0 = the shape policy),
-    back to back, rotating over >= 1 GiB of weight copies so the 256 MB
-    Infinity Cache cannot serve them."""
+    back to back from a HIP graph, rotating over >= 1 GiB of weight copies
+    so the 256 MB Infinity Cache cannot serve them."""
     import torch
     from q4rdna import api
     size = api.packed_size(rows, cols)
-    copies = max(4, min(128, (1 << 30) // size + 1))
+    copies = max(4, min(512, (1 << 30) // size + 1))
     tiles = api.pack(outlier_weights(rows, cols, seed))
     buf = tiles.unsqueeze(0).repeat(copies, 1)
     ws = [api.QWeight.from_tiles(buf[c], rows, cols) for c in range(copies)]
     x = torch.randn(cols, device="cuda")
     y = torch.empty(rows, device="cuda")
-    for i in range(3):
-        api.mul_mat_ex(ws[i % copies], x, y, split_k=split)
-    torch.cuda.synchronize()
-    a = torch.cuda.Event(enable_timing=True)
-    b = torch.cuda.Event(enable_timing=True)
-    a.record()
-    for i in range(reps):
-        api.mul_mat_ex(ws[i % copies], x, y, split_k=split)
-    b.record()
-    torch.cuda.synchronize()
-    return a.elapsed_time(b) * 1000.0 / reps, copies
+    us = time_launches(lambda i: api.mul_mat_ex(ws[i % copies], x, y, split_k=split), max(reps, copies))
+    return us, copies
 
 
 def batch_table(tensors, batches, steps: int, warmup: int, seed: int):
@@ -359,11 +379,14 @@ def tensor_table(seed: int):
     import torch
     for name, r, c, kind in [("gate+up SwiGLU", 12288, 4096, "glu"), ("o_proj + add", 4096, 4096, "add")]:
         size = api.packed_size(r, c)
-        copies = max(4, min(128, (1 << 30) // (2 * size) + 1))
+        streams = 2 if kind == "glu" else 1
+        copies = max(4, min(512, (1 << 30) // (streams * size) + 1))
         up = api.pack(outlier_weights(r, c, seed + 1))
-        gt = api.pack(outlier_weights(r, c, seed + 2))
         ups = [api.QWeight.from_tiles(t, r, c) for t in up.unsqueeze(0).repeat(copies, 1)]
-        gates = [api.QWeight.from_tiles(t, r, c) for t in gt.unsqueeze(0).repeat(copies, 1)]
+        gates = gt = None
+        if kind == "glu":
+            gt = api.pack(outlier_weights(r, c, seed + 2))
+            gates = [api.QWeight.from_tiles(t, r, c) for t in gt.unsqueeze(0).repeat(copies, 1)]
         x = torch.randn(c, device="cuda")
         add = torch.randn(r, device="cuda")
         y = torch.empty(r, device="cuda")
@@ -373,17 +396,7 @@ def tensor_table(seed: int):
                 api.mul_mat_glu(ups[i % copies], gates[i % copies], x, y)
             else:
                 api.mul_mat_add(ups[i % copies], x, add, y)
-        for i in range(3):
-            launch(i)
-        torch.cuda.synchronize()
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record()
-        for i in range(40):
-            launch(i)
-        b.record()
-        torch.cuda.synchronize()
-        us = a.elapsed_time(b) * 1000 / 40
+        us = time_launches(launch, max(40, copies))
         nbytes = algorithmic_bytes(r, c) + (17 * r * c // 32 if kind == "glu" else 4 * r)
         rows_out.append(dict(kind="fused", name=name, rows=r, cols=c, us=round(us, 2),
                              gb_per_s=round(nbytes / us / 1e3, 1), copies=copies))
@@ -405,7 +418,7 @@ def tensor_table(seed: int):
     plan.close()
     del items, copies, tiles
     for r, c in [(4096, 12288), (2048, 28672)]:
-        for split in (1, 2, 3, 4, 6, 8, 12, 16, 24, 32):
+        for split in (1, 2, 3, 4, 6, 8, 12, 14, 16, 24, 32):
             us, copies = time_tensor(r, c, split, seed + split)
             gbs = algorithmic_bytes(r, c) / us / 1e3
             rows_out.append(dict(kind="split_sweep", rows=r, cols=c, split=split, us=round(us, 2),

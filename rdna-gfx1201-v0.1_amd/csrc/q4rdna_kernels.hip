@@ -141,6 +141,48 @@ __device__ __forceinline__ void compute_batch(const TileRegs (&t)[BATCH], const 
     }
 }
 
+// Sum the lanes' row partials of a row tile over the workgroup: xor-8/16/32
+// shuffles within each wave, then the four waves in wave order through LDS.
+// Threads 0..31 return the row sums (out, gout).
+template <bool GATE>
+__device__ __forceinline__ void reduce_rows(Shared &sh, float (&acc)[4], float (&gacc)[4], float &out, float &gout) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = lane & 7, a = lane >> 3;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        acc[r] += __shfl_xor(acc[r], 8);
+        acc[r] += __shfl_xor(acc[r], 16);
+        acc[r] += __shfl_xor(acc[r], 32);
+        if constexpr (GATE) {
+            gacc[r] += __shfl_xor(gacc[r], 8);
+            gacc[r] += __shfl_xor(gacc[r], 16);
+            gacc[r] += __shfl_xor(gacc[r], 32);
+        }
+    }
+    if (a == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sh.red[0][wave][4 * q + r] = acc[r];
+            if constexpr (GATE) sh.red[1][wave][4 * q + r] = gacc[r];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 32) {
+        const int t = threadIdx.x;
+        float v = sh.red[0][0][t];
+#pragma unroll
+        for (int wv = 1; wv < kWaves; ++wv) v += sh.red[0][wv][t];
+        out = v;
+        if constexpr (GATE) {
+            float gv = sh.red[1][0][t];
+#pragma unroll
+            for (int wv = 1; wv < kWaves; ++wv) gv += sh.red[1][wv][t];
+            gout = gv;
+        }
+    }
+}
+
+
 // Partial dot products of row tile `rt` over groups [g_begin, g_end), summed
 // over the workgroup.  Threads 0..31 return the row partials (out, gout).
 // Wave w takes groups g_begin + w, + 4, ...; each wave keeps the next batch
@@ -181,38 +223,81 @@ __device__ __forceinline__ void tile_row_partial(Shared &sh, const uint8_t *__re
         }
     }
 
+    reduce_rows<GATE>(sh, acc, gacc, out, gout);
+}
+
+// The same partial sums for a short K range: at most 4*T groups (T <= 16
+// tiles per wave, so the range fits one LDS stage).  Every load is issued
+// before the first wait: the activations first, so staging them waits for x
+// only, then all of the wave's tiles (groups wave + 4i, clamped to the range;
+// a clamped duplicate is loaded but never used).  The tiles then arrive in
+// one overlapped window instead of one batch after another.
+template <bool GATE, int T>
+__device__ __forceinline__ void tile_row_partial_short(Shared &sh, const uint8_t *__restrict__ w,
+                                                       const uint8_t *__restrict__ gw,
+                                                       const float *__restrict__ x, uint32_t cols, uint32_t rt,
+                                                       uint32_t g_begin, uint32_t g_end, float &out, float &gout) {
+    static_assert(4 * T <= kStageGroups, "the range fits one stage");
+    const uint32_t groups = cols / kGroup;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = lane & 7, a = lane >> 3;
+    const int ng = static_cast<int>(g_end - g_begin);
+    const size_t first = (static_cast<size_t>(rt) * groups + g_begin) * kTileBytes;
+    const uint8_t *wt = w + first;
+    const uint8_t *gt = GATE ? gw + first : nullptr;
+
+    // Thread t stages x items (group t/8 + 32m, lane slot t%8), m < XI.
+    constexpr int XI = (4 * T * 8 + kThreads - 1) / kThreads;
+    const int xa = threadIdx.x & 7;
+    float l[XI][4], h[XI][4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        acc[r] += __shfl_xor(acc[r], 8);
-        acc[r] += __shfl_xor(acc[r], 16);
-        acc[r] += __shfl_xor(acc[r], 32);
-        if constexpr (GATE) {
-            gacc[r] += __shfl_xor(gacc[r], 8);
-            gacc[r] += __shfl_xor(gacc[r], 16);
-            gacc[r] += __shfl_xor(gacc[r], 32);
+    for (int m = 0; m < XI; ++m) {
+        const int xg = (threadIdx.x >> 3) + 32 * m;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) l[m][j] = h[m][j] = 0.f;
+        if (xg < ng) {
+            const gptr_cf32 b = (gptr_cf32)x + (static_cast<size_t>(g_begin) + xg) * kGroup + 2 * xa;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                l[m][j] = b[16 * j];
+                h[m][j] = b[16 * j + 1];
+            }
         }
     }
-    if (a == 0) {
+    __builtin_amdgcn_sched_barrier(0);
+    TileRegs t[T], u[T];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            sh.red[0][wave][4 * q + r] = acc[r];
-            if constexpr (GATE) sh.red[1][wave][4 * q + r] = gacc[r];
+    for (int i = 0; i < T; ++i) {
+        const int gg = min(wave + kWaves * i, ng - 1);
+        t[i] = load_tile(wt + static_cast<size_t>(gg) * kTileBytes, q, a);
+        if constexpr (GATE) u[i] = load_tile(gt + static_cast<size_t>(gg) * kTileBytes, q, a);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int m = 0; m < XI; ++m) {
+        const int xg = (threadIdx.x >> 3) + 32 * m;
+        if (xg < ng) {
+            const float *lm = l[m], *hm = h[m];
+            sh.st.v[xg][xa] = make_float4(lm[0], lm[1], lm[2], lm[3]);
+            sh.st.v[xg][8 + xa] = make_float4(hm[0] * 0.0625f, hm[1] * 0.0625f, hm[2] * 0.0625f, hm[3] * 0.0625f);
+            sh.st.c[xg][xa] = -8.0f * (((((((lm[0] + hm[0]) + lm[1]) + hm[1]) + lm[2]) + hm[2]) + lm[3]) + hm[3]);
         }
     }
     __syncthreads();
-    if (threadIdx.x < 32) {
-        const int t = threadIdx.x;
-        float v = sh.red[0][0][t];
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float gacc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int wv = 1; wv < kWaves; ++wv) v += sh.red[0][wv][t];
-        out = v;
-        if constexpr (GATE) {
-            float gv = sh.red[1][0][t];
-#pragma unroll
-            for (int wv = 1; wv < kWaves; ++wv) gv += sh.red[1][wv][t];
-            gout = gv;
+    for (int i = 0; i < T; ++i) {
+        const int gg = wave + kWaves * i;
+        if (gg < ng) {
+            const float4 xl = sh.st.v[gg][a];
+            const float4 xh = sh.st.v[gg][8 + a];
+            const float c = sh.st.c[gg][a];
+            tile_fma(t[i], xl, xh, c, acc);
+            if constexpr (GATE) tile_fma(u[i], xl, xh, c, gacc);
         }
     }
+    reduce_rows<GATE>(sh, acc, gacc, out, gout);
 }
 
 template <bool GATE, bool ADD>
@@ -224,7 +309,7 @@ __device__ __forceinline__ float epilogue(float v, float gv, const float *__rest
 
 // Workgroup b covers row tile rt and K chunk s of `split`, remapped so the
 // chunks of one row tile run on one XCD.
-template <bool GATE, bool ADD>
+template <bool GATE, bool ADD, int T>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args) {
     __shared__ Shared sh;
     const uint32_t groups = args.cols / kGroup;
@@ -234,7 +319,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args) {
     const uint32_t g_begin = static_cast<uint32_t>((static_cast<uint64_t>(s) * groups) / split);
     const uint32_t g_end = static_cast<uint32_t>((static_cast<uint64_t>(s + 1) * groups) / split);
     float v = 0.f, gv = 0.f;
-    tile_row_partial<GATE>(sh, args.w, args.gate, args.x, args.cols, rt, g_begin, g_end, v, gv);
+    if constexpr (T == 0)
+        tile_row_partial<GATE>(sh, args.w, args.gate, args.x, args.cols, rt, g_begin, g_end, v, gv);
+    else
+        tile_row_partial_short<GATE, T>(sh, args.w, args.gate, args.x, args.cols, rt, g_begin, g_end, v, gv);
     const uint32_t row = rt * kTileRows + (threadIdx.x & 31);
     if (split == 1) {
         if (threadIdx.x < 32) args.y[row] = epilogue<GATE, ADD>(v, gv, args.add, row);
@@ -526,10 +614,27 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(const float *__restrict_
 
 #pragma clang fp contract(on)
 
+// T = tiles per wave of the short-range kernel (the workgroup's K chunk is at
+// most 4*T groups), or 0 for the pipelined loop over longer chunks.  The
+// host keeps split <= groups, so every chunk holds at least one group.
 template <bool GATE, bool ADD>
 hipError_t launch_gemv_t(const GemvArgs &args, hipStream_t stream) {
     const uint32_t blocks = (args.rows / kTileRows) * args.split;
-    hipLaunchKernelGGL((gemv_kernel<GATE, ADD>), dim3(blocks), dim3(kThreads), 0, stream, args);
+    const uint32_t groups = args.cols / kGroup;
+    const uint32_t per_wave = ((groups + args.split - 1) / args.split + kWaves - 1) / kWaves;
+    const dim3 grid(blocks), block(kThreads);
+    if (per_wave <= 1)
+        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 1>), grid, block, 0, stream, args);
+    else if (per_wave <= 2)
+        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 2>), grid, block, 0, stream, args);
+    else if (per_wave <= 4)
+        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 4>), grid, block, 0, stream, args);
+    else if (per_wave <= 8)
+        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 8>), grid, block, 0, stream, args);
+    else if (per_wave <= 16)
+        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 16>), grid, block, 0, stream, args);
+    else
+        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 0>), grid, block, 0, stream, args);
     return hipGetLastError();
 }
 
