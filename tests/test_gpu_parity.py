@@ -197,6 +197,41 @@ def test_mul_mat_glu_swiglu(cuda, rows, cols):
     assert (np.abs(yh - want) <= 1e-5 * bound_abs + 1e-30).all()
 
 
+@pytest.mark.parametrize("kind", ["plain", "add", "glu", "glu+add"])
+def test_every_kernel_path_matches_oracle(cuda, kind):
+    """Each per-tensor kernel path: K chunks of at most 64 groups (4, 8, 16,
+    32, 64 and 43 groups: 1, 2, 4, 8 and 16 tiles per wave, every load issued
+    before the first wait) and longer chunks (the pipelined loop), each with
+    the plain, add, SwiGLU and SwiGLU-after-add epilogues."""
+    rows = 96
+    for cols, splits in [(4096, (16, 8, 4, 2, 1)), (8192, (1, 3))]:
+        up_t = random_tiles(rows, cols, 31 + cols)
+        x = O.gaussian_x(cols, 32 + cols)
+        up = api.QWeight.from_tiles(dev_u8(up_t), rows, cols)
+        u64, ua = O.gemv_f64(up_t, rows, cols, x)
+        gate = add = None
+        want, bound = u64, ua
+        if "add" in kind:
+            add_np = O.gaussian_x(rows, 33 + cols)
+            add = dev_f32(add_np)
+            want, bound = u64 + add_np, ua + np.abs(add_np)
+        if "glu" in kind:
+            gate_t = random_tiles(rows, cols, 34 + cols)
+            gate = api.QWeight.from_tiles(dev_u8(gate_t), rows, cols)
+            g64, ga = O.gemv_f64(gate_t, rows, cols, x)
+            bound = bound * np.abs(O.silu(g64)) + np.abs(want) * 1.1 * ga
+            want = want * O.silu(g64)
+        rms = np.sqrt(np.mean(want ** 2))
+        for split in splits:
+            y = torch.full((rows,), float("nan"), device="cuda")
+            assert api.mul_mat_ex(up, dev_f32(x), y, gate=gate, add=add, split_k=split)
+            torch.cuda.synchronize()
+            yh = y.cpu().numpy().astype(np.float64)
+            rel = np.abs(yh - want) / np.maximum(np.abs(want), 0.01 * rms)
+            assert rel.max() <= GATE_TOL, (kind, cols, split, rel.max())
+            assert (np.abs(yh - want) <= 1e-5 * bound + 1e-30).all(), (kind, cols, split)
+
+
 def test_not_applicable_leaves_output_untouched(cuda):
     rows, cols = 64, 512
     w = api.QWeight.from_tiles(dev_u8(random_tiles(rows, cols, 1)), rows, cols)
