@@ -87,11 +87,16 @@ def time_plan(plan, steps: int, warmup: int, sample_every: int = 8):
     import torch
     stream = torch.cuda.current_stream()
     s = stream.cuda_stream
+    # Events are made before the warmup, so the timed loop starts right after
+    # the synchronize: an idle gap there has measured as ~20 slower steps.
+    sampled = list(range(0, steps, sample_every))
+    ev = {i: [torch.cuda.Event(enable_timing=True) for _ in range(3)] for i in sampled}
+    for e in ev.values():
+        for x in e:
+            x.record(stream)
     for _ in range(warmup):
         plan.launch(s)
     torch.cuda.synchronize()
-    sampled = list(range(0, steps, sample_every))
-    ev = {i: [torch.cuda.Event(enable_timing=True) for _ in range(3)] for i in sampled}
     t0 = time.perf_counter()
     for i in range(steps):
         e = ev.get(i)
@@ -288,10 +293,18 @@ def time_launches(launch, count: int, replays: int = 5) -> float:
     with torch.cuda.graph(graph, stream=stream):
         for i in range(count):
             launch(i)
-    graph.replay()
-    torch.cuda.synchronize()
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    # About 30 ms of untimed replays first: on fresh buffers the first tens of
+    # ms stream measurably slower (151936x4096: 67 us per launch, settling
+    # to 60-61).
+    for _ in range(max(1, int(30.0 / max(a.elapsed_time(b), 1e-3)))):
+        graph.replay()
+    torch.cuda.synchronize()
     a.record()
     for _ in range(replays):
         graph.replay()
@@ -307,6 +320,7 @@ def time_tensor(rows: int, cols: int, split: int, seed: int, reps: int = 40):
     so the 256 MB Infinity Cache cannot serve them."""
     import torch
     from q4rdna import api
+    torch.cuda.empty_cache()
     size = api.packed_size(rows, cols)
     copies = max(4, min(512, (1 << 30) // size + 1))
     tiles = api.pack(outlier_weights(rows, cols, seed))
@@ -378,6 +392,7 @@ def tensor_table(seed: int):
     # the bias add, one launch each.
     import torch
     for name, r, c, kind in [("gate+up SwiGLU", 12288, 4096, "glu"), ("o_proj + add", 4096, 4096, "add")]:
+        torch.cuda.empty_cache()
         size = api.packed_size(r, c)
         streams = 2 if kind == "glu" else 1
         copies = max(4, min(512, (1 << 30) // (streams * size) + 1))

@@ -145,9 +145,7 @@ int q4rdna_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const f
                       const float *add, float *y, const q4rdna_launch_options *options,
                       void *stream);
 
-/* Split-K factor the shape policy picks for rows x columns on `device`, for
- * one weight stream (q4rdna_mul_mat / _add).  A SwiGLU launch reads two
- * streams and picks about twice the split. */
+/* Split-K factor the shape policy picks for rows x columns on `device`. */
 uint32_t q4rdna_policy_split_k(uint32_t rows, uint32_t columns, int device);
 
 /* ---- multi-tensor stack --------------------------------------------------

@@ -26,6 +26,7 @@ struct GemvArgs {
     uint32_t split;
     float *partial;
     uint32_t *counters;
+    uint32_t short_waves;  // 8 or 4: waves per workgroup for K chunks of at most 64 groups
 };
 
 // Device-side descriptor of one GEMV in a multi-tensor plan.  Work items are

@@ -25,8 +25,13 @@
 // and c with two ds_read_b128 and one ds_read_b32 (8 lanes share each
 // address, a broadcast).
 //
+// Workgroups.  A K chunk of at most 64 groups is taken by eight waves (four
+// when the launch has many workgroups per CU) with every load issued before
+// the first wait; longer chunks by four waves that keep two tile batches in
+// flight.
+//
 // Reduction.  Lane partials are summed over a with xor-8/16/32 shuffles, the
-// four waves' results in LDS in wave order, and K chunks split across
+// waves' results in LDS in wave order, and K chunks split across
 // workgroups through a partial buffer summed in chunk order by the last
 // workgroup to arrive, so every result is bit-reproducible run to run.
 #include "q4rdna_device.h"
@@ -34,7 +39,8 @@
 namespace q4rdna {
 namespace {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 4;       // waves of the pipelined loop's workgroup
+constexpr int kShortWaves = 8;  // waves of the short-range kernel's workgroup
 constexpr int kStageGroups = 64;  // groups of x staged in LDS at once
 constexpr int kBatch = 2;         // default tiles per wave per loop trip (x2 in flight)
 
@@ -106,7 +112,7 @@ __device__ __forceinline__ void stage_x(XStage &st, const float *__restrict__ x,
 
 struct Shared {
     XStage st;
-    float red[2][kWaves][32];
+    float red[2][kShortWaves][32];
     uint32_t last;
 };
 
@@ -142,9 +148,9 @@ __device__ __forceinline__ void compute_batch(const TileRegs (&t)[BATCH], const 
 }
 
 // Sum the lanes' row partials of a row tile over the workgroup: xor-8/16/32
-// shuffles within each wave, then the four waves in wave order through LDS.
+// shuffles within each wave, then the W waves in wave order through LDS.
 // Threads 0..31 return the row sums (out, gout).
-template <bool GATE>
+template <bool GATE, int W>
 __device__ __forceinline__ void reduce_rows(Shared &sh, float (&acc)[4], float (&gacc)[4], float &out, float &gout) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int q = lane & 7, a = lane >> 3;
@@ -171,12 +177,12 @@ __device__ __forceinline__ void reduce_rows(Shared &sh, float (&acc)[4], float (
         const int t = threadIdx.x;
         float v = sh.red[0][0][t];
 #pragma unroll
-        for (int wv = 1; wv < kWaves; ++wv) v += sh.red[0][wv][t];
+        for (int wv = 1; wv < W; ++wv) v += sh.red[0][wv][t];
         out = v;
         if constexpr (GATE) {
             float gv = sh.red[1][0][t];
 #pragma unroll
-            for (int wv = 1; wv < kWaves; ++wv) gv += sh.red[1][wv][t];
+            for (int wv = 1; wv < W; ++wv) gv += sh.red[1][wv][t];
             gout = gv;
         }
     }
@@ -223,21 +229,22 @@ __device__ __forceinline__ void tile_row_partial(Shared &sh, const uint8_t *__re
         }
     }
 
-    reduce_rows<GATE>(sh, acc, gacc, out, gout);
+    reduce_rows<GATE, kWaves>(sh, acc, gacc, out, gout);
 }
 
-// The same partial sums for a short K range: at most 4*T groups (T <= 16
-// tiles per wave, so the range fits one LDS stage).  Every load is issued
-// before the first wait: the activations first, so staging them waits for x
-// only, then all of the wave's tiles (groups wave + 4i, clamped to the range;
-// a clamped duplicate is loaded but never used).  The tiles then arrive in
-// one overlapped window instead of one batch after another.
-template <bool GATE, int T>
+// The same partial sums for a short K range, by a workgroup of W waves: at
+// most W*T groups (T tiles per wave; the range fits one LDS stage).  Every
+// load is issued before the first wait: the activations first, so staging
+// them waits for x only, then all of the wave's tiles (groups wave + W*i,
+// clamped to the range; a clamped duplicate is loaded but never used).  The
+// tiles then arrive in one overlapped window instead of one batch after
+// another.
+template <bool GATE, int T, int W>
 __device__ __forceinline__ void tile_row_partial_short(Shared &sh, const uint8_t *__restrict__ w,
                                                        const uint8_t *__restrict__ gw,
                                                        const float *__restrict__ x, uint32_t cols, uint32_t rt,
                                                        uint32_t g_begin, uint32_t g_end, float &out, float &gout) {
-    static_assert(4 * T <= kStageGroups, "the range fits one stage");
+    static_assert(W * T <= kStageGroups && W <= kShortWaves, "the range fits one stage");
     const uint32_t groups = cols / kGroup;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int q = lane & 7, a = lane >> 3;
@@ -246,13 +253,13 @@ __device__ __forceinline__ void tile_row_partial_short(Shared &sh, const uint8_t
     const uint8_t *wt = w + first;
     const uint8_t *gt = GATE ? gw + first : nullptr;
 
-    // Thread t stages x items (group t/8 + 32m, lane slot t%8), m < XI.
-    constexpr int XI = (4 * T * 8 + kThreads - 1) / kThreads;
+    // Thread t stages x items (group t/8 + 8Wm, lane slot t%8), m < XI.
+    constexpr int XI = (T + 7) / 8;
     const int xa = threadIdx.x & 7;
     float l[XI][4], h[XI][4];
 #pragma unroll
     for (int m = 0; m < XI; ++m) {
-        const int xg = (threadIdx.x >> 3) + 32 * m;
+        const int xg = (threadIdx.x >> 3) + 8 * W * m;
 #pragma unroll
         for (int j = 0; j < 4; ++j) l[m][j] = h[m][j] = 0.f;
         if (xg < ng) {
@@ -268,14 +275,14 @@ __device__ __forceinline__ void tile_row_partial_short(Shared &sh, const uint8_t
     TileRegs t[T], u[T];
 #pragma unroll
     for (int i = 0; i < T; ++i) {
-        const int gg = min(wave + kWaves * i, ng - 1);
+        const int gg = min(wave + W * i, ng - 1);
         t[i] = load_tile(wt + static_cast<size_t>(gg) * kTileBytes, q, a);
         if constexpr (GATE) u[i] = load_tile(gt + static_cast<size_t>(gg) * kTileBytes, q, a);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int m = 0; m < XI; ++m) {
-        const int xg = (threadIdx.x >> 3) + 32 * m;
+        const int xg = (threadIdx.x >> 3) + 8 * W * m;
         if (xg < ng) {
             const float *lm = l[m], *hm = h[m];
             sh.st.v[xg][xa] = make_float4(lm[0], lm[1], lm[2], lm[3]);
@@ -288,7 +295,7 @@ __device__ __forceinline__ void tile_row_partial_short(Shared &sh, const uint8_t
     float gacc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < T; ++i) {
-        const int gg = wave + kWaves * i;
+        const int gg = wave + W * i;
         if (gg < ng) {
             const float4 xl = sh.st.v[gg][a];
             const float4 xh = sh.st.v[gg][8 + a];
@@ -297,7 +304,7 @@ __device__ __forceinline__ void tile_row_partial_short(Shared &sh, const uint8_t
             if constexpr (GATE) tile_fma(u[i], xl, xh, c, gacc);
         }
     }
-    reduce_rows<GATE>(sh, acc, gacc, out, gout);
+    reduce_rows<GATE, W>(sh, acc, gacc, out, gout);
 }
 
 template <bool GATE, bool ADD>
@@ -309,8 +316,8 @@ __device__ __forceinline__ float epilogue(float v, float gv, const float *__rest
 
 // Workgroup b covers row tile rt and K chunk s of `split`, remapped so the
 // chunks of one row tile run on one XCD.
-template <bool GATE, bool ADD, int T>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args) {
+template <bool GATE, bool ADD, int T, int W>
+__global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs args) {
     __shared__ Shared sh;
     const uint32_t groups = args.cols / kGroup;
     const uint32_t split = args.split;
@@ -322,7 +329,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args) {
     if constexpr (T == 0)
         tile_row_partial<GATE>(sh, args.w, args.gate, args.x, args.cols, rt, g_begin, g_end, v, gv);
     else
-        tile_row_partial_short<GATE, T>(sh, args.w, args.gate, args.x, args.cols, rt, g_begin, g_end, v, gv);
+        tile_row_partial_short<GATE, T, W>(sh, args.w, args.gate, args.x, args.cols, rt, g_begin, g_end, v, gv);
     const uint32_t row = rt * kTileRows + (threadIdx.x & 31);
     if (split == 1) {
         if (threadIdx.x < 32) args.y[row] = epilogue<GATE, ADD>(v, gv, args.add, row);
@@ -614,28 +621,35 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(const float *__restrict_
 
 #pragma clang fp contract(on)
 
-// T = tiles per wave of the short-range kernel (the workgroup's K chunk is at
-// most 4*T groups), or 0 for the pipelined loop over longer chunks.  The
-// host keeps split <= groups, so every chunk holds at least one group.
-template <bool GATE, bool ADD>
-hipError_t launch_gemv_t(const GemvArgs &args, hipStream_t stream) {
+// K chunks of at most 64 groups run the short-range kernel with W = 8 or 4
+// waves (args.short_waves) and T <= 64 / W tiles per wave; longer chunks the
+// pipelined loop (T = 0) with kWaves waves.  The host keeps split <= groups,
+// so every chunk holds at least one group.
+template <bool GATE, bool ADD, int W>
+hipError_t launch_gemv_w(const GemvArgs &args, hipStream_t stream) {
     const uint32_t blocks = (args.rows / kTileRows) * args.split;
     const uint32_t groups = args.cols / kGroup;
-    const uint32_t per_wave = ((groups + args.split - 1) / args.split + kWaves - 1) / kWaves;
-    const dim3 grid(blocks), block(kThreads);
+    const uint32_t per_wave = ((groups + args.split - 1) / args.split + W - 1) / W;
+    const dim3 grid(blocks), block(64 * W);
     if (per_wave <= 1)
-        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 1>), grid, block, 0, stream, args);
+        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 1, W>), grid, block, 0, stream, args);
     else if (per_wave <= 2)
-        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 2>), grid, block, 0, stream, args);
+        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 2, W>), grid, block, 0, stream, args);
     else if (per_wave <= 4)
-        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 4>), grid, block, 0, stream, args);
+        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 4, W>), grid, block, 0, stream, args);
     else if (per_wave <= 8)
-        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 8>), grid, block, 0, stream, args);
-    else if (per_wave <= 16)
-        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 16>), grid, block, 0, stream, args);
+        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 8, W>), grid, block, 0, stream, args);
+    else if (W == 4 && per_wave <= 16)
+        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 64 / W, W>), grid, block, 0, stream, args);
     else
-        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 0>), grid, block, 0, stream, args);
+        hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 0, kWaves>), grid, dim3(kThreads), 0, stream, args);
     return hipGetLastError();
+}
+
+template <bool GATE, bool ADD>
+hipError_t launch_gemv_t(const GemvArgs &args, hipStream_t stream) {
+    return args.short_waves == kShortWaves ? launch_gemv_w<GATE, ADD, kShortWaves>(args, stream)
+                                           : launch_gemv_w<GATE, ADD, kWaves>(args, stream);
 }
 
 uint32_t grid_for(uint64_t work, uint32_t per_block) {

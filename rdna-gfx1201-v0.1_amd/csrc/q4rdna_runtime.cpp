@@ -210,20 +210,20 @@ bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 
 constexpr uint32_t kMaxSplit = 64;
 
-uint32_t policy_split(uint32_t rows, uint32_t cols, uint32_t streams, int device) {
-    // About 32 groups per workgroup and weight stream (eight tiles per wave,
-    // all in flight at once), then kept between one and six workgroups per
-    // CU: shorter chunks (down to 16 groups) when the row tiles are too few
-    // to fill the chip, longer ones when there are plenty.  Measured on
-    // MI355X (split sweep): 4096x4096 best at 2-4, 1024x4096 at 4,
-    // 12288x4096 at 2 (4 with a SwiGLU gate), 4096x12288 at 6, 2048x28672
-    // at 8-14, 151936x4096 at 1.
+uint32_t policy_split(uint32_t rows, uint32_t cols, int device) {
+    // About 32 groups per workgroup (eight waves of four tiles, all in flight
+    // at once) and at most 8 chunks; more chunks only when the row tiles are
+    // so few that under a quarter of the CUs would get a workgroup, fewer
+    // when there would be more than six workgroups per CU.  Measured on
+    // MI355X (split sweep, with and without a SwiGLU gate): 4096x4096 best at
+    // 2, 1024x4096 at 2-4, 12288x4096 at 2, 4096x12288 at 6, 2048x28672 at
+    // 7-8, 151936x4096 at 1-2.
     const uint32_t tiles = rows / kTileRows;
     const uint32_t groups = cols / kGroup;
     const uint32_t cus = cu_count(device);
-    uint32_t split = (groups * streams + 31) / 32;
-    if (static_cast<uint64_t>(tiles) * split < cus)
-        split = std::min((cus + tiles - 1) / tiles, std::max<uint32_t>(1, groups / 16));
+    uint32_t split = std::min<uint32_t>((groups + 31) / 32, 8);
+    if (static_cast<uint64_t>(tiles) * split * 4 < cus)
+        split = std::min((cus / 4 + tiles - 1) / tiles, std::max<uint32_t>(1, groups / 16));
     if (static_cast<uint64_t>(tiles) * split > 6ull * cus) split = std::max<uint32_t>(1, 6 * cus / tiles);
     split = std::min(split, std::min(groups, kMaxSplit));
     return std::max<uint32_t>(split, 1);
@@ -240,10 +240,15 @@ int launch_one(const q4rdna_weight *w, const uint8_t *gate, const float *x, cons
     args.rows = w->rows;
     args.cols = w->columns;
     const uint32_t groups = w->columns / kGroup;
-    if (split == 0) split = policy_split(w->rows, w->columns, gate != nullptr ? 2u : 1u, w->device);
+    if (split == 0) split = policy_split(w->rows, w->columns, w->device);
     split = std::min(split, groups);
     split = std::min(split, kMaxSplit);
     args.split = std::max<uint32_t>(split, 1);
+    // Eight waves per workgroup while the launch is latency-bound (at most
+    // four workgroups per CU); with more, four waves of up to 16 tiles keep
+    // more bytes in flight per CU (151936x4096: 60 us against 68).
+    const uint64_t workgroups = static_cast<uint64_t>(w->rows / kTileRows) * args.split;
+    args.short_waves = workgroups <= 4ull * cu_count(w->device) ? 8u : 4u;
     if (args.split > 1) {
         Workspace *ws = nullptr;
         const size_t pf = static_cast<size_t>(args.split) * w->rows * (gate ? 2 : 1);
@@ -491,7 +496,7 @@ int q4rdna_scope_allows(const char *scope, const char *name) {
 
 uint32_t q4rdna_policy_split_k(uint32_t rows, uint32_t columns, int device) {
     if (!valid_shape(rows, columns)) return 0;
-    return policy_split(rows, columns, 1, device);
+    return policy_split(rows, columns, device);
 }
 
 int q4rdna_mul_mat(const q4rdna_weight *w, const float *x, int64_t x_ne0, float *y, int64_t y_ne0, void *stream) {

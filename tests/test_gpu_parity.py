@@ -200,9 +200,9 @@ def test_mul_mat_glu_swiglu(cuda, rows, cols):
 @pytest.mark.parametrize("kind", ["plain", "add", "glu", "glu+add"])
 def test_every_kernel_path_matches_oracle(cuda, kind):
     """Each per-tensor kernel path: K chunks of at most 64 groups (4, 8, 16,
-    32, 64 and 43 groups: 1, 2, 4, 8 and 16 tiles per wave, every load issued
-    before the first wait) and longer chunks (the pipelined loop), each with
-    the plain, add, SwiGLU and SwiGLU-after-add epilogues."""
+    32, 64 and 43 groups: 1, 2, 4 and 8 tiles per wave of eight, every load
+    issued before the first wait) and longer chunks (the pipelined loop),
+    each with the plain, add, SwiGLU and SwiGLU-after-add epilogues."""
     rows = 96
     for cols, splits in [(4096, (16, 8, 4, 2, 1)), (8192, (1, 3))]:
         up_t = random_tiles(rows, cols, 31 + cols)
