@@ -376,8 +376,10 @@ def batch_table(tensors, batches, steps: int, warmup: int, seed: int):
 
 def tensor_table(seed: int):
     """Per-tensor figures: the seven projection shapes and lm_head at the
-    shape policy, and the long-K split sweep (S = 1..32) with 1% outlier
-    groups."""
+    shape policy, the projection shapes with N = 2, 4, 8 vectors in one
+    launch, the fused sites, and the long-K split sweep (S = 1..32) with 1%
+    outlier groups."""
+    import torch
     from q4rdna import api
     rows_out = []
     shapes = [("q/o_proj", 4096, 4096), ("k/v_proj", 1024, 4096), ("gate/up_proj", 12288, 4096),
@@ -388,6 +390,24 @@ def tensor_table(seed: int):
         rows_out.append(dict(kind="policy", name=name, rows=r, cols=c, split=api.policy_split_k(r, c), us=round(us, 2),
                              gb_per_s=round(gbs, 1), copies=copies))
         log(f"[tensors] {name} {r}x{c}: {us:.2f} us {gbs:.0f} GB/s")
+    # Small batches in one launch (q4rdna_mul_mat_batch): N activation vectors
+    # against one weight, each tile read once.
+    for name, r, c in shapes[:4]:
+        torch.cuda.empty_cache()
+        size = api.packed_size(r, c)
+        copies = max(4, min(512, (1 << 30) // size + 1))
+        tiles = api.pack(outlier_weights(r, c, seed + 3))
+        buf = tiles.unsqueeze(0).repeat(copies, 1)
+        ws = [api.QWeight.from_tiles(buf[i], r, c) for i in range(copies)]
+        for n in (2, 4, 8):
+            x = torch.randn(n, c, device="cuda")
+            y = torch.empty(n, r, device="cuda")
+            us = time_launches(lambda i: api.mul_mat_batch(ws[i % copies], x, y), max(40, copies))
+            gbs = algorithmic_bytes(r, c, n) / us / 1e3
+            rows_out.append(dict(kind="batched", name=name, rows=r, cols=c, n=n, us=round(us, 2),
+                                 gb_per_s=round(gbs, 1), copies=copies))
+            log(f"[tensors] {name} {r}x{c} N={n}: {us:.2f} us {gbs:.0f} GB/s")
+        del ws, buf, tiles
     # The reference's fused sites: SwiGLU gate/up (two weight streams) and
     # the bias add, one launch each.
     import torch

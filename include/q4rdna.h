@@ -145,6 +145,20 @@ int q4rdna_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const f
                       const float *add, float *y, const q4rdna_launch_options *options,
                       void *stream);
 
+/* n = 1..Q4RDNA_MAX_BATCH activation vectors against one weight in one
+ * launch (no reference counterpart: the reference's hooks decline batches
+ * above 1, source/q4rdna.cu:722,754,777).  x holds n vectors of `columns`
+ * floats back to back, y (and add) n rows of `rows` floats, as ggml's src1
+ * and dst with ne[1] = n, contiguous.  gate (may be NULL) makes it the
+ * SwiGLU site.  options->split_k as in q4rdna_mul_mat_ex (0 = the shape
+ * policy); for n >= 2 it is raised until every K chunk holds at most 32
+ * groups (16 for n > 4).  Each tile is read once for all n vectors; each
+ * vector's result is bit-identical to q4rdna_mul_mat_ex of that vector with
+ * that split where that call runs eight-wave workgroups. */
+int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x, uint32_t n,
+                         const float *add, float *y, const q4rdna_launch_options *options,
+                         void *stream);
+
 /* Split-K factor the shape policy picks for rows x columns on `device`. */
 uint32_t q4rdna_policy_split_k(uint32_t rows, uint32_t columns, int device);
 

@@ -27,6 +27,7 @@ struct GemvArgs {
     float *partial;
     uint32_t *counters;
     uint32_t short_waves;  // 8 or 4: waves per workgroup for K chunks of at most 64 groups
+    uint32_t vectors;      // launch_gemv_multi: activation vectors (x [vectors][cols], y/add [vectors][rows])
 };
 
 // Device-side descriptor of one GEMV in a multi-tensor plan.  Work items are
@@ -58,6 +59,10 @@ constexpr uint32_t kChunkGroups = 64;
 constexpr uint32_t kBlockRows = 64;
 
 hipError_t launch_gemv(const GemvArgs &args, hipStream_t stream);
+// args.vectors = 2..8 activation vectors; every K chunk (args.split of them)
+// must hold at most gemv_multi_stage_groups(args.vectors) groups.
+hipError_t launch_gemv_multi(const GemvArgs &args, hipStream_t stream);
+uint32_t gemv_multi_stage_groups(uint32_t vectors);
 // descs[count] plus a sentinel whose item_begin / group_begin are the totals.
 // The prep launch converts every activation into digits: group g of the
 // plan (global numbering) reads its 64 floats at group_x[g] and writes

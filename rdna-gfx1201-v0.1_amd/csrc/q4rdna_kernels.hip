@@ -359,6 +359,225 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs args) {
     if (threadIdx.x == 0) store_agent(&args.counters[rt], 0u);
 }
 
+// ---- several activation vectors against one weight (n = 2..8) -------------
+//
+// The short-range kernel above with NV vector slots (n <= NV used): x is
+// [n][cols], y and add are [n][rows].  Each tile is loaded and decoded once
+// and applied to every vector, so a launch costs about what one vector does
+// while it is latency-bound.  Every step of a vector's arithmetic and
+// summation is the one-vector kernel's (same x staging, same fma order, same
+// lane, wave and chunk order), so each vector's result is bit-identical to
+// q4rdna_mul_mat_ex of that vector with the same split and eight waves.
+constexpr int kMvWaves = 8;
+
+// Groups one workgroup stages: NV vectors' x fit 37 KB of LDS.
+template <int NV>
+constexpr int mv_stage_groups() { return NV >= 8 ? 16 : 32; }
+
+template <int NV>
+struct MvShared {
+    float4 v[NV][mv_stage_groups<NV>()][16];  // [vector][g][a] even-k x, [..][8 + a] odd-k x / 16
+    float c[NV][mv_stage_groups<NV>()][8];    // -8 * sum of the lane's 8 x values
+    float red[2][NV][kMvWaves][32];
+    uint32_t last;
+};
+
+// The 32 weights of a lane's tile slice as offset-binary floats: wl[j][r] =
+// low nibble + 8 of row 4q + r at k-pair a + 8j, wh[j][r] = 16 * (high + 8).
+__device__ __forceinline__ void decode_tile(const TileRegs &r, float (&wl)[4][4], float (&wh)[4][4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t e = r.d[j] ^ 0x88888888u;
+        uint32_t lo = e & 0x0f0f0f0fu;
+        uint32_t hi = e & 0xf0f0f0f0u;
+        asm("" : "+v"(lo));
+        asm("" : "+v"(hi));
+        wl[j][0] = static_cast<float>(lo & 0xffu);
+        wl[j][1] = static_cast<float>((lo >> 8) & 0xffu);
+        wl[j][2] = static_cast<float>((lo >> 16) & 0xffu);
+        wl[j][3] = static_cast<float>(lo >> 24);
+        wh[j][0] = static_cast<float>(hi & 0xffu);
+        wh[j][1] = static_cast<float>((hi >> 8) & 0xffu);
+        wh[j][2] = static_cast<float>((hi >> 16) & 0xffu);
+        wh[j][3] = static_cast<float>(hi >> 24);
+    }
+}
+
+// acc[r] += scale(row 4q + r) * (c + sum_j wl[j][r] xl[j] + wh[j][r] xh[j]),
+// in tile_fma's order.
+__device__ __forceinline__ void apply_tile(const float (&wl)[4][4], const float (&wh)[4][4], uint32_t s01,
+                                           uint32_t s23, const float4 xl, const float4 xh, const float c,
+                                           float (&acc)[4]) {
+    const float xlv[4] = {xl.x, xl.y, xl.z, xl.w};
+    const float xhv[4] = {xh.x, xh.y, xh.z, xh.w};
+    float p[4] = {c, c, c, c};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p[r] = fmaf(wl[j][r], xlv[j], p[r]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p[r] = fmaf(wh[j][r], xhv[j], p[r]);
+    }
+    acc[0] = fmaf(half_bits_to_float(s01), p[0], acc[0]);
+    acc[1] = fmaf(half_bits_to_float(s01 >> 16), p[1], acc[1]);
+    acc[2] = fmaf(half_bits_to_float(s23), p[2], acc[2]);
+    acc[3] = fmaf(half_bits_to_float(s23 >> 16), p[3], acc[3]);
+}
+
+template <bool GATE, bool ADD, int NV, int T>
+__global__ __launch_bounds__(64 * kMvWaves) void gemv_multi_kernel(GemvArgs args) {
+    constexpr int W = kMvWaves;
+    constexpr int SG = mv_stage_groups<NV>();
+    static_assert(W * T <= SG, "a chunk fits the stage");
+    __shared__ MvShared<NV> sh;
+    const uint32_t groups = args.cols / kGroup;
+    const uint32_t split = args.split;
+    const uint32_t nv = args.vectors;
+    const uint32_t logical = xcd_remap(blockIdx.x, gridDim.x);
+    const uint32_t rt = logical / split, s = logical % split;
+    const uint32_t g_begin = static_cast<uint32_t>((static_cast<uint64_t>(s) * groups) / split);
+    const uint32_t g_end = static_cast<uint32_t>((static_cast<uint64_t>(s + 1) * groups) / split);
+    const int ng = static_cast<int>(g_end - g_begin);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = lane & 7, a = lane >> 3;
+    const size_t first = (static_cast<size_t>(rt) * groups + g_begin) * kTileBytes;
+    const uint8_t *wt = args.w + first;
+    const uint8_t *gt = GATE ? args.gate + first : nullptr;
+
+    // Activations first (item = (vector, group, lane slot), thread t takes
+    // items t + 64W*m), then every tile of the wave, then the x staging.
+    constexpr int XI = (NV * SG * 8 + 64 * W - 1) / (64 * W);
+    float l[XI][4], h[XI][4];
+#pragma unroll
+    for (int m = 0; m < XI; ++m) {
+        const int item = threadIdx.x + 64 * W * m;
+        const int v = item / (SG * 8), xg = (item >> 3) % SG, xa = item & 7;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) l[m][j] = h[m][j] = 0.f;
+        if (v < static_cast<int>(nv) && xg < ng) {
+            const gptr_cf32 b = (gptr_cf32)args.x + static_cast<size_t>(v) * args.cols +
+                                (static_cast<size_t>(g_begin) + xg) * kGroup + 2 * xa;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                l[m][j] = b[16 * j];
+                h[m][j] = b[16 * j + 1];
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    TileRegs t[T], u[T];
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+        const int gg = min(wave + W * i, ng - 1);
+        t[i] = load_tile(wt + static_cast<size_t>(gg) * kTileBytes, q, a);
+        if constexpr (GATE) u[i] = load_tile(gt + static_cast<size_t>(gg) * kTileBytes, q, a);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int m = 0; m < XI; ++m) {
+        const int item = threadIdx.x + 64 * W * m;
+        const int v = item / (SG * 8), xg = (item >> 3) % SG, xa = item & 7;
+        if (v < static_cast<int>(nv) && xg < ng) {
+            const float *lm = l[m], *hm = h[m];
+            sh.v[v][xg][xa] = make_float4(lm[0], lm[1], lm[2], lm[3]);
+            sh.v[v][xg][8 + xa] = make_float4(hm[0] * 0.0625f, hm[1] * 0.0625f, hm[2] * 0.0625f, hm[3] * 0.0625f);
+            sh.c[v][xg][xa] = -8.0f * (((((((lm[0] + hm[0]) + lm[1]) + hm[1]) + lm[2]) + hm[2]) + lm[3]) + hm[3]);
+        }
+    }
+    __syncthreads();
+
+    float acc[NV][4], gacc[NV][4];
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[v][r] = gacc[v][r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+        const int gg = wave + W * i;
+        if (gg < ng) {
+            float wl[4][4], wh[4][4], gl[4][4], gh[4][4];
+            decode_tile(t[i], wl, wh);
+            if constexpr (GATE) decode_tile(u[i], gl, gh);
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                if (v < static_cast<int>(nv)) {
+                    const float4 xl = sh.v[v][gg][a];
+                    const float4 xh = sh.v[v][gg][8 + a];
+                    const float c = sh.c[v][gg][a];
+                    apply_tile(wl, wh, t[i].s01, t[i].s23, xl, xh, c, acc[v]);
+                    if constexpr (GATE) apply_tile(gl, gh, u[i].s01, u[i].s23, xl, xh, c, gacc[v]);
+                }
+            }
+        }
+    }
+
+    // Lanes, then waves in wave order (reduce_rows, per vector).
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            acc[v][r] += __shfl_xor(acc[v][r], 8);
+            acc[v][r] += __shfl_xor(acc[v][r], 16);
+            acc[v][r] += __shfl_xor(acc[v][r], 32);
+            if constexpr (GATE) {
+                gacc[v][r] += __shfl_xor(gacc[v][r], 8);
+                gacc[v][r] += __shfl_xor(gacc[v][r], 16);
+                gacc[v][r] += __shfl_xor(gacc[v][r], 32);
+            }
+        }
+    if (a == 0) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                sh.red[0][v][wave][4 * q + r] = acc[v][r];
+                if constexpr (GATE) sh.red[1][v][wave][4 * q + r] = gacc[v][r];
+            }
+    }
+    __syncthreads();
+    // Thread t < 32*nv finishes row t % 32 of vector t / 32.
+    const uint32_t v = threadIdx.x >> 5, rl = threadIdx.x & 31;
+    const bool mine = v < nv;
+    const uint32_t row = rt * kTileRows + rl;
+    const size_t M = args.rows;
+    float out = 0.f, gout = 0.f;
+    if (mine) {
+        out = sh.red[0][v][0][rl];
+#pragma unroll
+        for (int wv = 1; wv < W; ++wv) out += sh.red[0][v][wv][rl];
+        if constexpr (GATE) {
+            gout = sh.red[1][v][0][rl];
+#pragma unroll
+            for (int wv = 1; wv < W; ++wv) gout += sh.red[1][v][wv][rl];
+        }
+    }
+    if (split == 1) {
+        if (mine) args.y[v * M + row] = epilogue<GATE, ADD>(out, gout, args.add ? args.add + v * M : nullptr, row);
+        return;
+    }
+    // Split K as in gemv_kernel; partials [chunk][vector][rows], gate
+    // partials after the split * n value partials.
+    if (mine) {
+        store_agent(&args.partial[(static_cast<size_t>(s) * nv + v) * M + row], out);
+        if constexpr (GATE) store_agent(&args.partial[(static_cast<size_t>(split + s) * nv + v) * M + row], gout);
+    }
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) sh.last = (add_agent(&args.counters[rt], 1u) == split - 1) ? 1u : 0u;
+    __syncthreads();
+    if (sh.last == 0u) return;
+    if (mine) {
+        float sum = load_agent(&args.partial[static_cast<size_t>(v) * M + row]);
+        float gsum = GATE ? load_agent(&args.partial[(static_cast<size_t>(split) * nv + v) * M + row]) : 0.f;
+        for (uint32_t c = 1; c < split; ++c) {
+            sum += load_agent(&args.partial[(static_cast<size_t>(c) * nv + v) * M + row]);
+            if constexpr (GATE) gsum += load_agent(&args.partial[(static_cast<size_t>(split + c) * nv + v) * M + row]);
+        }
+        args.y[v * M + row] = epilogue<GATE, ADD>(sum, gsum, args.add ? args.add + v * M : nullptr, row);
+    }
+    if (threadIdx.x == 0) store_agent(&args.counters[rt], 0u);
+}
+
 // out[row][k] = fp32(scale) * code, one thread per code byte.
 __global__ __launch_bounds__(kThreads) void dequant_kernel(const uint8_t *__restrict__ w, uint32_t rows,
                                                            uint32_t cols, float *__restrict__ out) {
@@ -652,6 +871,29 @@ hipError_t launch_gemv_t(const GemvArgs &args, hipStream_t stream) {
                                            : launch_gemv_w<GATE, ADD, kWaves>(args, stream);
 }
 
+template <bool GATE, bool ADD, int NV>
+hipError_t launch_multi_nv(const GemvArgs &args, hipStream_t stream) {
+    constexpr int W = kMvWaves;
+    const uint32_t blocks = (args.rows / kTileRows) * args.split;
+    const uint32_t groups = args.cols / kGroup;
+    const uint32_t per_wave = ((groups + args.split - 1) / args.split + W - 1) / W;
+    const dim3 grid(blocks), block(64 * W);
+    if (per_wave <= 1)
+        hipLaunchKernelGGL((gemv_multi_kernel<GATE, ADD, NV, 1>), grid, block, 0, stream, args);
+    else if (per_wave <= 2 || NV >= 8)
+        hipLaunchKernelGGL((gemv_multi_kernel<GATE, ADD, NV, 2>), grid, block, 0, stream, args);
+    else
+        hipLaunchKernelGGL((gemv_multi_kernel<GATE, ADD, NV, (NV >= 8 ? 2 : 4)>), grid, block, 0, stream, args);
+    return hipGetLastError();
+}
+
+template <bool GATE, bool ADD>
+hipError_t launch_multi_t(const GemvArgs &args, hipStream_t stream) {
+    if (args.vectors <= 2) return launch_multi_nv<GATE, ADD, 2>(args, stream);
+    if (args.vectors <= 4) return launch_multi_nv<GATE, ADD, 4>(args, stream);
+    return launch_multi_nv<GATE, ADD, 8>(args, stream);
+}
+
 uint32_t grid_for(uint64_t work, uint32_t per_block) {
     uint64_t blocks = (work + per_block - 1) / per_block;
     if (blocks > 65536) blocks = 65536;
@@ -668,6 +910,17 @@ hipError_t launch_gemv(const GemvArgs &args, hipStream_t stream) {
     return args.add != nullptr ? launch_gemv_t<false, true>(args, stream)
                                : launch_gemv_t<false, false>(args, stream);
 }
+
+hipError_t launch_gemv_multi(const GemvArgs &args, hipStream_t stream) {
+    if (args.gate != nullptr) {
+        return args.add != nullptr ? launch_multi_t<true, true>(args, stream)
+                                   : launch_multi_t<true, false>(args, stream);
+    }
+    return args.add != nullptr ? launch_multi_t<false, true>(args, stream)
+                               : launch_multi_t<false, false>(args, stream);
+}
+
+uint32_t gemv_multi_stage_groups(uint32_t vectors) { return vectors > 4 ? 16u : 32u; }
 
 hipError_t launch_dequant(const uint8_t *w, uint32_t rows, uint32_t cols, float *out, hipStream_t stream) {
     const uint64_t work = static_cast<uint64_t>(rows) * cols / 2;

@@ -550,6 +550,57 @@ int q4rdna_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const f
     return launch_one(w, gate ? gate->tiles : nullptr, x, add, y, split, static_cast<hipStream_t>(stream));
 }
 
+int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x, uint32_t n,
+                         const float *add, float *y, const q4rdna_launch_options *options, void *stream) {
+    int rc = check_weight(w);
+    if (rc != Q4RDNA_OK) return rc;
+    if (gate != nullptr) {
+        if ((rc = check_weight(gate)) != Q4RDNA_OK) return rc;
+        if (gate->rows != w->rows || gate->columns != w->columns) return fail(Q4RDNA_NOT_APPLICABLE, "up and gate shapes differ");
+    }
+    if ((rc = check_io(x, y)) != Q4RDNA_OK) return rc;
+    if (add != nullptr && !aligned(add, 4)) return fail(Q4RDNA_ERR_ARGUMENT, "misaligned add");
+    if (n < 1 || n > Q4RDNA_MAX_BATCH) return fail(Q4RDNA_ERR_ARGUMENT, "batch %u is outside 1..%d", n, Q4RDNA_MAX_BATCH);
+    uint32_t split = options ? options->split_k : 0;
+    if (split > kMaxSplit) return fail(Q4RDNA_ERR_ARGUMENT, "split_k %u exceeds %u", split, kMaxSplit);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint8_t *gt = gate ? gate->tiles : nullptr;
+    const uint32_t groups = w->columns / kGroup;
+    // Every K chunk of the n-vector kernel fits its x stage.  Longer rows than
+    // 64 such chunks go one launch per vector.
+    const uint32_t stage = q4rdna::gemv_multi_stage_groups(n);
+    const uint32_t need = (groups + stage - 1) / stage;
+    if (n == 1 || need > std::min(groups, kMaxSplit)) {
+        const size_t M = w->rows, K = w->columns;
+        for (uint32_t v = 0; v < n; ++v)
+            if ((rc = launch_one(w, gt, x + v * K, add ? add + v * M : nullptr, y + v * M, split, s)) != Q4RDNA_OK)
+                return rc;
+        return Q4RDNA_OK;
+    }
+    if (split == 0) split = policy_split(w->rows, w->columns, w->device);
+    split = std::min(std::max(split, need), std::min(groups, kMaxSplit));
+    q4rdna::GemvArgs args{};
+    args.w = w->tiles;
+    args.gate = gt;
+    args.x = x;
+    args.add = add;
+    args.y = y;
+    args.rows = w->rows;
+    args.cols = w->columns;
+    args.split = split;
+    args.vectors = n;
+    if (split > 1) {
+        Workspace *ws = nullptr;
+        const size_t pf = static_cast<size_t>(split) * n * w->rows * (gate ? 2 : 1);
+        if ((rc = get_workspace(w->device, s, pf, w->rows / kTileRows, &ws)) != Q4RDNA_OK) return rc;
+        args.partial = ws->partial;
+        args.counters = ws->counters;
+    }
+    hipError_t e = q4rdna::launch_gemv_multi(args, s);
+    if (e != hipSuccess) return hip_fail(e, "batched GEMV launch");
+    return Q4RDNA_OK;
+}
+
 int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device, q4rdna_plan **out) {
     return q4rdna_plan_create_batch(descs, count, 1, device, out);
 }

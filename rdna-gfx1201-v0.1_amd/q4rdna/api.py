@@ -125,6 +125,26 @@ def mul_mat_ex(w: QWeight, x: torch.Tensor, y: torch.Tensor, gate: QWeight | Non
                                           x.data_ptr(), _ptr(add), y.data_ptr(), ctypes.byref(opts), s))
 
 
+def mul_mat_batch(w: QWeight, x: torch.Tensor, y: torch.Tensor, gate: QWeight | None = None,
+                  add: torch.Tensor | None = None, split_k: int = 0, stream: int | None = None) -> bool:
+    """n activation vectors against one weight, one launch: x [n][cols], y and
+    add [n][rows] (contiguous float32 on the weight's device)."""
+    if x.dim() != 2 or not x.is_contiguous() or x.dtype != torch.float32:
+        raise ValueError("x must be a contiguous float32 [n, cols] tensor")
+    if y.dim() != 2 or not y.is_contiguous() or y.dtype != torch.float32 or y.shape[0] != x.shape[0]:
+        raise ValueError("y must be a contiguous float32 [n, rows] tensor")
+    if x.shape[1] != w.cols or y.shape[1] != w.rows:
+        raise ValueError("x / y shapes do not match the weight")
+    if add is not None and (add.shape != y.shape or not add.is_contiguous() or add.dtype != torch.float32):
+        raise ValueError("add must match y")
+    opts = LaunchOptions()
+    opts.split_k = split_k
+    s = _stream(x.device) if stream is None else stream
+    return check(load().q4rdna_mul_mat_batch(ctypes.byref(w.raw), ctypes.byref(gate.raw) if gate else None,
+                                             x.data_ptr(), x.shape[0], _ptr(add), y.data_ptr(),
+                                             ctypes.byref(opts), s))
+
+
 def policy_split_k(rows: int, cols: int, device: int = 0) -> int:
     return load().q4rdna_policy_split_k(rows, cols, device)
 

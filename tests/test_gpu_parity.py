@@ -5,6 +5,8 @@ Bars: dequant and packing bit-exact; GEMV within the gate
 oracle (fp32 accumulation), plus the reference bench's own gate, relative L2
 <= 1e-5 against the sequential fp32 oracle (source/q4rdna_gemv_bench.hip:259).
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -230,6 +232,83 @@ def test_every_kernel_path_matches_oracle(cuda, kind):
             rel = np.abs(yh - want) / np.maximum(np.abs(want), 0.01 * rms)
             assert rel.max() <= GATE_TOL, (kind, cols, split, rel.max())
             assert (np.abs(yh - want) <= 1e-5 * bound + 1e-30).all(), (kind, cols, split)
+
+
+@pytest.mark.parametrize("n", [2, 3, 4, 5, 8])
+def test_mul_mat_batch_matches_oracle(cuda, n):
+    """q4rdna_mul_mat_batch: every vector against the fp64 oracle, on short
+    and long K (28672 columns: 448 groups in 16- or 32-group chunks), odd
+    row-tile counts, with the add, SwiGLU and SwiGLU-after-add epilogues."""
+    cases = [(96, 1024, "plain"), (4096, 4096, "add"), (1024, 12288, "glu"), (256, 28672, "glu+add"),
+             (160, 4096, "plain")]
+    for rows, cols, kind in cases:
+        up_t = random_tiles(rows, cols, 41 + rows + n)
+        xs = np.stack([O.gaussian_x(cols, 42 + cols + 7 * v) for v in range(n)])
+        up = api.QWeight.from_tiles(dev_u8(up_t), rows, cols)
+        gate = add = gate_t = add_np = None
+        if "add" in kind:
+            add_np = np.stack([O.gaussian_x(rows, 43 + rows + v) for v in range(n)])
+            add = dev_f32(add_np)
+        if "glu" in kind:
+            gate_t = random_tiles(rows, cols, 44 + rows + n)
+            gate = api.QWeight.from_tiles(dev_u8(gate_t), rows, cols)
+        y = torch.full((n, rows), float("nan"), device="cuda")
+        assert api.mul_mat_batch(up, dev_f32(xs), y, gate=gate, add=add)
+        torch.cuda.synchronize()
+        yh = y.cpu().numpy().astype(np.float64)
+        for v in range(n):
+            want, bound = O.gemv_f64(up_t, rows, cols, xs[v])
+            if add_np is not None:
+                want, bound = want + add_np[v], bound + np.abs(add_np[v])
+            if gate_t is not None:
+                g64, ga = O.gemv_f64(gate_t, rows, cols, xs[v])
+                bound = bound * np.abs(O.silu(g64)) + np.abs(want) * 1.1 * ga
+                want = want * O.silu(g64)
+            rms = np.sqrt(np.mean(want ** 2))
+            rel = np.abs(yh[v] - want) / np.maximum(np.abs(want), 0.01 * rms)
+            assert rel.max() <= GATE_TOL, (rows, cols, kind, n, v, rel.max())
+            assert (np.abs(yh[v] - want) <= 1e-5 * bound + 1e-30).all(), (rows, cols, kind, n, v)
+
+
+@pytest.mark.parametrize("n,split", [(2, 2), (4, 2), (8, 4), (3, 4)])
+def test_mul_mat_batch_equals_single_vector_launches(cuda, n, split):
+    """Each vector of a batched launch equals q4rdna_mul_mat_ex of that vector
+    with the same split, bit for bit (same staging, fma order and summation
+    order; both run eight-wave workgroups at this shape)."""
+    rows, cols = 4096, 4096
+    t = random_tiles(rows, cols, 51)
+    w = api.QWeight.from_tiles(dev_u8(t), rows, cols)
+    gt = api.QWeight.from_tiles(dev_u8(random_tiles(rows, cols, 52)), rows, cols)
+    xs = dev_f32(np.stack([O.gaussian_x(cols, 53 + v) for v in range(n)]))
+    for gate in (None, gt):
+        y = torch.empty((n, rows), device="cuda")
+        assert api.mul_mat_batch(w, xs, y, gate=gate, split_k=split)
+        for v in range(n):
+            y1 = torch.empty(rows, device="cuda")
+            assert api.mul_mat_ex(w, xs[v].contiguous(), y1, gate=gate, split_k=split)
+            torch.cuda.synchronize()
+            assert torch.equal(y[v], y1), (n, split, v, gate is not None)
+
+
+def test_mul_mat_batch_long_rows_fall_back_per_vector(cuda):
+    """Rows longer than 64 chunks of the n-vector kernel's stage (here 1025
+    groups at n = 5: 16-group chunks would need 65) run one launch per
+    vector, still against the oracle; n outside 1..8 is an argument error."""
+    rows, cols, n = 32, 1025 * 64, 5
+    t = random_tiles(rows, cols, 61)
+    w = api.QWeight.from_tiles(dev_u8(t), rows, cols)
+    xs = np.stack([O.gaussian_x(cols, 62 + v) for v in range(n)])
+    y = torch.full((n, rows), float("nan"), device="cuda")
+    assert api.mul_mat_batch(w, dev_f32(xs), y)
+    torch.cuda.synchronize()
+    for v in range(n):
+        check_gemv(y[v], t, rows, cols, xs[v], f"fallback vector {v}")
+    lib = q4rdna.load()
+    xd = dev_f32(xs)
+    for bad in (0, 9):
+        rc = lib.q4rdna_mul_mat_batch(ctypes.byref(w.raw), None, xd.data_ptr(), bad, None, y.data_ptr(), None,
+                                      api._stream(xd.device))
+        assert rc == q4rdna.ERR_ARGUMENT
 
 
 def test_not_applicable_leaves_output_untouched(cuda):
