@@ -3,8 +3,8 @@
  * (llama.cpp's ggml-cuda backend) would bind it: no Python, no torch.
  *
  * Builds a three-tensor sidecar image in memory, opens it on device 0, looks
- * weights up by ggml name and shape, and runs q4rdna_mul_mat, _add, _glu and
- * a two-GEMV plan against a double-precision CPU dot product of the same
+ * weights up by ggml name and shape, and runs q4rdna_mul_mat, _add, _glu,
+ * _batch and a two-GEMV plan against a double-precision CPU dot product of the same
  * tiles (IEEE fp16 scales).  Also checks the not-applicable paths leave the
  * output untouched.  Exit status 0 and "c abi ok" on success.
  */
@@ -185,6 +185,27 @@ int main(void) {
     cpu_gemv(img + off[0], 256, 1024, hx, want, NULL);
     EXPECT(gate_ok(hy, want, 256));
     q4rdna_plan_destroy(plan);
+
+    /* mul_mat_batch: three vectors, x [3][1024], y [3][256] */
+    {
+        float *hxb = malloc(3 * 1024 * sizeof(float)), *hyb = malloc(3 * 256 * sizeof(float));
+        for (int i = 0; i < 3 * 1024; ++i) hxb[i] = next_gauss();
+        float *dxb, *dyb;
+        CHECK_HIP(hipMalloc((void **)&dxb, 3 * 1024 * sizeof(float)));
+        CHECK_HIP(hipMalloc((void **)&dyb, 3 * 256 * sizeof(float)));
+        CHECK_HIP(hipMemcpy(dxb, hxb, 3 * 1024 * sizeof(float), hipMemcpyHostToDevice));
+        EXPECT(q4rdna_mul_mat_batch(&wq, NULL, dxb, 3, NULL, dyb, NULL, NULL) == Q4RDNA_OK);
+        EXPECT(q4rdna_mul_mat_batch(&wq, NULL, dxb, 9, NULL, dyb, NULL, NULL) == Q4RDNA_ERR_ARGUMENT);
+        CHECK_HIP(hipMemcpy(hyb, dyb, 3 * 256 * sizeof(float), hipMemcpyDeviceToHost));
+        for (int v = 0; v < 3; ++v) {
+            cpu_gemv(img + off[0], 256, 1024, hxb + 1024 * v, want, NULL);
+            EXPECT(gate_ok(hyb + 256 * v, want, 256));
+        }
+        CHECK_HIP(hipFree(dxb));
+        CHECK_HIP(hipFree(dyb));
+        free(hxb);
+        free(hyb);
+    }
 
     q4rdna_sidecar_close(sc);
     CHECK_HIP(hipFree(dx)); CHECK_HIP(hipFree(dy)); CHECK_HIP(hipFree(dy2)); CHECK_HIP(hipFree(dadd));
