@@ -1,7 +1,8 @@
 // Host runtime of the Q4_RDNA dequant-GEMV C ABI (include/q4rdna.h): sidecar
 // parsing and upload, the name registry, shape policy, split-K workspaces and
 // the entry points.  All compute runs in the gfx950 kernels of
-// q4rdna_kernels.hip; this file never computes a result on the CPU.
+// q4rdna_kernels.hip and q4rdna_mfma.hip; this file never computes a result
+// on the CPU.
 #include "q4rdna.h"
 
 #include <hip/hip_runtime_api.h>
