@@ -218,10 +218,10 @@ def host_description() -> str:
 
 def pack_figures(seed: int, sample_rows: int = 1024):
     """Quantize + pack of one 4096x4096 N(0, 0.02) tensor with the sidecar
-    search: the GPU packer on the whole tensor, the oracle's C restatement of
+    search: the GPU packer on the whole tensor; the oracle's C restatement of
     the native packer (source/q4rdna_sidecar_pack.cpp:126-179) on one thread
-    over the first `sample_rows` rows, extrapolated; and whether the two
-    agree byte for byte on the sample."""
+    over the first `sample_rows` rows, extrapolated, and on all host cores
+    over the whole tensor; and whether they agree byte for byte."""
     import numpy as np
     import torch
     import oracle as O
@@ -242,10 +242,18 @@ def pack_figures(seed: int, sample_rows: int = 1024):
     ref = O.pack(sample, O.ALGO_SIDECAR)
     cpu_s = time.perf_counter() - t0
     same = bool(np.array_equal(ref, tiles[:ref.size].cpu().numpy()))
+    # All host cores (the reference packer spreads independent groups over
+    # OpenMP threads, source/q4rdna_sidecar_pack.cpp:262): the whole tensor.
+    whole = w.cpu().numpy()
+    t0 = time.perf_counter()
+    ref_all, threads = O.pack_mt(whole, O.ALGO_SIDECAR)
+    cpu_all_s = time.perf_counter() - t0
+    same_all = bool(np.array_equal(ref_all, tiles.cpu().numpy()))
     return dict(shape="4096x4096", algorithm="sidecar (10 starts x 12 LSQ iterations)", gpu_ms=round(gpu_ms, 3),
                 cpu_s=round(cpu_s * rows / sample_rows, 2), cpu_threads=1,
                 cpu_sample=f"first {sample_rows} rows, {cpu_s:.2f} s, extrapolated to 4096 rows",
-                gpu_matches_oracle_on_sample=same)
+                cpu_all_cores_s=round(cpu_all_s, 3), cpu_all_cores_threads=threads,
+                gpu_matches_oracle_on_sample=same, gpu_matches_oracle_all_cores=same_all)
 
 
 def load_traffic():

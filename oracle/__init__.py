@@ -65,6 +65,8 @@ def lib() -> ctypes.CDLL:
         L.q4o_select_scale.argtypes = [f32p, ctypes.c_int]
         L.q4o_select_scale.restype = ctypes.c_uint16
         L.q4o_pack.argtypes = [f32p, u32, u32, ctypes.c_int, u8p]
+        L.q4o_pack_mt.argtypes = [f32p, u32, u32, ctypes.c_int, u8p, ctypes.c_int]
+        L.q4o_pack_mt.restype = ctypes.c_int
         L.q4o_dequant.argtypes = [u8p, u32, u32, f32p]
         L.q4o_dequant_ref_cpu.argtypes = [u8p, u32, u32, f32p]
         L.q4o_gemv_seq_f32.argtypes = [u8p, u32, u32, f32p, f32p, u32, u32, ctypes.c_int]
@@ -121,6 +123,18 @@ def pack(w: np.ndarray, algorithm: int = ALGO_SIDECAR) -> np.ndarray:
     if rc != 0:
         raise ValueError(f"unsupported shape {w.shape} or algorithm {algorithm}")
     return out
+
+
+def pack_mt(w: np.ndarray, algorithm: int = ALGO_SIDECAR, threads: int = 0):
+    """pack() with row tiles spread over OpenMP threads (0 = the OpenMP
+    default); returns (tiles, threads used)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    out = np.zeros(packed_size(rows, cols), dtype=np.uint8)
+    used = lib().q4o_pack_mt(_ptr(w, ctypes.c_float), rows, cols, algorithm, _ptr(out, ctypes.c_uint8), threads)
+    if used < 0:
+        raise ValueError(f"unsupported shape {w.shape} or algorithm {algorithm}")
+    return out, used
 
 
 def dequant(tiles: np.ndarray, rows: int, cols: int, ref_cpu_decode: bool = False) -> np.ndarray:

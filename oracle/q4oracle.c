@@ -20,6 +20,7 @@
  *   q4o_select_scale_experiment  byte-identical to the compiled reference CPU
  *                              experiment (oracle/_ref) and golden fixtures
  *   q4o_pack                   same as the scale selectors (tile placement)
+ *   q4o_pack_mt                byte-identical to q4o_pack (tests)
  *   q4o_dequant                exhaustive closed form fp32(s)*q incl. signed zero
  *   q4o_gemv_seq_f32           vs fp64 brute force + planted-mistake checks
  *   q4o_gemv_seq_f32_mt        bit-identical to q4o_gemv_seq_f32 (tests)
@@ -484,6 +485,39 @@ int q4o_gemv_seq_f32_mt(const uint8_t *tiles, uint32_t rows, uint32_t cols, cons
 #else
     (void)threads;
     q4o_gemv_seq_f32(tiles, rows, cols, x, y, 0, rows, 0);
+#endif
+    return used;
+}
+
+/* q4o_pack with rows spread over OpenMP threads (every (row, group) is
+ * independent, so the bytes are identical to q4o_pack's); the all-cores
+ * variant of the packing baseline, as the reference packer parallelises
+ * independent groups (source/q4rdna_sidecar_pack.cpp:262).  Returns the
+ * number of threads used, or -1 for an unsupported shape or algorithm. */
+int q4o_pack_mt(const float *w, uint32_t rows, uint32_t cols, int algorithm, uint8_t *tiles, int threads)
+{
+    if (rows % Q4O_TILE_ROWS || cols % Q4O_GROUP || algorithm < 0 || algorithm > 3) return -1;
+    int used = 1;
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+    int64_t blocks = rows / Q4O_TILE_ROWS;
+    int bad = 0;
+#pragma omp parallel reduction(| : bad)
+    {
+#pragma omp single
+        used = omp_get_num_threads();
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t b = 0; b < blocks; ++b) {
+            /* One row tile at a time through q4o_pack on a view of its rows:
+             * a row tile's bytes are one contiguous run of the tensor. */
+            uint64_t off = (uint64_t)b * (cols / Q4O_GROUP) * Q4O_TILE_BYTES;
+            bad |= q4o_pack(w + (uint64_t)b * Q4O_TILE_ROWS * cols, Q4O_TILE_ROWS, cols, algorithm, tiles + off) != 0;
+        }
+    }
+    if (bad) return -1;
+#else
+    (void)threads;
+    if (q4o_pack(w, rows, cols, algorithm, tiles) != 0) return -1;
 #endif
     return used;
 }

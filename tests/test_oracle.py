@@ -259,6 +259,19 @@ def test_gemv_seq_f32_threads_match_one_thread():
     assert np.array_equal(y1, ym)
 
 
+@pytest.mark.parametrize("algorithm", [0, 1, 2, 3])
+def test_pack_threads_match_one_thread(algorithm):
+    """The all-cores packer writes the same bytes as the one-thread packer,
+    on Gaussian weights with outlier and near-zero groups."""
+    w = O.gaussian_weights(128, 256, 17 + algorithm)
+    w.reshape(-1, 64)[::7] *= 20
+    w.reshape(-1, 64)[3::11] *= 1e-5
+    one = O.pack(w, algorithm)
+    many, used = O.pack_mt(w, algorithm, threads=4)
+    assert used >= 1
+    assert np.array_equal(one, many)
+
+
 def test_gemv_gates_accept_oracle_and_catch_planted_mistakes():
     tiles, x = small_problem(256, 1024, 8)
     rows, cols = 256, 1024
