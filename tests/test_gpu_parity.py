@@ -489,26 +489,29 @@ def test_batched_plan_rows_are_independent_of_batch(cuda):
 
 @pytest.mark.gpu
 def test_plan_and_mul_mat_replay_from_a_hip_graph(cuda):
-    """A plan launch and per-tensor launches captured into one HIP graph (the
-    plan allocates nothing per launch; the per-tensor workspace is allocated
-    by an eager call first).  Replayed several times with new activations and
-    eager work in between; every replay must equal the eager results bit for
-    bit."""
+    """A plan launch, a per-tensor launch and a four-vector launch captured
+    into one HIP graph (the plan allocates nothing per launch; the per-tensor
+    workspace is allocated by an eager call first).  Replayed several times
+    with new activations and eager work in between; every replay must equal
+    the eager results bit for bit."""
     rows, cols = 1024, 4096
     tiles = [random_tiles(rows, cols, 1200 + i) for i in range(3)]
     ws = [api.QWeight.from_tiles(dev_u8(t), rows, cols) for t in tiles]
     xs = [torch.empty(cols, device="cuda") for _ in ws]
     ys_plan = [torch.empty(rows, device="cuda") for _ in ws]
     y_single = torch.empty(rows, device="cuda")
+    xb = torch.empty(4, cols, device="cuda")
+    yb = torch.empty(4, rows, device="cuda")
     s = torch.cuda.Stream()
     plan = api.Plan([(w, x, y) for w, x, y in zip(ws, xs, ys_plan)])
 
     def work():
         assert plan.launch(s.cuda_stream)
         api.mul_mat(ws[0], xs[1], y_single, stream=s.cuda_stream)
+        assert api.mul_mat_batch(ws[1], xb, yb, stream=s.cuda_stream)
 
     with torch.cuda.stream(s):
-        for x in xs:
+        for x in xs + [xb]:
             x.normal_()
         work()  # allocates the per-tensor split-K workspace of stream s
     torch.cuda.synchronize()
@@ -517,18 +520,19 @@ def test_plan_and_mul_mat_replay_from_a_hip_graph(cuda):
         work()
     for rep in range(4):
         with torch.cuda.stream(s):
-            for x in xs:
+            for x in xs + [xb]:
                 x.normal_()
             work()
         s.synchronize()
-        eager = [y.clone() for y in ys_plan] + [y_single.clone()]
-        for y in ys_plan + [y_single]:
+        outs = ys_plan + [y_single, yb]
+        eager = [y.clone() for y in outs]
+        for y in outs:
             y.fill_(float("nan"))
         torch.cuda.synchronize()
         with torch.cuda.stream(s):
             g.replay()
         s.synchronize()
-        for got, want in zip(ys_plan + [y_single], eager):
+        for got, want in zip(outs, eager):
             assert torch.equal(got, want), rep
         # and the replay is right, not just repeatable
         y64, a64 = O.gemv_f64(tiles[2], rows, cols, xs[2].cpu().numpy())
