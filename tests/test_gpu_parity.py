@@ -400,6 +400,43 @@ def test_plan_matches_oracle(cuda):
     plan.close()
 
 
+def wide_x(cols: int, seed: int) -> np.ndarray:
+    """N(0, 1) activations with groups scaled by 1e4 and by 1e-4, and one
+    all-zero group: block exponents far apart and a zero block."""
+    x = O.gaussian_x(cols, seed)
+    g = x.reshape(-1, 64)
+    g[1::5] *= 1e4
+    g[3::7] *= 1e-4
+    g[2] = 0.0
+    return x
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_plan_subnormal_scales_and_wide_activations(cuda, batch):
+    """Plans (one vector and a batch of three) on tiles with subnormal fp16
+    scales and activations whose groups span eight decades plus a zero group;
+    a vector of zeros gives exact zeros."""
+    rows, cols = 256, 4096
+    t = random_tiles(rows, cols, 71, subnormal=True)
+    w = api.QWeight.from_tiles(dev_u8(t), rows, cols)
+    xs = [wide_x(cols, 72 + v) for v in range(batch)]
+    if batch > 1:
+        xs[-1] = np.zeros(cols, np.float32)
+    xd = dev_f32(np.stack(xs)) if batch > 1 else dev_f32(xs[0])
+    y = torch.full((batch, rows) if batch > 1 else (rows,), float("nan"), device="cuda")
+    plan = api.Plan([(w, xd, y)], batch=batch)
+    assert plan.launch()
+    torch.cuda.synchronize()
+    yh = y.cpu().numpy().reshape(batch, rows)
+    for v, x in enumerate(xs):
+        if not x.any():
+            assert (yh[v] == 0).all()
+            continue
+        y64, a64 = O.gemv_f64(t, rows, cols, x)
+        assert O.gemv_errors(yh[v], y64, a64)["gate"] <= GATE_TOL, v
+    plan.close()
+
+
 @pytest.mark.gpu
 def test_plan_nonfinite_activation(cuda):
     """A NaN in x makes every row NaN, as in the fp32 reference.  An infinity
