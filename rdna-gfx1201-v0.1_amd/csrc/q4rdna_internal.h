@@ -55,7 +55,9 @@ struct PlanDesc {
 };
 
 constexpr uint32_t kPrepBytes = 272;
-constexpr uint32_t kChunkGroups = 64;
+// K chunk of a single-vector plan item: 192 groups holds a whole 12288-wide
+// row in one item, so such GEMVs need no split-K partials.
+constexpr uint32_t kChunkGroups = 192;
 constexpr uint32_t kBlockRows = 64;
 
 hipError_t launch_gemv(const GemvArgs &args, hipStream_t stream);

@@ -37,9 +37,6 @@ namespace q4rdna {
 namespace {
 
 constexpr int kWaves = 4;
-// Wave steps in flight per wave (register sets that rotate) on a full chunk;
-// deeper pipelines measured no faster.
-constexpr int kPlanDepth = 2;
 
 // Activation digits.  One lane takes one k-slot of a 64-element group: the
 // 16 elements 2*(kslot + 4c) + h (c = 0..7, h = 0..1), i.e. its operand bytes
@@ -141,11 +138,14 @@ __device__ __forceinline__ uint32_t high_nibbles_x16(uint32_t t) { return t & 0x
 
 // ---- sweep kernel ---------------------------------------------------------
 //
-// An item is (64-row block, stream, K chunk of up to 64 groups), taken by one
-// workgroup.  Its four waves read the block's two row tiles side by side: in
-// workgroup step s, wave w takes groups g0 + 4w .. g0 + 4w + 3 with
-// g0 = chunk start + 16s, so the workgroup streams two contiguous runs of 16
-// tiles.
+// An item is (64-row block, stream, K chunk of up to kChunkGroups = 192
+// groups), taken by one workgroup.  Its four waves read the block's two row
+// tiles side by side: in workgroup step s, wave w takes groups
+// g0 + 4w .. g0 + 4w + 3 with g0 = chunk start + 16s, so the workgroup
+// streams two contiguous runs of 16 tiles.  A 192-group chunk holds a whole
+// 12288-wide row, so such GEMVs finish without split-K partials: an item's
+// end (a workgroup barrier, the reduction, and for split items an arrival
+// chain through global memory) is where the sweep stalls.
 //
 // Loads.  Per step a wave reads eight tiles (4 groups x 2 row tiles).  Load
 // instruction c reads the whole 1024-byte code area of tile (group c/2, row
@@ -170,7 +170,10 @@ __device__ __forceinline__ uint32_t high_nibbles_x16(uint32_t t) { return t & 0x
 //    each row meet in LDS at the item's end.
 constexpr int kStepGroups = 4;                         // groups per wave step
 constexpr int kWgStepGroups = kWaves * kStepGroups;    // groups per workgroup step
-constexpr int kItemSteps = kChunkGroups / kWgStepGroups;
+constexpr uint32_t kChunkBlockGroups = 64;                          // groups of one full block of steps
+constexpr uint32_t kBlockSteps = kChunkBlockGroups / kWgStepGroups;  // 4
+static_assert(kChunkGroups % kChunkBlockGroups == 0, "chunks are whole blocks of steps");
+static_assert(kBlockSteps == 4, "item_steps spells out a block's four steps");
 // LDS bytes per staged tile: 1024 + a 64-byte skew.  Over the 252-tensor
 // stack the 64-byte skew measures 10.2M SQ_LDS_BANK_CONFLICT cycles against
 // 23.7M for a 32- or 128-byte skew and 50.9M for none, at equal sweep time.
@@ -331,53 +334,73 @@ struct Shared {
 };
 
 // The wave's steps of one item: rt0 / rt1 = the block's two row tiles.
-template <bool FULL>
+// Groups [g_begin, g_begin + 64 * blocks) are full 64-group blocks; the
+// rest up to g_end (fewer than 64 groups) is a short tail.
 __device__ __forceinline__ void item_steps(const uint8_t *rt0, const uint8_t *rt1, const uint8_t *prep,
                                            uint32_t g_begin, uint32_t g_end, int wave, int lane, const LaneRole &ln,
                                            uint8_t *stage, float (&acc)[16]) {
-    if constexpr (FULL) {
-        // Straight-line code: the waitcnt pass then counts outstanding loads
-        // exactly, and each step waits only for its own loads while the
-        // next kPlanDepth-1 steps' are in flight.  sched_barrier keeps a
-        // prefetch from sinking below the previous step's arithmetic.
-        constexpr int D = kPlanDepth;
-        WaveRegs r[D];
-        auto load = [&](int s, WaveRegs &rr) {
-            const uint32_t g = g_begin + kWgStepGroups * s + kStepGroups * wave;
+    const uint32_t blocks = (g_end - g_begin) / kChunkBlockGroups;
+    if (blocks > 0) {
+        // Step t reads groups g_begin + 16t + 4*wave .. +3.  Two register
+        // sets in rotation: set t % 2 holds step t and, once step t's
+        // arithmetic is done, takes step t + 2, so each step waits only for
+        // its own loads while the next step's are in flight -- across the
+        // blocks of a chunk too.  Each block's four steps are straight-line
+        // code (the last block peeled off, so that no load is conditional),
+        // which lets the waitcnt pass count outstanding loads exactly;
+        // sched_barrier keeps a load from sinking below the arithmetic that
+        // follows it.
+        WaveRegs r[2];
+        auto load = [&](uint32_t t, WaveRegs &rr) {
+            const uint32_t g = g_begin + kWgStepGroups * t + kStepGroups * wave;
             load_wave(rr, rt0 + static_cast<size_t>(g) * kTileBytes, rt1 + static_cast<size_t>(g) * kTileBytes,
                       prep + static_cast<size_t>(g + ln.gB) * kPrepBytes + ln.a_offset,
                       prep + static_cast<size_t>(g + ln.kslot) * kPrepBytes + 256, ln, lane);
             __builtin_amdgcn_sched_barrier(0);
         };
-#pragma unroll
-        for (int p = 0; p + 1 < D; ++p) load(p, r[p]);
-#pragma unroll
-        for (int s = 0; s < kItemSteps; ++s) {
-            if (s + D - 1 < kItemSteps) load(s + D - 1, r[(s + D - 1) % D]);
-            restage(r[s % D], stage, ln, lane);
-            compute_wave<false>(r[s % D], acc, true);
-        }
-    } else {
-        // A short last chunk: the step's four groups are clamped to the
-        // chunk for the loads, and those past its end are masked out.
-        for (uint32_t g = g_begin + kStepGroups * wave; g < g_end; g += kWgStepGroups) {
-            const uint32_t gb = min(g + ln.gB, g_end - 1);
-            const uint32_t gf = g + ln.kslot;
-            WaveRegs rr;
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const uint32_t gc = min(g + (c >> 1), g_end - 1);
-                const uint8_t *tile = ((c & 1) ? rt1 : rt0) + static_cast<size_t>(gc) * kTileBytes;
-                rr.code[c] = __builtin_nontemporal_load((gptr_i32x4)(tile + 64 + 16 * lane));
-            }
-            const uint8_t *own = (ln.T ? rt1 : rt0) + static_cast<size_t>(gb) * kTileBytes + 32 * ln.h;
-            rr.sc[0] = __builtin_nontemporal_load((gptr_i32x4)own);
-            rr.sc[1] = __builtin_nontemporal_load((gptr_i32x4)(own + 16));
-            rr.a = *(gptr_i32x4)(prep + static_cast<size_t>(gb) * kPrepBytes + ln.a_offset);
-            rr.f = *(gptr_cf32)(prep + static_cast<size_t>(min(gf, g_end - 1)) * kPrepBytes + 256);
+        auto step = [&](WaveRegs &rr) {
             restage(rr, stage, ln, lane);
-            compute_wave<true>(rr, acc, gf < g_end);
+            compute_wave<false>(rr, acc, true);
+        };
+        load(0, r[0]);
+        load(1, r[1]);
+        uint32_t t = 0;
+        for (uint32_t b = 0; b + 1 < blocks; ++b, t += kBlockSteps) {
+            step(r[0]);
+            load(t + 2, r[0]);
+            step(r[1]);
+            load(t + 3, r[1]);
+            step(r[0]);
+            load(t + 4, r[0]);
+            step(r[1]);
+            load(t + 5, r[1]);
         }
+        step(r[0]);
+        load(t + 2, r[0]);
+        step(r[1]);
+        load(t + 3, r[1]);
+        step(r[0]);
+        step(r[1]);
+    }
+    // The short tail: the step's four groups are clamped to the chunk for
+    // the loads, and those past its end are masked out.
+    for (uint32_t g = g_begin + blocks * kChunkBlockGroups + kStepGroups * wave; g < g_end; g += kWgStepGroups) {
+        const uint32_t gb = min(g + ln.gB, g_end - 1);
+        const uint32_t gf = g + ln.kslot;
+        WaveRegs rr;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const uint32_t gc = min(g + (c >> 1), g_end - 1);
+            const uint8_t *tile = ((c & 1) ? rt1 : rt0) + static_cast<size_t>(gc) * kTileBytes;
+            rr.code[c] = __builtin_nontemporal_load((gptr_i32x4)(tile + 64 + 16 * lane));
+        }
+        const uint8_t *own = (ln.T ? rt1 : rt0) + static_cast<size_t>(gb) * kTileBytes + 32 * ln.h;
+        rr.sc[0] = __builtin_nontemporal_load((gptr_i32x4)own);
+        rr.sc[1] = __builtin_nontemporal_load((gptr_i32x4)(own + 16));
+        rr.a = *(gptr_i32x4)(prep + static_cast<size_t>(gb) * kPrepBytes + ln.a_offset);
+        rr.f = *(gptr_cf32)(prep + static_cast<size_t>(min(gf, g_end - 1)) * kPrepBytes + 256);
+        restage(rr, stage, ln, lane);
+        compute_wave<true>(rr, acc, gf < g_end);
     }
 }
 
@@ -398,10 +421,7 @@ __device__ __forceinline__ void run_item(Shared &sh, const PlanDesc &d, uint32_t
     float acc[16];
 #pragma unroll
     for (int n = 0; n < 16; ++n) acc[n] = 0.0f;
-    if (g_end - g_begin == kChunkGroups)
-        item_steps<true>(rt0, rt1, d.prep, g_begin, g_end, wave, lane, ln, sh.stage[wave], acc);
-    else
-        item_steps<false>(rt0, rt1, d.prep, g_begin, g_end, wave, lane, ln, sh.stage[wave], acc);
+    item_steps(rt0, rt1, d.prep, g_begin, g_end, wave, lane, ln, sh.stage[wave], acc);
 
     ItemOut o{d.add, d.y, d.partial, d.counters, d.rows, block, part, per, d.chunks, d.streams};
     finish_item(sh, o, acc, ln, wave);

@@ -617,13 +617,7 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
     const uint32_t block_rows = n == 1 ? q4rdna::kBlockRows : q4rdna::kBatchBlockRows;
     const uint64_t prep_per_group =
         n == 1 ? q4rdna::kPrepBytes : static_cast<uint64_t>((n + 3) / 4) * q4rdna::kBatchQuadBytesHost;
-    std::vector<q4rdna::PlanDesc> host(static_cast<size_t>(count) + 1);
-    // Scratch layout: activation digits of every group in global group order
-    // (prep_per_group each), the prep launch's group table, then per GEMV
-    // with several items per block its partials and per-block counters
-    // (offsets below are relative to the end of the first two regions).
-    uint64_t items = 0, groups = 0, scratch = 0;
-    std::vector<uint64_t> part_off(count), cnt_off(count);
+    const uint32_t chunk_groups = n == 1 ? kChunkGroups : q4rdna::kBatchChunkGroups;
     for (uint32_t i = 0; i < count; ++i) {
         const q4rdna_gemv_desc &d = descs[i];
         if (d.weight.tiles == nullptr || d.x == nullptr || d.y == nullptr)
@@ -633,8 +627,25 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
             (d.add != nullptr && !aligned(d.add, 4)))
             return fail(Q4RDNA_ERR_ARGUMENT, "descriptor %u: invalid shape or alignment", i);
         if (d.weight.device != device) return fail(Q4RDNA_ERR_ARGUMENT, "descriptor %u lives on device %d", i, d.weight.device);
+    }
+    // The GEMVs of a plan are independent, so the sweep may take them in any
+    // order: GEMVs with longer items (wider K chunks) go first, so that the
+    // end of the sweep, where workgroups run out of items, deals short ones.
+    std::vector<uint32_t> order(count);
+    for (uint32_t i = 0; i < count; ++i) order[i] = i;
+    auto item_groups = [&](uint32_t i) { return std::min(descs[i].weight.columns / kGroup, chunk_groups); };
+    std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) { return item_groups(a) > item_groups(b); });
+    std::vector<q4rdna::PlanDesc> host(static_cast<size_t>(count) + 1);
+    // Scratch layout: activation digits of every group in global group order
+    // (prep_per_group each), the prep launch's group table, then per GEMV
+    // with several items per block its partials and per-block counters
+    // (offsets below are relative to the end of the first two regions).
+    // host[i] describes descs[order[i]].
+    uint64_t items = 0, groups = 0, scratch = 0;
+    std::vector<uint64_t> part_off(count), cnt_off(count);
+    for (uint32_t i = 0; i < count; ++i) {
+        const q4rdna_gemv_desc &d = descs[order[i]];
         const uint32_t g = d.weight.columns / kGroup;
-        const uint32_t chunk_groups = n == 1 ? kChunkGroups : q4rdna::kBatchChunkGroups;
         const uint32_t chunks = (g + chunk_groups - 1) / chunk_groups;
         const uint32_t blocks = (d.weight.rows + block_rows - 1) / block_rows;
         const uint32_t streams = d.gate_tiles != nullptr ? 2u : 1u;
@@ -675,7 +686,7 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
     for (uint32_t i = 0; i < count; ++i)
         for (uint32_t g = host[i].group_begin; g < host[i + 1].group_begin; ++g) {
             if (n == 1)
-                table[g] = reinterpret_cast<uint64_t>(descs[i].x + static_cast<size_t>(g - host[i].group_begin) * kGroup);
+                table[g] = reinterpret_cast<uint64_t>(host[i].x + static_cast<size_t>(g - host[i].group_begin) * kGroup);
             else
                 reinterpret_cast<uint32_t *>(table.data())[g] = i;
         }

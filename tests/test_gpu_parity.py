@@ -351,12 +351,14 @@ def test_sidecar_open_find_and_gemv(cuda, golden, tmp_path):
 # ----------------------------------------------------------------- multi-tensor plan
 
 def test_plan_matches_oracle(cuda):
-    # Short and full 64-group chunks, several chunks with a short last one,
-    # odd row-tile counts, and the add / SwiGLU epilogues over one and
-    # several chunks.
+    # K chunks (up to 192 groups) made of 64-group blocks with and without a
+    # short tail, tail-only chunks, several chunks (split-K) with a short
+    # last one, odd row-tile counts, and the add / SwiGLU epilogues over one
+    # and several chunks.
     shapes = [(128, 512, None), (32, 512, None), (32, 512, "add"), (128, 512, None), (384, 512, "glu"),
               (128, 1536, None), (4096, 4096, None), (1024, 4096, "add"), (96, 4736, None),
-              (160, 8192, "glu"), (96, 12288, "add"), (32, 4096, "glu"), (224, 28672, None)]
+              (160, 8192, "glu"), (96, 12288, "add"), (32, 4096, "glu"), (224, 28672, None),
+              (64, 12800, None), (96, 8320, "add"), (160, 4096, None), (224, 2048, "glu")]
     items, checks = [], []
     for i, (rows, cols, kind) in enumerate(shapes):
         t = random_tiles(rows, cols, 100 + i)
