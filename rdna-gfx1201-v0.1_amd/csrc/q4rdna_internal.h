@@ -79,7 +79,7 @@ hipError_t launch_plan(const PlanDesc *descs, uint32_t items, uint32_t workgroup
 // kBatchQuadBytesHost per (group, quad of 4 vectors).
 constexpr uint32_t kBatchQuadBytesHost = 1040;
 constexpr uint32_t kBatchBlockRows = 256;
-constexpr uint32_t kBatchChunkGroups = 64;  // K chunk of a batched item (smaller chunks measured slower)
+constexpr uint32_t kBatchChunkGroups = 192;  // K chunk of a batched item (a whole 12288-wide row)
 hipError_t launch_prep_batch(const PlanDesc *descs, const uint32_t *owner, uint32_t groups, uint32_t n,
                              hipStream_t stream);
 hipError_t launch_plan_batch(const PlanDesc *descs, uint32_t items, uint32_t n, uint32_t workgroups, uint32_t *sched,

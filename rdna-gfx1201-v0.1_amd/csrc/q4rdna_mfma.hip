@@ -461,8 +461,9 @@ __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ 
 // three digits of up to four vectors (rows 4n + d of A, d = 3 zero), so
 // every lane of D is useful for N = 4 and a second vector quad costs one more
 // MFMA per operand, not more loads or transposes.
-//  * Item: (256-row block = 8 row tiles, stream, K chunk of up to 64
-//    groups); wave w takes groups chunk start + w + 4s, one per step.
+//  * Item: (256-row block = 8 row tiles, stream, K chunk of up to
+//    kBatchChunkGroups = 192 groups); wave w takes groups
+//    chunk start + w + 4s, one per step.
 //  * Loads per step: load instruction c reads the whole code area of row
 //    tile c at the step's group (1 KB contiguous), restaged through LDS as in
 //    the single-vector sweep; lane (kslot, j) then reads rows 16h..16h+15 of
@@ -499,6 +500,9 @@ __global__ __launch_bounds__(256) void prep_batch_kernel(const PlanDesc *__restr
 }
 
 constexpr int kBatchWaves = 4;  // eight waves per workgroup measured slower
+constexpr uint32_t kBatchBlockGroups = 64;  // groups of one unrolled block of steps
+static_assert(kBatchChunkGroups % kBatchBlockGroups == 0, "batched chunks are whole blocks of steps");
+static_assert((kBatchBlockGroups / kBatchWaves) % 2 == 0, "a block's first step lands in r[0]");
 
 // A wave's stage also receives its partial sums at the item's end (after
 // its last step, so the two uses never overlap): 4*NQ x 256 floats <= 8 KB.
@@ -596,21 +600,34 @@ __device__ __forceinline__ void run_batch_item(BatchShared<NQ> &sh, const PlanDe
         for (int c = 0; c < 8; ++c) r.code[c] = *reinterpret_cast<const i32x4 *>(sh.stage[wave] + lds_read + 128 * c);
         compute_batch<NQ>(r, a, f, acc);
     };
-    if (g_end - g_begin == kBatchChunkGroups) {
-        constexpr int kSteps = kBatchChunkGroups / kBatchWaves;
+    // Full 64-group blocks: 16 steps each, straight-line code with two steps
+    // in flight; a block's last step loads the next block's first, so the
+    // pipeline runs through a multi-block chunk (the last block peeled off,
+    // so that no load is conditional).  Then a short tail, one step at a
+    // time.
+    constexpr int kSteps = kBatchBlockGroups / kBatchWaves;
+    const uint32_t blocks = (g_end - g_begin) / kBatchBlockGroups;
+    if (blocks > 0) {
         BatchRegs r[2];
         load(g_begin + wave, r[0]);
+        uint32_t base = g_begin + wave;
+        for (uint32_t b = 0; b + 1 < blocks; ++b, base += kBatchBlockGroups) {
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s) {
+                load(base + kBatchWaves * (s + 1), r[(s + 1) & 1]);
+                step(base + kBatchWaves * s, r[s & 1]);
+            }
+        }
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) {
-            if (s + 1 < kSteps) load(g_begin + wave + kBatchWaves * (s + 1), r[(s + 1) & 1]);
-            step(g_begin + wave + kBatchWaves * s, r[s & 1]);
+            if (s + 1 < kSteps) load(base + kBatchWaves * (s + 1), r[(s + 1) & 1]);
+            step(base + kBatchWaves * s, r[s & 1]);
         }
-    } else {
-        for (uint32_t g = g_begin + wave; g < g_end; g += kBatchWaves) {
-            BatchRegs r;
-            load(g, r);
-            step(g, r);
-        }
+    }
+    for (uint32_t g = g_begin + blocks * kBatchBlockGroups + wave; g < g_end; g += kBatchWaves) {
+        BatchRegs r;
+        load(g, r);
+        step(g, r);
     }
 
     // Lane (kslot, j) holds vector 4*vq + kslot, rows 32T + 16h + n; the
