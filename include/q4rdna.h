@@ -163,9 +163,11 @@ int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, cons
 uint32_t q4rdna_policy_split_k(uint32_t rows, uint32_t columns, int device);
 
 /* ---- multi-tensor stack --------------------------------------------------
- * One launch that sweeps many independent GEMVs in order (a decode step's
- * weight streaming).  No reference counterpart: the reference launches one
- * kernel per tensor (source/q4rdna.cu:736-741). */
+ * One launch that sweeps many independent GEMVs (a decode step's weight
+ * streaming).  The GEMVs run concurrently and in an order the plan picks
+ * (longest K chunks first), so no descriptor's x, add or y may alias
+ * another's y.  No reference counterpart: the reference launches one kernel
+ * per tensor (source/q4rdna.cu:736-741). */
 typedef struct q4rdna_gemv_desc {
     q4rdna_weight weight;      /* W (the up projection for SwiGLU) */
     const uint8_t *gate_tiles; /* SwiGLU gate tiles of the same shape, or NULL */
