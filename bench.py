@@ -4,8 +4,8 @@
 Workload: one decode step's weight streaming for the Qwen3-8B 36-layer stack,
 252 distinct packed tensors (per layer q 4096x4096, k/v 1024x4096,
 o 4096x4096, gate/up 12288x4096, down 4096x12288; 3,689,938,944 packed
-bytes), swept in layer order at batch 1 with a fresh N(0,1) activation per
-tensor.  Weights are N(0, 0.02) fp32 generated on the GPU and packed by the
+bytes), given to the plan in layer order at batch 1 with a fresh N(0,1)
+activation per tensor (the plan sweeps the longest items first).  Weights are N(0, 0.02) fp32 generated on the GPU and packed by the
 GPU packer (bit-identical to the reference's native packer); everything is
 resident in HBM before timing.
 
@@ -22,8 +22,9 @@ prepare launch plus the GEMV sweep launch.  Printed: one JSON line with
               timed on host cores over a bounded sample of the same stack
 
 plus the same stack run the reference's way -- one GEMV launch per tensor --
-replayed from a HIP graph, and a full-size parity check of five tensors
-against the fp64 oracle.
+replayed from a HIP graph, the stack as the reference's fused dispatch (gate
+and up as one SwiGLU GEMV per layer: 216 GEMVs in one plan), and a full-size
+parity check of five tensors against the fp64 oracle.
 """
 from __future__ import annotations
 
@@ -166,6 +167,44 @@ def check_parity(tensors, picks):
         y64, a64 = O.gemv_f64(tiles, t["rows"], t["cols"], x)
         worst = max(worst, O.gemv_errors(t["y"].cpu().numpy(), y64, a64)["gate"])
     return worst
+
+
+def swiglu_stack(tensors, steps: int, warmup: int):
+    """The stack as the reference's fused dispatch: per layer q, k, v, o, one
+    SwiGLU GEMV for up and gate (two weight streams, the up projection's x)
+    and down -- 216 GEMVs over the same bytes.  Timed like the main plan; one
+    layer's SwiGLU output is checked against the fp64 oracle."""
+    import numpy as np
+    import torch
+    import oracle as O
+    from q4rdna import api
+
+    by = {t["name"]: t for t in tensors}
+    items, glu = [], []
+    for t in tensors:
+        if t["name"].endswith("ffn_gate.weight"):
+            continue
+        if t["name"].endswith("ffn_up.weight"):
+            gate = by[t["name"].replace("ffn_up", "ffn_gate")]
+            y = torch.empty_like(t["y"])
+            items.append((t["w"], t["x"], y, gate["w"]))
+            glu.append((t, gate, y))
+        else:
+            items.append((t["w"], t["x"], t["y"]))
+    plan = api.Plan(items)
+    ms, sweep_ms, _ = time_plan(plan, steps, warmup)
+    plan.close()
+    up, gate, y = glu[0]
+    x = up["x"].cpu().numpy()
+    u64, _ = O.gemv_f64(up["w"].tiles.cpu().numpy(), up["rows"], up["cols"], x)
+    g64, _ = O.gemv_f64(gate["w"].tiles.cpu().numpy(), gate["rows"], gate["cols"], x)
+    want = u64 * O.silu(g64)
+    rms = np.sqrt(np.mean(want ** 2))
+    err = np.abs(y.cpu().numpy().astype(np.float64) - want) / np.maximum(np.abs(want), 0.01 * rms)
+    nbytes = sum(algorithmic_bytes(t["rows"], t["cols"]) for t in tensors)
+    return dict(gemvs=len(items), us_per_stack=round(ms * 1000.0, 2),
+                gb_per_s=round(nbytes / (ms / 1000.0) / 1e9, 1), sweep_us=round(mean(sweep_ms) * 1000.0, 2),
+                parity_gate_max=float(err.max()))
 
 
 def cpu_baseline(tensors, budget_s: float):
@@ -480,6 +519,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-per-tensor", action="store_true")
+    ap.add_argument("--no-fused", action="store_true",
+                    help="skip the SwiGLU-fused stack (216 GEMVs, gate/up as one SwiGLU GEMV per layer)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc: five plan launches over the stack, then three plain 1 GiB "
                          "device copies (the FETCH_SIZE calibration); prints no JSON")
@@ -535,6 +576,12 @@ def main() -> int:
                           graph_replays_equal_eager=same)
         log(f"[bench] one launch per tensor (graph replay): {us:.1f} us per stack, replays equal eager: {same}")
 
+    fused = None
+    if not args.no_fused:
+        fused = swiglu_stack(tensors, args.steps // 2, args.warmup // 2)
+        log(f"[bench] SwiGLU-fused stack ({fused['gemvs']} GEMVs): {fused['us_per_stack']:.1f} us per step, "
+            f"parity gate {fused['parity_gate_max']:.2e}")
+
     value = stack_bytes / (ms_per_step / 1000.0) / 1e9
     achieved = stack_bytes / (sweep_us / 1e6) / 1e9
     traffic = load_traffic()
@@ -552,13 +599,14 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": f"qwen3-8b {args.layers}-layer stack: {len(tensors)} Q4_RDNA group-64 GEMVs at batch 1, "
-                               "layer order, fresh x per tensor, one multi-tensor plan per step",
+                               "descriptors in layer order, fresh x per tensor, one multi-tensor plan per step",
                    "tensors": len(tensors), "algorithmic_bytes_per_step": stack_bytes, "batch": 1},
         "us_per_stack": round(ms_per_step * 1000.0, 2),
         "pct_of_peak": round(100.0 * value / PEAK_GBS, 2),
         "prepare_us": round(prep_us, 2),
         "sweep_us": round(sweep_us, 2),
         "per_tensor_launches": per_tensor,
+        "swiglu_fused_stack": fused,
         "parity_gate_max": parity,
         "roofline": {"bound": "hbm", "kernel": "plan sweep", "achieved": round(achieved, 2), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
