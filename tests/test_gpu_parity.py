@@ -507,6 +507,33 @@ def test_batched_plan_matches_oracle(cuda, batch):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("batch", [1, 4])
+def test_plan_result_is_independent_of_descriptor_order(cuda, batch):
+    """The plan sweeps its GEMVs in an order of its own (longest K chunks
+    first); a GEMV's arithmetic does not depend on that order, so the same
+    descriptors given forwards and backwards give bit-identical outputs."""
+    shapes = [(256, 4096, None), (64, 12288, "add"), (96, 512, "glu"), (128, 8320, None), (32, 28672, None)]
+    descs = []
+    for i, (rows, cols, kind) in enumerate(shapes):
+        w = api.QWeight.from_tiles(dev_u8(random_tiles(rows, cols, 1200 + i)), rows, cols)
+        gate = api.QWeight.from_tiles(dev_u8(random_tiles(rows, cols, 1300 + i)), rows, cols) if kind == "glu" else None
+        add = dev_f32(np.stack([O.gaussian_x(rows, 1400 + i + v) for v in range(batch)])) if kind == "add" else None
+        x = dev_f32(np.stack([O.gaussian_x(cols, 1500 + i + v) for v in range(batch)]))
+        descs.append((w, x, gate, add, rows))
+    outs = []
+    for order in (list(range(len(descs))), list(reversed(range(len(descs))))):
+        ys = [torch.full((batch, d[4]), np.nan, device="cuda") for d in descs]
+        plan = api.Plan([(descs[i][0], descs[i][1], ys[i], descs[i][2], descs[i][3]) for i in order], batch=batch)
+        assert plan.launch()
+        torch.cuda.synchronize()
+        plan.close()
+        outs.append(ys)
+    for a, b in zip(*outs):
+        assert not torch.isnan(a).any()
+        assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
 def test_batched_plan_rows_are_independent_of_batch(cuda):
     """A vector's result depends only on that vector: the batch-4 result of
     vector v equals the batch-8 result of the same vector bit for bit (both
