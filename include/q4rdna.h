@@ -117,6 +117,14 @@ int q4rdna_scope_allows(const char *scope, const char *name);
  * on another device or a NULL weight returns NOT_APPLICABLE with nothing
  * launched.  x and y are contiguous fp32 device buffers (4-byte aligned).
  *
+ * Launches with split K use a scratch buffer per (device, stream).  The
+ * first call that needs more than the stream has allocates it (and waits
+ * for the device), so it cannot run under HIP graph capture: make one call
+ * of each shape on the stream before capturing.  Outgrown buffers are
+ * never freed, so a graph captured earlier stays valid.  Calls on one
+ * stream are ordered by it; a graph must not replay on another stream
+ * while the stream it was captured on runs such calls.
+ *
  * Replaces ggml_cuda_q4rdna_mul_mat (source/q4rdna.cuh:5-9, q4rdna.cu:713-745). */
 int q4rdna_mul_mat(const q4rdna_weight *w, const float *x, int64_t x_ne0, float *y, int64_t y_ne0,
                    void *stream);
@@ -189,7 +197,10 @@ int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device
 #define Q4RDNA_MAX_BATCH 8
 int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint32_t n, int device,
                              q4rdna_plan **out);
-/* Launch the whole plan on `stream` (prepare + sweep); allocates nothing. */
+/* Launch the whole plan on `stream` (prepare + sweep); allocates nothing.
+ * Launches of one plan share its digit buffers, split-K partials and
+ * counters, so they must not overlap: keep them on one stream or order
+ * them with events.  Different plans are independent. */
 int q4rdna_plan_launch(q4rdna_plan *plan, void *stream);
 /* The two launches of q4rdna_plan_launch, for callers that time or overlap
  * them: prepare converts every activation x into the plan's int8 digit

@@ -160,20 +160,19 @@ struct Workspace {
 
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+// Outgrown workspaces are kept, never freed: launches still queued and HIP
+// graphs captured earlier keep using their pointers.  A workspace at least
+// doubles when it grows, so few are ever retired.
+std::vector<Workspace> g_ws_retired;
 
 int get_workspace(int device, hipStream_t stream, size_t partial_floats, size_t counters, Workspace **out) {
     std::lock_guard<std::mutex> lock(g_ws_mu);
     Workspace &ws = g_ws[{device, stream}];
     if (ws.partial_floats < partial_floats || ws.counter_count < counters) {
-        const size_t pf = std::max(partial_floats, ws.partial_floats);
-        const size_t cc = std::max(counters, ws.counter_count);
+        const size_t pf = std::max(partial_floats, 2 * ws.partial_floats);
+        const size_t cc = std::max(counters, 2 * ws.counter_count);
         if (ws.partial != nullptr || ws.counters != nullptr) {
-            // Launches already queued on this stream may still use the old
-            // buffers: wait for them before releasing.
-            hipError_t e = hipStreamSynchronize(stream);
-            if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-            (void)hipFree(ws.partial);
-            (void)hipFree(ws.counters);
+            g_ws_retired.push_back(ws);
             ws = Workspace{};
         }
         float *p = nullptr;

@@ -607,6 +607,50 @@ def test_plan_and_mul_mat_replay_from_a_hip_graph(cuda):
 
 
 @pytest.mark.gpu
+def test_graph_replays_after_the_split_k_workspace_grows(cuda):
+    """A per-tensor launch captured into a HIP graph keeps the stream's
+    split-K workspace of that moment.  A larger shape on the same stream
+    afterwards grows the workspace; the outgrown buffers are kept, so the
+    graph still replays correctly (bit-identical to an eager call), and the
+    larger call is right too."""
+    small_rows, small_cols = 1024, 4096
+    big_rows, big_cols = 4096, 28672
+    assert api.policy_split_k(small_rows, small_cols) > 1
+    assert api.policy_split_k(big_rows, big_cols) * big_rows > api.policy_split_k(small_rows, small_cols) * small_rows
+    t_small = random_tiles(small_rows, small_cols, 1600)
+    t_big = random_tiles(big_rows, big_cols, 1601)
+    w_small = api.QWeight.from_tiles(dev_u8(t_small), small_rows, small_cols)
+    w_big = api.QWeight.from_tiles(dev_u8(t_big), big_rows, big_cols)
+    x_small = torch.empty(small_cols, device="cuda")
+    y_small = torch.empty(small_rows, device="cuda")
+    x_big = dev_f32(O.gaussian_x(big_cols, 1602))
+    y_big = torch.empty(big_rows, device="cuda")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        x_small.normal_()
+        api.mul_mat(w_small, x_small, y_small, stream=s.cuda_stream)  # allocates the small workspace
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        api.mul_mat(w_small, x_small, y_small, stream=s.cuda_stream)
+    for rep in range(3):
+        with torch.cuda.stream(s):
+            api.mul_mat(w_big, x_big, y_big, stream=s.cuda_stream)  # grows the workspace on the first pass
+            x_small.normal_()
+            api.mul_mat(w_small, x_small, y_small, stream=s.cuda_stream)
+        s.synchronize()
+        want = y_small.clone()
+        y_small.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+        s.synchronize()
+        assert torch.equal(y_small, want), rep
+    y64, a64 = O.gemv_f64(t_big, big_rows, big_cols, x_big.cpu().numpy())
+    assert O.gemv_errors(y_big.cpu().numpy(), y64, a64)["gate"] <= GATE_TOL
+
+
+@pytest.mark.gpu
 def test_plan_rejects_bad_descriptors(cuda):
     """Argument errors raise (negative status) and create nothing."""
     t = random_tiles(64, 128, 5)
