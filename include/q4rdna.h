@@ -86,6 +86,9 @@ int q4rdna_sidecar_inspect(const void *image, uint64_t image_size, uint64_t file
 int q4rdna_sidecar_open(const char *path, int device, q4rdna_sidecar **out);
 /* Same from an in-memory image of `size` bytes. */
 int q4rdna_sidecar_open_memory(const void *image, uint64_t size, int device, q4rdna_sidecar **out);
+/* Frees the sidecar's device buffer (hipFree waits for work in flight):
+ * every q4rdna_weight found in it is invalid afterwards.  Not for the
+ * process-wide sidecar of q4rdna_default_sidecar, which lives until exit. */
 void q4rdna_sidecar_close(q4rdna_sidecar *sidecar);
 uint32_t q4rdna_sidecar_count(const q4rdna_sidecar *sidecar);
 /* Entry metadata; name receives up to 64 bytes including the NUL. */
@@ -104,7 +107,9 @@ int q4rdna_weight_from_device(const void *tiles, uint32_t rows, uint32_t columns
                               q4rdna_weight *out);
 
 /* Sidecar named by LLAMA_Q4_RDNA_SIDECAR, opened once per process on the
- * first call (source/q4rdna.cu:683,698).  NULL when unset or invalid. */
+ * first call (source/q4rdna.cu:683,698) on that call's device, and kept
+ * until exit (never pass it to q4rdna_sidecar_close).  NULL when unset or
+ * invalid, or for another device. */
 q4rdna_sidecar *q4rdna_default_sidecar(int device);
 /* The reference's LLAMA_Q4_RDNA_SCOPE name filter (source/q4rdna.cu:685-696):
  * scope NULL/"" admits every name; "ffn", "qkv-fallback", "hotspot", "attn"
