@@ -44,8 +44,9 @@ constexpr int kWaves = 4;
 // and non-finite flag are reduced over the four lanes holding its k-slots
 // (lanes 4p .. 4p+3 of the wave); each element becomes A = rint(x*2^(22-E)),
 // split into three balanced int8 digits.  The lane writes the three digit
-// rows and a zero row as 64 contiguous bytes (row d at out + 16*d): the
-// single-vector and batched layouts both keep a k-slot's rows together.
+// rows as 48 contiguous bytes (row d at out + 16*d) of a 64-byte k-slot
+// record: the single-vector and batched layouts both keep a k-slot's rows
+// together.  Row 3 is never written: the MFMA rows it feeds are discarded.
 // `have` false: the lane reads nothing and writes nothing (its group lies
 // past the end); its three sibling lanes are in the same state.
 __device__ __forceinline__ void prep_kslot(const float *x, int kslot, bool have, gptr_u8 out, bool &bad, int &e_out) {
@@ -94,12 +95,10 @@ __device__ __forceinline__ void prep_kslot(const float *x, int kslot, bool have,
                          static_cast<int>(row[d][3])};
         *(gptr_wi32x4)(out + 16 * d) = v;
     }
-    const i32x4 zero = {0, 0, 0, 0};
-    *(gptr_wi32x4)(out + 48) = zero;
 }
 
 // Single-vector layout per group (kPrepBytes = 272): byte (kslot*4 + d)*16 + e
-// for digit d (d = 3 zero), the float factor 2^(E-26) at 256 (NaN for a
+// for digit d (d = 3 unused), the float factor 2^(E-26) at 256 (NaN for a
 // non-finite group).  Lane 4p + kslot of a wave converts k-slot kslot of the
 // wave's group p (16 groups per wave); group_x[g] is the address of global
 // group g's 64 activations (built by the host); its digits go to
@@ -458,7 +457,7 @@ __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ 
 //
 // With several activation vectors the A operand's rows carry the vectors
 // instead of groups: one MFMA multiplies 16 row sets of ONE group by the
-// three digits of up to four vectors (rows 4n + d of A, d = 3 zero), so
+// three digits of up to four vectors (rows 4n + d of A, d = 3 unused), so
 // every lane of D is useful for N = 4 and a second vector quad costs one more
 // MFMA per operand, not more loads or transposes.
 //  * Item: (256-row block = 8 row tiles, stream, K chunk of up to
