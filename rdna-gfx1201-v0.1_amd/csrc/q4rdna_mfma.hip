@@ -169,10 +169,7 @@ __device__ __forceinline__ uint32_t high_nibbles_x16(uint32_t t) { return t & 0x
 //    each row meet in LDS at the item's end.
 constexpr int kStepGroups = 4;                         // groups per wave step
 constexpr int kWgStepGroups = kWaves * kStepGroups;    // groups per workgroup step
-constexpr uint32_t kChunkBlockGroups = 64;                          // groups of one full block of steps
-constexpr uint32_t kBlockSteps = kChunkBlockGroups / kWgStepGroups;  // 4
-static_assert(kChunkGroups % kChunkBlockGroups == 0, "chunks are whole blocks of steps");
-static_assert(kBlockSteps == 4, "item_steps spells out a block's four steps");
+static_assert(kChunkGroups % kWgStepGroups == 0, "chunks are whole workgroup steps");
 // LDS bytes per staged tile: 1024 + a 64-byte skew.  Over the 252-tensor
 // stack the 64-byte skew measures 10.2M SQ_LDS_BANK_CONFLICT cycles against
 // 23.7M for a 32- or 128-byte skew and 50.9M for none, at equal sweep time.
@@ -333,57 +330,28 @@ struct Shared {
 };
 
 // The wave's steps of one item: rt0 / rt1 = the block's two row tiles.
-// Groups [g_begin, g_begin + 64 * blocks) are full 64-group blocks; the
-// rest up to g_end (fewer than 64 groups) is a short tail.
+// Full step t reads groups g_begin + 16t + 4*wave .. +3; the rest up to
+// g_end (fewer than 16 groups) is a short tail.  Each step's loads are issued after the
+// previous step's arithmetic, so a wave has one step in flight: with two
+// workgroups per CU that keeps about 12 MB in flight across the chip, and
+// measured faster than two steps in flight (more outstanding loads only
+// queue in the memory system once HBM is near its rate).
 __device__ __forceinline__ void item_steps(const uint8_t *rt0, const uint8_t *rt1, const uint8_t *prep,
                                            uint32_t g_begin, uint32_t g_end, int wave, int lane, const LaneRole &ln,
                                            uint8_t *stage, float (&acc)[16]) {
-    const uint32_t blocks = (g_end - g_begin) / kChunkBlockGroups;
-    if (blocks > 0) {
-        // Step t reads groups g_begin + 16t + 4*wave .. +3.  Two register
-        // sets in rotation: set t % 2 holds step t and, once step t's
-        // arithmetic is done, takes step t + 2, so each step waits only for
-        // its own loads while the next step's are in flight -- across the
-        // blocks of a chunk too.  Each block's four steps are straight-line
-        // code (the last block peeled off, so that no load is conditional),
-        // which lets the waitcnt pass count outstanding loads exactly;
-        // sched_barrier keeps a load from sinking below the arithmetic that
-        // follows it.
-        WaveRegs r[2];
-        auto load = [&](uint32_t t, WaveRegs &rr) {
-            const uint32_t g = g_begin + kWgStepGroups * t + kStepGroups * wave;
-            load_wave(rr, rt0 + static_cast<size_t>(g) * kTileBytes, rt1 + static_cast<size_t>(g) * kTileBytes,
-                      prep + static_cast<size_t>(g + ln.gB) * kPrepBytes + ln.a_offset,
-                      prep + static_cast<size_t>(g + ln.kslot) * kPrepBytes + 256, ln, lane);
-            __builtin_amdgcn_sched_barrier(0);
-        };
-        auto step = [&](WaveRegs &rr) {
-            restage(rr, stage, ln, lane);
-            compute_wave<false>(rr, acc, true);
-        };
-        load(0, r[0]);
-        load(1, r[1]);
-        uint32_t t = 0;
-        for (uint32_t b = 0; b + 1 < blocks; ++b, t += kBlockSteps) {
-            step(r[0]);
-            load(t + 2, r[0]);
-            step(r[1]);
-            load(t + 3, r[1]);
-            step(r[0]);
-            load(t + 4, r[0]);
-            step(r[1]);
-            load(t + 5, r[1]);
-        }
-        step(r[0]);
-        load(t + 2, r[0]);
-        step(r[1]);
-        load(t + 3, r[1]);
-        step(r[0]);
-        step(r[1]);
+    const uint32_t steps = (g_end - g_begin) / kWgStepGroups;
+    for (uint32_t t = 0; t < steps; ++t) {
+        const uint32_t g = g_begin + kWgStepGroups * t + kStepGroups * wave;
+        WaveRegs r;
+        load_wave(r, rt0 + static_cast<size_t>(g) * kTileBytes, rt1 + static_cast<size_t>(g) * kTileBytes,
+                  prep + static_cast<size_t>(g + ln.gB) * kPrepBytes + ln.a_offset,
+                  prep + static_cast<size_t>(g + ln.kslot) * kPrepBytes + 256, ln, lane);
+        restage(r, stage, ln, lane);
+        compute_wave<false>(r, acc, true);
     }
     // The short tail: the step's four groups are clamped to the chunk for
     // the loads, and those past its end are masked out.
-    for (uint32_t g = g_begin + blocks * kChunkBlockGroups + kStepGroups * wave; g < g_end; g += kWgStepGroups) {
+    for (uint32_t g = g_begin + steps * kWgStepGroups + kStepGroups * wave; g < g_end; g += kWgStepGroups) {
         const uint32_t gb = min(g + ln.gB, g_end - 1);
         const uint32_t gf = g + ln.kslot;
         WaveRegs rr;
@@ -499,9 +467,6 @@ __global__ __launch_bounds__(256) void prep_batch_kernel(const PlanDesc *__restr
 }
 
 constexpr int kBatchWaves = 4;  // eight waves per workgroup measured slower
-constexpr uint32_t kBatchBlockGroups = 64;  // groups of one unrolled block of steps
-static_assert(kBatchChunkGroups % kBatchBlockGroups == 0, "batched chunks are whole blocks of steps");
-static_assert((kBatchBlockGroups / kBatchWaves) % 2 == 0, "a block's first step lands in r[0]");
 
 // A wave's stage also receives its partial sums at the item's end (after
 // its last step, so the two uses never overlap): 4*NQ x 256 floats <= 8 KB.
@@ -599,31 +564,10 @@ __device__ __forceinline__ void run_batch_item(BatchShared<NQ> &sh, const PlanDe
         for (int c = 0; c < 8; ++c) r.code[c] = *reinterpret_cast<const i32x4 *>(sh.stage[wave] + lds_read + 128 * c);
         compute_batch<NQ>(r, a, f, acc);
     };
-    // Full 64-group blocks: 16 steps each, straight-line code with two steps
-    // in flight; a block's last step loads the next block's first, so the
-    // pipeline runs through a multi-block chunk (the last block peeled off,
-    // so that no load is conditional).  Then a short tail, one step at a
-    // time.
-    constexpr int kSteps = kBatchBlockGroups / kBatchWaves;
-    const uint32_t blocks = (g_end - g_begin) / kBatchBlockGroups;
-    if (blocks > 0) {
-        BatchRegs r[2];
-        load(g_begin + wave, r[0]);
-        uint32_t base = g_begin + wave;
-        for (uint32_t b = 0; b + 1 < blocks; ++b, base += kBatchBlockGroups) {
-#pragma unroll
-            for (int s = 0; s < kSteps; ++s) {
-                load(base + kBatchWaves * (s + 1), r[(s + 1) & 1]);
-                step(base + kBatchWaves * s, r[s & 1]);
-            }
-        }
-#pragma unroll
-        for (int s = 0; s < kSteps; ++s) {
-            if (s + 1 < kSteps) load(base + kBatchWaves * (s + 1), r[(s + 1) & 1]);
-            step(base + kBatchWaves * s, r[s & 1]);
-        }
-    }
-    for (uint32_t g = g_begin + blocks * kBatchBlockGroups + wave; g < g_end; g += kBatchWaves) {
+    // One step in flight per wave: each step's loads follow the previous
+    // step's arithmetic (two steps in flight measured slower, as in the
+    // single-vector sweep).
+    for (uint32_t g = g_begin + wave; g < g_end; g += kBatchWaves) {
         BatchRegs r;
         load(g, r);
         step(g, r);
