@@ -33,10 +33,12 @@ struct GemvArgs {
 // Device-side descriptor of one GEMV in a multi-tensor plan.  Work items are
 // (64-row block, stream, K chunk of up to kChunkGroups groups), numbered from
 // item_begin block-major, then stream (0 = w, 1 = the SwiGLU gate), then
-// chunk.  The activation is first converted into int8 digits (kPrepBytes per
-// 64-element group) in `prep`.  When a block has more than one item
-// (streams * chunks > 1) its items meet in partial[stream][chunk][rows]
-// through counters[block], zero between launches.
+// chunk; `per` items per block.  A single-vector SwiGLU GEMV whose rows fit
+// one chunk has per = 1: its item streams both weights.  The activation is
+// first converted into int8 digits (kPrepBytes per 64-element group) in
+// `prep`.  When a block has more than one item (per > 1) its items meet in
+// partial[stream][chunk][rows] through counters[block], zero between
+// launches.
 struct PlanDesc {
     const uint8_t *w;
     const uint8_t *gate;
@@ -52,6 +54,7 @@ struct PlanDesc {
     uint32_t group_begin;
     uint32_t chunks;
     uint32_t streams;
+    uint32_t per;
 };
 
 constexpr uint32_t kPrepBytes = 272;
@@ -72,8 +75,10 @@ uint32_t gemv_multi_stage_groups(uint32_t vectors);
 // items.  sched holds two zeroed counters owned by the plan (left zero after
 // every launch).
 hipError_t launch_prep(const float *const *group_x, uint8_t *prep, uint32_t groups, hipStream_t stream);
+// both_streams: some GEMV has per == 1 with a SwiGLU gate (one item streams
+// both weights); plans without such GEMVs run a sweep built without that path.
 hipError_t launch_plan(const PlanDesc *descs, uint32_t items, uint32_t workgroups, uint32_t *sched,
-                       hipStream_t stream);
+                       bool both_streams, hipStream_t stream);
 // Batched plans (n = 2..8 activation vectors per GEMV; x [n][cols],
 // y and add [n][rows]): items are 256-row blocks, prep holds
 // kBatchQuadBytesHost per (group, quad of 4 vectors).

@@ -276,27 +276,42 @@ struct ItemOut {
 // (+ add), or the part is published and the block's last part to arrive sums
 // the parts in chunk order (device-scope stores, drained before the arrival
 // count, so the summing workgroup sees them) and applies the epilogue.
-template <class SH>
-__device__ __forceinline__ void finish_item(SH &sh, const ItemOut &o, const float (&acc)[16], const LaneRole &ln,
-                                            int wave) {
+// GLU: the item streamed W into acc and the SwiGLU gate into gacc (a block
+// with one item); y = (sum + add) * silu(gate sum), the arrival chain's
+// epilogue without the chain.
+template <bool GLU, class SH>
+__device__ __forceinline__ void finish_item(SH &sh, const ItemOut &o, const float (&acc)[16],
+                                            const float (&gacc)[16], const LaneRole &ln, int wave) {
     if (ln.useful) {
-        float *dst = &sh.red[wave][ln.gB][32 * ln.T + 16 * ln.h];
+        float *dst = &sh.red[0][wave][ln.gB][32 * ln.T + 16 * ln.h];
 #pragma unroll
         for (int n = 0; n < 16; ++n) dst[n] = acc[n];
+        if constexpr (GLU) {
+            float *gdst = &sh.red[1][wave][ln.gB][32 * ln.T + 16 * ln.h];
+#pragma unroll
+            for (int n = 0; n < 16; ++n) gdst[n] = gacc[n];
+        }
     }
     __syncthreads();
     const uint32_t row = o.block * kBlockRows + threadIdx.x;
     const bool mine = threadIdx.x < kBlockRows && row < o.rows;
-    float v = 0.0f;
+    float v = 0.0f, gv = 0.0f;
     if (threadIdx.x < kBlockRows) {
 #pragma unroll
         for (int w = 0; w < kWaves; ++w)
 #pragma unroll
-            for (int g = 0; g < kStepGroups; ++g) v += sh.red[w][g][threadIdx.x];
+            for (int g = 0; g < kStepGroups; ++g) v += sh.red[0][w][g][threadIdx.x];
+        if constexpr (GLU) {
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w)
+#pragma unroll
+                for (int g = 0; g < kStepGroups; ++g) gv += sh.red[1][w][g][threadIdx.x];
+        }
     }
     if (o.per == 1) {
         if (mine) {
             if (o.add != nullptr) v += ((gptr_cf32)o.add)[row];
+            if constexpr (GLU) v *= silu(gv);
             __builtin_nontemporal_store(v, (gptr_f32)o.y + row);
         }
         return;
@@ -324,7 +339,7 @@ __device__ __forceinline__ void finish_item(SH &sh, const ItemOut &o, const floa
 
 struct Shared {
     uint8_t stage[kWaves][kStageBytes];
-    float red[kWaves][kStepGroups][kBlockRows];
+    float red[2][kWaves][kStepGroups][kBlockRows];  // [0] W, [1] the SwiGLU gate of a one-item block
     uint32_t next_item[2];
     uint32_t last;
 };
@@ -371,32 +386,48 @@ __device__ __forceinline__ void item_steps(const uint8_t *rt0, const uint8_t *rt
     }
 }
 
+// Item `local` of GEMV d.  A SwiGLU GEMV whose rows fit one chunk
+// (d.per == 1, two streams) streams W and then the gate over the same block
+// in one item and applies the epilogue itself; otherwise an item is one
+// stream's chunk and a block's items meet in the arrival chain.  BOTH: the
+// plan has such GEMVs (the sweep without them is built without that path).
+template <bool BOTH>
 __device__ __forceinline__ void run_item(Shared &sh, const PlanDesc &d, uint32_t local, const LaneRole &ln, int lane,
                                          int wave) {
     const uint32_t groups = d.cols / kGroup;
     const uint32_t tiles = d.rows / kTileRows;
-    const uint32_t per = d.streams * d.chunks;  // items of one 64-row block
+    const uint32_t per = d.per;  // items of one 64-row block
     const uint32_t block = local / per, part = local - block * per;
-    const uint32_t stream = part / d.chunks, chunk = part - stream * d.chunks;
+    const bool both = BOTH && d.streams > 1 && per == 1;
+    const uint32_t stream = both ? 0 : part / d.chunks, chunk = both ? 0 : part - stream * d.chunks;
     const uint32_t g_begin = chunk * kChunkGroups;
     const uint32_t g_end = min(groups, g_begin + kChunkGroups);
     // The second row tile of a block past the last one re-reads the last
     // (its rows are never written).
     const size_t row_tile_bytes = static_cast<size_t>(groups) * kTileBytes;
-    const uint8_t *rt0 = (stream != 0 ? d.gate : d.w) + static_cast<size_t>(2 * block) * row_tile_bytes;
-    const uint8_t *rt1 = 2 * block + 1 < tiles ? rt0 + row_tile_bytes : rt0;
-    float acc[16];
+    const size_t block_offset = static_cast<size_t>(2 * block) * row_tile_bytes;
+    const size_t second = 2 * block + 1 < tiles ? row_tile_bytes : 0;
+    const uint8_t *rt0 = (stream != 0 ? d.gate : d.w) + block_offset;
+    float acc[16], gacc[16];
 #pragma unroll
-    for (int n = 0; n < 16; ++n) acc[n] = 0.0f;
-    item_steps(rt0, rt1, d.prep, g_begin, g_end, wave, lane, ln, sh.stage[wave], acc);
-
+    for (int n = 0; n < 16; ++n) acc[n] = gacc[n] = 0.0f;
+    item_steps(rt0, rt0 + second, d.prep, g_begin, g_end, wave, lane, ln, sh.stage[wave], acc);
     ItemOut o{d.add, d.y, d.partial, d.counters, d.rows, block, part, per, d.chunks, d.streams};
-    finish_item(sh, o, acc, ln, wave);
+    if constexpr (BOTH) {
+        if (both) {
+            const uint8_t *gt0 = d.gate + block_offset;
+            item_steps(gt0, gt0 + second, d.prep, g_begin, g_end, wave, lane, ln, sh.stage[wave], gacc);
+            finish_item<true>(sh, o, acc, gacc, ln, wave);
+            return;
+        }
+    }
+    finish_item<false>(sh, o, acc, gacc, ln, wave);
 }
 
 // Persistent grid: items are taken in sweep order from sched[0] (the next
 // one is fetched while the current one runs); sched[1] counts finished
 // workgroups and the last one resets both.
+template <bool BOTH>
 __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ descs, uint32_t items,
                                                    uint32_t *__restrict__ sched) {
     __shared__ Shared sh;
@@ -410,7 +441,7 @@ __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ 
     while (item < items) {
         if (threadIdx.x == 0) sh.next_item[slot ^ 1] = add_agent(&sched[0], 1u);
         while (item >= descs[d + 1].item_begin) ++d;
-        run_item(sh, descs[d], item - descs[d].item_begin, ln, lane, wave);
+        run_item<BOTH>(sh, descs[d], item - descs[d].item_begin, ln, lane, wave);
         __syncthreads();
         slot ^= 1;
         item = sh.next_item[slot];
@@ -670,8 +701,11 @@ hipError_t launch_prep(const float *const *group_x, uint8_t *prep, uint32_t grou
 }
 
 hipError_t launch_plan(const PlanDesc *descs, uint32_t items, uint32_t workgroups, uint32_t *sched,
-                       hipStream_t stream) {
-    hipLaunchKernelGGL(plan_kernel, dim3(workgroups), dim3(256), 0, stream, descs, items, sched);
+                       bool both_streams, hipStream_t stream) {
+    if (both_streams)
+        hipLaunchKernelGGL(plan_kernel<true>, dim3(workgroups), dim3(256), 0, stream, descs, items, sched);
+    else
+        hipLaunchKernelGGL(plan_kernel<false>, dim3(workgroups), dim3(256), 0, stream, descs, items, sched);
     return hipGetLastError();
 }
 

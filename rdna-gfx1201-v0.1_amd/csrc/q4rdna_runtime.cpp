@@ -301,6 +301,7 @@ struct q4rdna_plan {
     uint32_t groups = 0;
     uint32_t workgroups = 0;
     uint32_t batch = 1;  // activation vectors per GEMV
+    bool both_streams = false;  // some SwiGLU GEMV runs both weight streams in one item
 };
 
 
@@ -632,7 +633,14 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
     // end of the sweep, where workgroups run out of items, deals short ones.
     std::vector<uint32_t> order(count);
     for (uint32_t i = 0; i < count; ++i) order[i] = i;
-    auto item_groups = [&](uint32_t i) { return std::min(descs[i].weight.columns / kGroup, chunk_groups); };
+    // A single-vector SwiGLU GEMV whose rows fit one chunk runs both weight
+    // streams in one item per block (no split-K partials).
+    auto both_streams = [&](uint32_t i) {
+        return n == 1 && descs[i].gate_tiles != nullptr && descs[i].weight.columns / kGroup <= chunk_groups;
+    };
+    auto item_groups = [&](uint32_t i) {
+        return std::min(descs[i].weight.columns / kGroup, chunk_groups) * (both_streams(i) ? 2u : 1u);
+    };
     std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) { return item_groups(a) > item_groups(b); });
     std::vector<q4rdna::PlanDesc> host(static_cast<size_t>(count) + 1);
     // Scratch layout: activation digits of every group in global group order
@@ -660,7 +668,8 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
         p.group_begin = static_cast<uint32_t>(groups);
         p.chunks = chunks;
         p.streams = streams;
-        if (chunks * streams > 1) {
+        p.per = both_streams(order[i]) ? 1u : chunks * streams;
+        if (p.per > 1) {
             part_off[i] = scratch;
             scratch += static_cast<uint64_t>(chunks) * streams * n * d.weight.rows * sizeof(float);
             scratch = (scratch + 255) & ~uint64_t(255);
@@ -668,7 +677,7 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
             scratch += static_cast<uint64_t>(blocks) * sizeof(uint32_t);
         }
         scratch = (scratch + 255) & ~uint64_t(255);
-        items += static_cast<uint64_t>(blocks) * chunks * streams;
+        items += static_cast<uint64_t>(blocks) * p.per;
         groups += g;
         if (items > 0xffffffffull || groups * n > 0xffffffffull) return fail(Q4RDNA_ERR_ARGUMENT, "plan too large");
     }
@@ -695,6 +704,7 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
     auto plan = std::make_unique<q4rdna_plan>();
     plan->device = device;
     plan->batch = n;
+    for (uint32_t i = 0; i < count; ++i) plan->both_streams |= host[i].streams > 1 && host[i].per == 1;
     plan->count = count;
     plan->items = static_cast<uint32_t>(items);
     plan->groups = static_cast<uint32_t>(groups);
@@ -718,7 +728,7 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
     }
     for (uint32_t i = 0; i < count; ++i) {
         host[i].prep = plan->scratch + static_cast<uint64_t>(host[i].group_begin) * prep_per_group;
-        if (host[i].chunks * host[i].streams > 1) {
+        if (host[i].per > 1) {
             host[i].partial = reinterpret_cast<float *>(plan->scratch + tail_off + part_off[i]);
             host[i].counters = reinterpret_cast<uint32_t *>(plan->scratch + tail_off + cnt_off[i]);
         }
@@ -767,7 +777,7 @@ int q4rdna_plan_sweep(q4rdna_plan *plan, void *stream) {
     if (rc != Q4RDNA_OK) return rc;
     if (plan->items == 0) return Q4RDNA_OK;
     hipError_t e = plan->batch == 1
-                       ? q4rdna::launch_plan(plan->descs, plan->items, plan->workgroups, plan->sched,
+                       ? q4rdna::launch_plan(plan->descs, plan->items, plan->workgroups, plan->sched, plan->both_streams,
                                              static_cast<hipStream_t>(stream))
                        : q4rdna::launch_plan_batch(plan->descs, plan->items, plan->batch, plan->workgroups,
                                                    plan->sched, static_cast<hipStream_t>(stream));

@@ -351,14 +351,16 @@ def test_sidecar_open_find_and_gemv(cuda, golden, tmp_path):
 # ----------------------------------------------------------------- multi-tensor plan
 
 def test_plan_matches_oracle(cuda):
-    # K chunks (up to 192 groups) made of 64-group blocks with and without a
+    # K chunks (up to 192 groups) of whole 16-group steps with and without a
     # short tail, tail-only chunks, several chunks (split-K) with a short
-    # last one, odd row-tile counts, and the add / SwiGLU epilogues over one
-    # and several chunks.
+    # last one, odd row-tile counts, and the add / SwiGLU epilogues: SwiGLU
+    # GEMVs of one chunk stream both weights in one item, longer ones meet
+    # in the split-K chain (12800 and 28672 columns).
     shapes = [(128, 512, None), (32, 512, None), (32, 512, "add"), (128, 512, None), (384, 512, "glu"),
               (128, 1536, None), (4096, 4096, None), (1024, 4096, "add"), (96, 4736, None),
               (160, 8192, "glu"), (96, 12288, "add"), (32, 4096, "glu"), (224, 28672, None),
-              (64, 12800, None), (96, 8320, "add"), (160, 4096, None), (224, 2048, "glu")]
+              (64, 12800, None), (96, 8320, "add"), (160, 4096, None), (224, 2048, "glu"),
+              (64, 12800, "glu"), (32, 28672, "glu"), (96, 12288, "glu")]
     items, checks = [], []
     for i, (rows, cols, kind) in enumerate(shapes):
         t = random_tiles(rows, cols, 100 + i)
