@@ -178,7 +178,7 @@ constexpr int kStageStride = 1088;
 constexpr int kStageBytes = 8 * kStageStride;          // per wave
 
 struct WaveRegs {
-    i32x4 code[8];  // tile c's 16 bytes at 16*lane (global), then the operand bytes (LDS)
+    i32x4 code[8];  // the operand bytes read from the LDS stage (a short tail first holds tile c's 16 bytes at 16*lane)
     i32x4 sc[2];    // the lane's 16 rows' fp16 scales
     i32x4 a;        // activation digits
     float f;        // group factor of the lane's D rows
@@ -344,11 +344,12 @@ struct Shared {
 
 // The wave's steps of one item: rt0 / rt1 = the block's two row tiles.
 // Full step t reads groups g_begin + 16t + 4*wave .. +3; the rest up to
-// g_end (fewer than 16 groups) is a short tail.  Each step's loads are issued after the
-// previous step's arithmetic, so a wave has one step in flight: with two
-// workgroups per CU that keeps about 12 MB in flight across the chip, and
-// measured faster than two steps in flight (more outstanding loads only
-// queue in the memory system once HBM is near its rate).
+// g_end (fewer than 16 groups) is a short tail.  Each step's loads are
+// issued after the previous step's arithmetic, so a wave has one step in
+// flight: with two workgroups per CU that keeps about 12 MB in flight
+// across the chip, and measured faster than two steps in flight (more
+// outstanding loads only queue in the memory system once HBM is near its
+// rate).
 __device__ __forceinline__ void item_steps(const uint8_t *rt0, const uint8_t *rt1, const uint8_t *prep,
                                            uint32_t g_begin, uint32_t g_end, int wave, int lane, const LaneRole &ln,
                                            uint8_t *stage, float (&acc)[16]) {
