@@ -34,7 +34,9 @@ struct GemvArgs {
 // (64-row block, stream, K chunk of up to kChunkGroups groups), numbered from
 // item_begin block-major, then stream (0 = w, 1 = the SwiGLU gate), then
 // chunk; `per` items per block.  A single-vector SwiGLU GEMV whose rows fit
-// one chunk has per = 1: its item streams both weights.  The activation is
+// one chunk has per = 1: its item streams both weights.  A `pair` GEMV
+// (single vector, no gate, rows of at most 64 groups) has items of two
+// 64-row blocks, numbered from item_begin, one per 128 rows.  The activation is
 // first converted into int8 digits (kPrepBytes per 64-element group) in
 // `prep`.  When a block has more than one item (per > 1) its items meet in
 // partial[stream][chunk][rows] through counters[block], zero between
@@ -55,6 +57,7 @@ struct PlanDesc {
     uint32_t chunks;
     uint32_t streams;
     uint32_t per;
+    uint32_t pair;  // single vector, no gate, one chunk: an item covers two 64-row blocks (128 rows)
 };
 
 constexpr uint32_t kPrepBytes = 272;

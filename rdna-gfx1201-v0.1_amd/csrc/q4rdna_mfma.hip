@@ -337,10 +337,42 @@ __device__ __forceinline__ void finish_item(SH &sh, const ItemOut &o, const floa
 
 struct Shared {
     uint8_t stage[kWaves][kStageBytes];
-    float red[2][kWaves][kStepGroups][kBlockRows];  // [0] W, [1] the SwiGLU gate of a one-item block
-    uint32_t next_item[2];
+    // [0] W, [1] the SwiGLU gate of a one-item block, or the two row blocks
+    // of a pair item
+    float red[2][kWaves][kStepGroups][kBlockRows];
     uint32_t last;
 };
+
+// The end of a pair item (two 64-row blocks, 128 rows from row
+// 128 * pair): acc0 / acc1 hold the blocks' sums in the useful lanes;
+// thread t < 128 sums row t's 16 (wave, group) partials in the fixed order
+// and writes y (+ add).
+__device__ __forceinline__ void finish_pair(Shared &sh, const PlanDesc &d, uint32_t pair, const float (&acc0)[16],
+                                            const float (&acc1)[16], const LaneRole &ln, int wave) {
+    if (ln.useful) {
+        float *dst0 = &sh.red[0][wave][ln.gB][32 * ln.T + 16 * ln.h];
+        float *dst1 = &sh.red[1][wave][ln.gB][32 * ln.T + 16 * ln.h];
+#pragma unroll
+        for (int n = 0; n < 16; ++n) {
+            dst0[n] = acc0[n];
+            dst1[n] = acc1[n];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 2 * kBlockRows) {
+        const uint32_t rb = threadIdx.x / kBlockRows, r = threadIdx.x % kBlockRows;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w)
+#pragma unroll
+            for (int g = 0; g < kStepGroups; ++g) v += sh.red[rb][w][g][r];
+        const uint32_t row = pair * 2 * kBlockRows + threadIdx.x;
+        if (row < d.rows) {
+            if (d.add != nullptr) v += ((gptr_cf32)d.add)[row];
+            __builtin_nontemporal_store(v, (gptr_f32)d.y + row);
+        }
+    }
+}
 
 // The wave's steps of one item: rt0 / rt1 = the block's two row tiles.
 // Full step t reads groups g_begin + 16t + 4*wave .. +3; the rest up to
@@ -406,6 +438,21 @@ __device__ __forceinline__ void run_item(Shared &sh, const PlanDesc &d, uint32_t
                                          int wave) {
     const uint32_t groups = d.cols / kGroup;
     const uint32_t tiles = d.rows / kTileRows;
+    const size_t row_tile_bytes = static_cast<size_t>(groups) * kTileBytes;
+    if (d.pair) {
+        // Item `local` covers row tiles 4*local .. +3 (those past the last
+        // re-read the last; their rows are never written), one K chunk.
+        const uint8_t *rt[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) rt[c] = d.w + static_cast<size_t>(min(4 * local + c, tiles - 1)) * row_tile_bytes;
+        float acc0[16], acc1[16];
+#pragma unroll
+        for (int n = 0; n < 16; ++n) acc0[n] = acc1[n] = 0.0f;
+        item_steps(rt[0], rt[1], d.prep, 0, groups, wave, lane, ln, sh.stage[wave], acc0);
+        item_steps(rt[2], rt[3], d.prep, 0, groups, wave, lane, ln, sh.stage[wave], acc1);
+        finish_pair(sh, d, local, acc0, acc1, ln, wave);
+        return;
+    }
     const uint32_t per = d.per;  // items of one 64-row block
     const uint32_t block = local / per, part = local - block * per;
     const bool both = BOTH && d.streams > 1 && per == 1;
@@ -414,7 +461,6 @@ __device__ __forceinline__ void run_item(Shared &sh, const PlanDesc &d, uint32_t
     const uint32_t g_end = min(groups, g_begin + kChunkGroups);
     // The second row tile of a block past the last one re-reads the last
     // (its rows are never written).
-    const size_t row_tile_bytes = static_cast<size_t>(groups) * kTileBytes;
     const size_t block_offset = static_cast<size_t>(2 * block) * row_tile_bytes;
     const size_t second = 2 * block + 1 < tiles ? row_tile_bytes : 0;
     const uint8_t *rt0 = (stream != 0 ? d.gate : d.w) + block_offset;
@@ -434,31 +480,21 @@ __device__ __forceinline__ void run_item(Shared &sh, const PlanDesc &d, uint32_t
     finish_item<false>(sh, o, acc, gacc, ln, wave);
 }
 
-// Persistent grid: items are taken in sweep order from sched[0] (the next
-// one is fetched while the current one runs); sched[1] counts finished
-// workgroups and the last one resets both.
+// Persistent grid: workgroup b takes items b, b + gridDim.x, ... in sweep
+// order (longest items first, as the plan orders its GEMVs).  This fixed
+// deal measured faster than an atomic item queue: while the sweep is
+// bandwidth-bound, workgroups that finish early leave the others more of
+// the bandwidth, and the queue's claim costs every item.
 template <bool BOTH>
-__global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ descs, uint32_t items,
-                                                   uint32_t *__restrict__ sched) {
+__global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ descs, uint32_t items) {
     __shared__ Shared sh;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const LaneRole ln = lane_role(lane);
-    if (threadIdx.x == 0) sh.next_item[0] = add_agent(&sched[0], 1u);
-    __syncthreads();
-    uint32_t item = sh.next_item[0];
     uint32_t d = 0;
-    int slot = 0;
-    while (item < items) {
-        if (threadIdx.x == 0) sh.next_item[slot ^ 1] = add_agent(&sched[0], 1u);
+    for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
         while (item >= descs[d + 1].item_begin) ++d;
         run_item<BOTH>(sh, descs[d], item - descs[d].item_begin, ln, lane, wave);
-        __syncthreads();
-        slot ^= 1;
-        item = sh.next_item[slot];
-    }
-    if (threadIdx.x == 0 && add_agent(&sched[1], 1u) == gridDim.x - 1) {
-        store_agent(&sched[0], 0u);
-        store_agent(&sched[1], 0u);
+        __syncthreads();  // the item's LDS reduction is read before the next item writes it
     }
 }
 
@@ -714,10 +750,11 @@ hipError_t launch_prep(const float *const *group_x, uint8_t *prep, uint32_t grou
 
 hipError_t launch_plan(const PlanDesc *descs, uint32_t items, uint32_t workgroups, uint32_t *sched,
                        bool both_streams, hipStream_t stream) {
+    (void)sched;  // the single-vector sweep deals items without a queue
     if (both_streams)
-        hipLaunchKernelGGL(plan_kernel<true>, dim3(workgroups), dim3(256), 0, stream, descs, items, sched);
+        hipLaunchKernelGGL(plan_kernel<true>, dim3(workgroups), dim3(256), 0, stream, descs, items);
     else
-        hipLaunchKernelGGL(plan_kernel<false>, dim3(workgroups), dim3(256), 0, stream, descs, items, sched);
+        hipLaunchKernelGGL(plan_kernel<false>, dim3(workgroups), dim3(256), 0, stream, descs, items);
     return hipGetLastError();
 }
 

@@ -638,8 +638,13 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
     auto both_streams = [&](uint32_t i) {
         return n == 1 && descs[i].gate_tiles != nullptr && descs[i].weight.columns / kGroup <= chunk_groups;
     };
+    // A single-vector GEMV with no gate whose rows fit one 64-group step
+    // block runs two 64-row blocks per item: half the item ends.
+    auto pairs = [&](uint32_t i) {
+        return n == 1 && descs[i].gate_tiles == nullptr && descs[i].weight.columns / kGroup <= 64;
+    };
     auto item_groups = [&](uint32_t i) {
-        return std::min(descs[i].weight.columns / kGroup, chunk_groups) * (both_streams(i) ? 2u : 1u);
+        return std::min(descs[i].weight.columns / kGroup, chunk_groups) * (both_streams(i) || pairs(i) ? 2u : 1u);
     };
     std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) { return item_groups(a) > item_groups(b); });
     std::vector<q4rdna::PlanDesc> host(static_cast<size_t>(count) + 1);
@@ -654,7 +659,9 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
         const q4rdna_gemv_desc &d = descs[order[i]];
         const uint32_t g = d.weight.columns / kGroup;
         const uint32_t chunks = (g + chunk_groups - 1) / chunk_groups;
-        const uint32_t blocks = (d.weight.rows + block_rows - 1) / block_rows;
+        const bool pair = pairs(order[i]);
+        const uint32_t item_rows = pair ? 2 * block_rows : block_rows;
+        const uint32_t blocks = (d.weight.rows + item_rows - 1) / item_rows;
         const uint32_t streams = d.gate_tiles != nullptr ? 2u : 1u;
         q4rdna::PlanDesc &p = host[i];
         p.w = d.weight.tiles;
@@ -668,7 +675,8 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
         p.group_begin = static_cast<uint32_t>(groups);
         p.chunks = chunks;
         p.streams = streams;
-        p.per = both_streams(order[i]) ? 1u : chunks * streams;
+        p.per = both_streams(order[i]) || pair ? 1u : chunks * streams;
+        p.pair = pair ? 1u : 0u;
         if (p.per > 1) {
             part_off[i] = scratch;
             scratch += static_cast<uint64_t>(chunks) * streams * n * d.weight.rows * sizeof(float);
