@@ -75,13 +75,14 @@ uint32_t gemv_multi_stage_groups(uint32_t vectors);
 // The prep launch converts every activation into digits: group g of the
 // plan (global numbering) reads its 64 floats at group_x[g] and writes
 // kPrepBytes at prep + g * kPrepBytes.  The plan launch then sweeps the
-// items.  sched holds two zeroed counters owned by the plan (left zero after
-// every launch).
+// items, dealt to its workgroups in a fixed order.  The batched sweep takes
+// items from a queue instead: sched holds its two zeroed counters, owned by
+// the plan (left zero after every launch).
 hipError_t launch_prep(const float *const *group_x, uint8_t *prep, uint32_t groups, hipStream_t stream);
 // both_streams: some GEMV has per == 1 with a SwiGLU gate (one item streams
 // both weights); plans without such GEMVs run a sweep built without that path.
-hipError_t launch_plan(const PlanDesc *descs, uint32_t items, uint32_t workgroups, uint32_t *sched,
-                       bool both_streams, hipStream_t stream);
+hipError_t launch_plan(const PlanDesc *descs, uint32_t items, uint32_t workgroups, bool both_streams,
+                       hipStream_t stream);
 // Batched plans (n = 2..8 activation vectors per GEMV; x [n][cols],
 // y and add [n][rows]): items are 256-row blocks, prep holds
 // kBatchQuadBytesHost per (group, quad of 4 vectors).

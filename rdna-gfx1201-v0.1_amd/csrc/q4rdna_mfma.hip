@@ -748,9 +748,8 @@ hipError_t launch_prep(const float *const *group_x, uint8_t *prep, uint32_t grou
     return hipGetLastError();
 }
 
-hipError_t launch_plan(const PlanDesc *descs, uint32_t items, uint32_t workgroups, uint32_t *sched,
-                       bool both_streams, hipStream_t stream) {
-    (void)sched;  // the single-vector sweep deals items without a queue
+hipError_t launch_plan(const PlanDesc *descs, uint32_t items, uint32_t workgroups, bool both_streams,
+                       hipStream_t stream) {
     if (both_streams)
         hipLaunchKernelGGL(plan_kernel<true>, dim3(workgroups), dim3(256), 0, stream, descs, items);
     else

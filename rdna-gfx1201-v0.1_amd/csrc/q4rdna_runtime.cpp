@@ -294,7 +294,7 @@ struct q4rdna_plan {
     int device = 0;
     q4rdna::PlanDesc *descs = nullptr;  // count + 1 (sentinel)
     uint8_t *scratch = nullptr;         // activation digits, split-K partials and counters
-    uint32_t *sched = nullptr;          // [next item, finished workgroups], zero between launches
+    uint32_t *sched = nullptr;          // batched sweeps' [next item, finished workgroups], zero between launches
     uint8_t *table = nullptr;           // prep launch's group table (in scratch)
     uint32_t count = 0;
     uint32_t items = 0;
@@ -785,7 +785,7 @@ int q4rdna_plan_sweep(q4rdna_plan *plan, void *stream) {
     if (rc != Q4RDNA_OK) return rc;
     if (plan->items == 0) return Q4RDNA_OK;
     hipError_t e = plan->batch == 1
-                       ? q4rdna::launch_plan(plan->descs, plan->items, plan->workgroups, plan->sched, plan->both_streams,
+                       ? q4rdna::launch_plan(plan->descs, plan->items, plan->workgroups, plan->both_streams,
                                              static_cast<hipStream_t>(stream))
                        : q4rdna::launch_plan_batch(plan->descs, plan->items, plan->batch, plan->workgroups,
                                                    plan->sched, static_cast<hipStream_t>(stream));
