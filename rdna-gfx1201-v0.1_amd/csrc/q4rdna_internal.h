@@ -75,14 +75,20 @@ uint32_t gemv_multi_stage_groups(uint32_t vectors);
 // The prep launch converts every activation into digits: group g of the
 // plan (global numbering) reads its 64 floats at group_x[g] and writes
 // kPrepBytes at prep + g * kPrepBytes.  The plan launch then sweeps the
-// items, dealt to its workgroups in a fixed order.  The batched sweep takes
-// items from a queue instead: sched holds its two zeroed counters, owned by
-// the plan (left zero after every launch).
+// items, dealt to its workgroups by the plan: workgroup b runs items
+// deal[workgroups + 1 + k] for k in [deal[b], deal[b + 1]), in increasing
+// item order.  The batched sweep takes items from a queue instead: sched
+// holds its two zeroed counters, owned by the plan (left zero after every
+// launch).
 hipError_t launch_prep(const float *const *group_x, uint8_t *prep, uint32_t groups, hipStream_t stream);
 // both_streams: some GEMV has per == 1 with a SwiGLU gate (one item streams
 // both weights); plans without such GEMVs run a sweep built without that path.
-hipError_t launch_plan(const PlanDesc *descs, uint32_t items, uint32_t workgroups, bool both_streams,
+hipError_t launch_plan(const PlanDesc *descs, const uint32_t *deal, uint32_t workgroups, bool both_streams,
                        hipStream_t stream);
+// Cost of one single-vector item in the deal: 1,088-byte tiles it streams
+// plus a fixed charge for its end (reduction, stores, barrier), measured at
+// about the time one workgroup takes to stream eight tiles.
+constexpr uint32_t kItemEndTiles = 8;
 // Batched plans (n = 2..8 activation vectors per GEMV; x [n][cols],
 // y and add [n][rows]): items are 256-row blocks, prep holds
 // kBatchQuadBytesHost per (group, quad of 4 vectors).

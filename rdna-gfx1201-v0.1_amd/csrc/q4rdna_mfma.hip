@@ -480,18 +480,23 @@ __device__ __forceinline__ void run_item(Shared &sh, const PlanDesc &d, uint32_t
     finish_item<false>(sh, o, acc, gacc, ln, wave);
 }
 
-// Persistent grid: workgroup b takes items b, b + gridDim.x, ... in sweep
-// order (longest items first, as the plan orders its GEMVs).  This fixed
+// Persistent grid: workgroup b runs the items the plan dealt it,
+// deal[gridDim.x + 1 + k] for k in [deal[b], deal[b + 1]), in increasing
+// item order (so longest GEMVs first, as the plan orders them).  A fixed
 // deal measured faster than an atomic item queue: while the sweep is
 // bandwidth-bound, workgroups that finish early leave the others more of
 // the bandwidth, and the queue's claim costs every item.
 template <bool BOTH>
-__global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ descs, uint32_t items) {
+__global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ descs,
+                                                   const uint32_t *__restrict__ deal) {
     __shared__ Shared sh;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const LaneRole ln = lane_role(lane);
+    const uint32_t *list = deal + gridDim.x + 1;
+    const uint32_t end = deal[blockIdx.x + 1];
     uint32_t d = 0;
-    for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
+    for (uint32_t k = deal[blockIdx.x]; k < end; ++k) {
+        const uint32_t item = list[k];
         while (item >= descs[d + 1].item_begin) ++d;
         run_item<BOTH>(sh, descs[d], item - descs[d].item_begin, ln, lane, wave);
         __syncthreads();  // the item's LDS reduction is read before the next item writes it
@@ -748,12 +753,12 @@ hipError_t launch_prep(const float *const *group_x, uint8_t *prep, uint32_t grou
     return hipGetLastError();
 }
 
-hipError_t launch_plan(const PlanDesc *descs, uint32_t items, uint32_t workgroups, bool both_streams,
+hipError_t launch_plan(const PlanDesc *descs, const uint32_t *deal, uint32_t workgroups, bool both_streams,
                        hipStream_t stream) {
     if (both_streams)
-        hipLaunchKernelGGL(plan_kernel<true>, dim3(workgroups), dim3(256), 0, stream, descs, items);
+        hipLaunchKernelGGL(plan_kernel<true>, dim3(workgroups), dim3(256), 0, stream, descs, deal);
     else
-        hipLaunchKernelGGL(plan_kernel<false>, dim3(workgroups), dim3(256), 0, stream, descs, items);
+        hipLaunchKernelGGL(plan_kernel<false>, dim3(workgroups), dim3(256), 0, stream, descs, deal);
     return hipGetLastError();
 }
 
