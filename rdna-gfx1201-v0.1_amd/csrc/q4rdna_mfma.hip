@@ -344,10 +344,10 @@ struct Shared {
 };
 
 // The end of a pair item (two 64-row blocks, 128 rows from row
-// 128 * pair): acc0 / acc1 hold the blocks' sums in the useful lanes;
+// 128 * o.block): acc0 / acc1 hold the blocks' sums in the useful lanes;
 // thread t < 128 sums row t's 16 (wave, group) partials in the fixed order
 // and writes y (+ add).
-__device__ __forceinline__ void finish_pair(Shared &sh, const PlanDesc &d, uint32_t pair, const float (&acc0)[16],
+__device__ __forceinline__ void finish_pair(Shared &sh, const ItemOut &o, const float (&acc0)[16],
                                             const float (&acc1)[16], const LaneRole &ln, int wave) {
     if (ln.useful) {
         float *dst0 = &sh.red[0][wave][ln.gB][32 * ln.T + 16 * ln.h];
@@ -366,12 +366,27 @@ __device__ __forceinline__ void finish_pair(Shared &sh, const PlanDesc &d, uint3
         for (int w = 0; w < kWaves; ++w)
 #pragma unroll
             for (int g = 0; g < kStepGroups; ++g) v += sh.red[rb][w][g][r];
-        const uint32_t row = pair * 2 * kBlockRows + threadIdx.x;
-        if (row < d.rows) {
-            if (d.add != nullptr) v += ((gptr_cf32)d.add)[row];
-            __builtin_nontemporal_store(v, (gptr_f32)d.y + row);
+        const uint32_t row = o.block * 2 * kBlockRows + threadIdx.x;
+        if (row < o.rows) {
+            if (o.add != nullptr) v += ((gptr_cf32)o.add)[row];
+            __builtin_nontemporal_store(v, (gptr_f32)o.y + row);
         }
     }
+}
+
+// Registers of one full wave step at group g (t0 / t1 = group g of the
+// block's two row tiles): the eight tiles' code bytes as restage() takes
+// them, the lane's scales, digits and factor.
+__device__ __forceinline__ void load_step_regs(WaveRegs &r, const uint8_t *t0, const uint8_t *t1, const uint8_t *prep,
+                                               uint32_t g, const LaneRole &ln, int lane) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+        r.code[c] = __builtin_nontemporal_load((gptr_i32x4)(((c & 1) ? t1 : t0) + (c >> 1) * kTileBytes + 64 + 16 * lane));
+    const uint8_t *own = (ln.T ? t1 : t0) + ln.gB * kTileBytes + 32 * ln.h;
+    r.sc[0] = __builtin_nontemporal_load((gptr_i32x4)own);
+    r.sc[1] = __builtin_nontemporal_load((gptr_i32x4)(own + 16));
+    r.a = *(gptr_i32x4)(prep + static_cast<size_t>(g + ln.gB) * kPrepBytes + ln.a_offset);
+    r.f = *(gptr_cf32)(prep + static_cast<size_t>(g + ln.kslot) * kPrepBytes + 256);
 }
 
 // The wave's steps of one item: rt0 / rt1 = the block's two row tiles.
@@ -384,9 +399,17 @@ __device__ __forceinline__ void finish_pair(Shared &sh, const PlanDesc &d, uint3
 // rate).
 __device__ __forceinline__ void item_steps(const uint8_t *rt0, const uint8_t *rt1, const uint8_t *prep,
                                            uint32_t g_begin, uint32_t g_end, int wave, int lane, const LaneRole &ln,
-                                           uint8_t *stage, float (&acc)[16]) {
+                                           uint8_t *stage, float (&acc)[16], WaveRegs &pre, bool have_pre) {
     const uint32_t steps = (g_end - g_begin) / kWgStepGroups;
-    for (uint32_t t = 0; t < steps; ++t) {
+    uint32_t t = 0;
+    if (have_pre) {
+        // Step 0 was loaded into registers across the previous item's end.
+        restage(pre, stage, ln, lane);
+        compute_wave<false>(pre, acc, true);
+        wait_lds_all();
+        t = 1;
+    }
+    for (; t < steps; ++t) {
         const uint32_t g = g_begin + kWgStepGroups * t + kStepGroups * wave;
         const uint8_t *t0 = rt0 + static_cast<size_t>(g) * kTileBytes;
         const uint8_t *t1 = rt1 + static_cast<size_t>(g) * kTileBytes;
@@ -428,56 +451,57 @@ __device__ __forceinline__ void item_steps(const uint8_t *rt0, const uint8_t *rt
     }
 }
 
-// Item `local` of GEMV d.  A SwiGLU GEMV whose rows fit one chunk
+// Item `local` of GEMV d, decoded.  A SwiGLU GEMV whose rows fit one chunk
 // (d.per == 1, two streams) streams W and then the gate over the same block
-// in one item and applies the epilogue itself; otherwise an item is one
-// stream's chunk and a block's items meet in the arrival chain.  BOTH: the
-// plan has such GEMVs (the sweep without them is built without that path).
+// in one item and applies the epilogue itself; a pair item streams its two
+// 64-row blocks one after the other; otherwise an item is one stream's
+// chunk and a block's items meet in the arrival chain.  rt[0..1] are the
+// row tiles of the first pass, rt[2..3] those of the second (pair and
+// both-streams items).  BOTH: the plan has both-streams GEMVs (the sweep
+// without them is built without that path).
+enum : uint32_t { kOnePass = 0, kPairPass = 1, kBothPass = 2 };
+struct ItemCtx {
+    const uint8_t *rt[4];
+    const uint8_t *prep;
+    uint32_t g_begin, g_end, kind;
+    ItemOut o;
+};
+
 template <bool BOTH>
-__device__ __forceinline__ void run_item(Shared &sh, const PlanDesc &d, uint32_t local, const LaneRole &ln, int lane,
-                                         int wave) {
+__device__ __forceinline__ ItemCtx decode_item(const PlanDesc &d, uint32_t local) {
+    ItemCtx c;
     const uint32_t groups = d.cols / kGroup;
     const uint32_t tiles = d.rows / kTileRows;
     const size_t row_tile_bytes = static_cast<size_t>(groups) * kTileBytes;
+    c.prep = d.prep;
     if (d.pair) {
-        // Item `local` covers row tiles 4*local .. +3 (those past the last
-        // re-read the last; their rows are never written), one K chunk.
-        const uint8_t *rt[4];
+        // Row tiles 4*local .. +3 (those past the last re-read the last;
+        // their rows are never written), one K chunk.
 #pragma unroll
-        for (int c = 0; c < 4; ++c) rt[c] = d.w + static_cast<size_t>(min(4 * local + c, tiles - 1)) * row_tile_bytes;
-        float acc0[16], acc1[16];
-#pragma unroll
-        for (int n = 0; n < 16; ++n) acc0[n] = acc1[n] = 0.0f;
-        item_steps(rt[0], rt[1], d.prep, 0, groups, wave, lane, ln, sh.stage[wave], acc0);
-        item_steps(rt[2], rt[3], d.prep, 0, groups, wave, lane, ln, sh.stage[wave], acc1);
-        finish_pair(sh, d, local, acc0, acc1, ln, wave);
-        return;
+        for (int i = 0; i < 4; ++i) c.rt[i] = d.w + static_cast<size_t>(min(4 * local + i, tiles - 1)) * row_tile_bytes;
+        c.g_begin = 0;
+        c.g_end = groups;
+        c.kind = kPairPass;
+        c.o = ItemOut{d.add, d.y, nullptr, nullptr, d.rows, local, 0, 1, 1, 1};
+        return c;
     }
     const uint32_t per = d.per;  // items of one 64-row block
     const uint32_t block = local / per, part = local - block * per;
     const bool both = BOTH && d.streams > 1 && per == 1;
     const uint32_t stream = both ? 0 : part / d.chunks, chunk = both ? 0 : part - stream * d.chunks;
-    const uint32_t g_begin = chunk * kChunkGroups;
-    const uint32_t g_end = min(groups, g_begin + kChunkGroups);
+    c.g_begin = chunk * kChunkGroups;
+    c.g_end = min(groups, c.g_begin + kChunkGroups);
     // The second row tile of a block past the last one re-reads the last
     // (its rows are never written).
     const size_t block_offset = static_cast<size_t>(2 * block) * row_tile_bytes;
     const size_t second = 2 * block + 1 < tiles ? row_tile_bytes : 0;
-    const uint8_t *rt0 = (stream != 0 ? d.gate : d.w) + block_offset;
-    float acc[16], gacc[16];
-#pragma unroll
-    for (int n = 0; n < 16; ++n) acc[n] = gacc[n] = 0.0f;
-    item_steps(rt0, rt0 + second, d.prep, g_begin, g_end, wave, lane, ln, sh.stage[wave], acc);
-    ItemOut o{d.add, d.y, d.partial, d.counters, d.rows, block, part, per, d.chunks, d.streams};
-    if constexpr (BOTH) {
-        if (both) {
-            const uint8_t *gt0 = d.gate + block_offset;
-            item_steps(gt0, gt0 + second, d.prep, g_begin, g_end, wave, lane, ln, sh.stage[wave], gacc);
-            finish_item<true>(sh, o, acc, gacc, ln, wave);
-            return;
-        }
-    }
-    finish_item<false>(sh, o, acc, gacc, ln, wave);
+    c.rt[0] = (stream != 0 ? d.gate : d.w) + block_offset;
+    c.rt[1] = c.rt[0] + second;
+    c.rt[2] = both ? d.gate + block_offset : c.rt[0];
+    c.rt[3] = c.rt[2] + second;
+    c.kind = both ? kBothPass : kOnePass;
+    c.o = ItemOut{d.add, d.y, d.partial, d.counters, d.rows, block, part, per, d.chunks, d.streams};
+    return c;
 }
 
 // Persistent grid: workgroup b runs the items the plan dealt it,
@@ -486,6 +510,9 @@ __device__ __forceinline__ void run_item(Shared &sh, const PlanDesc &d, uint32_t
 // deal measured faster than an atomic item queue: while the sweep is
 // bandwidth-bound, workgroups that finish early leave the others more of
 // the bandwidth, and the queue's claim costs every item.
+// Across an item's end (the barrier, the reduction and the stores) each
+// wave already has the next item's first step in flight, in registers: the
+// end would otherwise leave the workgroup with no loads outstanding.
 template <bool BOTH>
 __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ descs,
                                                    const uint32_t *__restrict__ deal) {
@@ -494,12 +521,46 @@ __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ 
     const LaneRole ln = lane_role(lane);
     const uint32_t *list = deal + gridDim.x + 1;
     const uint32_t end = deal[blockIdx.x + 1];
+    uint32_t k = deal[blockIdx.x];
+    if (k >= end) return;
     uint32_t d = 0;
-    for (uint32_t k = deal[blockIdx.x]; k < end; ++k) {
-        const uint32_t item = list[k];
+    auto locate = [&](uint32_t item) {
         while (item >= descs[d + 1].item_begin) ++d;
-        run_item<BOTH>(sh, descs[d], item - descs[d].item_begin, ln, lane, wave);
+        return decode_item<BOTH>(descs[d], item - descs[d].item_begin);
+    };
+    ItemCtx cur = locate(list[k]);
+    WaveRegs pre;
+    bool have_pre = false;
+    for (;;) {
+        float acc[16], acc1[16];
+#pragma unroll
+        for (int n = 0; n < 16; ++n) acc[n] = acc1[n] = 0.0f;
+        item_steps(cur.rt[0], cur.rt[1], cur.prep, cur.g_begin, cur.g_end, wave, lane, ln, sh.stage[wave], acc, pre,
+                   have_pre);
+        if (cur.kind != kOnePass)
+            item_steps(cur.rt[2], cur.rt[3], cur.prep, cur.g_begin, cur.g_end, wave, lane, ln, sh.stage[wave], acc1,
+                       pre, false);
+        ++k;
+        ItemCtx next;
+        have_pre = false;
+        if (k < end) {
+            next = locate(list[k]);
+            if (next.g_end - next.g_begin >= kWgStepGroups) {
+                const uint32_t g = next.g_begin + kStepGroups * wave;
+                load_step_regs(pre, next.rt[0] + static_cast<size_t>(g) * kTileBytes,
+                               next.rt[1] + static_cast<size_t>(g) * kTileBytes, next.prep, g, ln, lane);
+                have_pre = true;
+            }
+        }
+        if (cur.kind == kPairPass)
+            finish_pair(sh, cur.o, acc, acc1, ln, wave);
+        else if (BOTH && cur.kind == kBothPass)
+            finish_item<true>(sh, cur.o, acc, acc1, ln, wave);
+        else
+            finish_item<false>(sh, cur.o, acc, acc1, ln, wave);
         __syncthreads();  // the item's LDS reduction is read before the next item writes it
+        if (k >= end) break;
+        cur = next;
     }
 }
 
