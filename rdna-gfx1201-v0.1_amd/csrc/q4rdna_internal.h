@@ -75,9 +75,10 @@ uint32_t gemv_multi_stage_groups(uint32_t vectors);
 // The prep launch converts every activation into digits: group g of the
 // plan (global numbering) reads its 64 floats at group_x[g] and writes
 // kPrepBytes at prep + g * kPrepBytes.  The plan launch then sweeps the
-// items, dealt to its workgroups by the plan: workgroup b runs items
-// deal[workgroups + 1 + k] for k in [deal[b], deal[b + 1]), in increasing
-// item order.  The batched sweep takes items from a queue instead: sched
+// items, dealt to its workgroups by the plan: deal holds workgroups + 1
+// offsets (padded to an even count), then one (descriptor index, item within
+// the descriptor) pair of uint32 per item; workgroup b runs entries
+// [deal[b], deal[b + 1]), in increasing item order.  The batched sweep takes items from a queue instead: sched
 // holds its two zeroed counters, owned by the plan (left zero after every
 // launch).
 hipError_t launch_prep(const float *const *group_x, uint8_t *prep, uint32_t groups, hipStream_t stream);

@@ -504,12 +504,12 @@ __device__ __forceinline__ ItemCtx decode_item(const PlanDesc &d, uint32_t local
     return c;
 }
 
-// Persistent grid: workgroup b runs the items the plan dealt it,
-// deal[gridDim.x + 1 + k] for k in [deal[b], deal[b + 1]), in increasing
-// item order (so longest GEMVs first, as the plan orders them).  A fixed
-// deal measured faster than an atomic item queue: while the sweep is
-// bandwidth-bound, workgroups that finish early leave the others more of
-// the bandwidth, and the queue's claim costs every item.
+// Persistent grid: workgroup b runs the items the plan dealt it, entries
+// [deal[b], deal[b + 1]) of the (descriptor, item within it) pairs that
+// follow the gridDim.x + 1 offsets (padded to an even count), longest GEMVs
+// first, as the plan orders them.  A fixed deal measured faster than an atomic item queue: while the
+// sweep is bandwidth-bound, workgroups that finish early leave the others
+// more of the bandwidth, and the queue's claim costs every item.
 // Across an item's end (the barrier, the reduction and the stores) each
 // wave already has the next item's first step in flight, in registers: the
 // end would otherwise leave the workgroup with no loads outstanding.
@@ -519,19 +519,18 @@ __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ 
     __shared__ Shared sh;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const LaneRole ln = lane_role(lane);
-    const uint32_t *list = deal + gridDim.x + 1;
+    const uint2 *entry = reinterpret_cast<const uint2 *>(deal + ((gridDim.x + 2) & ~1u));
     const uint32_t end = deal[blockIdx.x + 1];
     uint32_t k = deal[blockIdx.x];
     if (k >= end) return;
-    uint32_t d = 0;
-    auto locate = [&](uint32_t item) {
-        while (item >= descs[d + 1].item_begin) ++d;
-        return decode_item<BOTH>(descs[d], item - descs[d].item_begin);
-    };
-    ItemCtx cur = locate(list[k]);
+    auto locate = [&](uint2 e) { return decode_item<BOTH>(descs[e.x], e.y); };
+    ItemCtx cur = locate(entry[k]);
     WaveRegs pre;
     bool have_pre = false;
     for (;;) {
+        // The next entry is read now, so that only its descriptor's loads
+        // stand between this item's last step and the next item's loads.
+        const uint2 next_entry = k + 1 < end ? entry[k + 1] : make_uint2(0, 0);
         float acc[16], acc1[16];
 #pragma unroll
         for (int n = 0; n < 16; ++n) acc[n] = acc1[n] = 0.0f;
@@ -544,7 +543,7 @@ __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ 
         ItemCtx next;
         have_pre = false;
         if (k < end) {
-            next = locate(list[k]);
+            next = locate(next_entry);
             if (next.g_end - next.g_begin >= kWgStepGroups) {
                 const uint32_t g = next.g_begin + kStepGroups * wave;
                 load_step_regs(pre, next.rt[0] + static_cast<size_t>(g) * kTileBytes,

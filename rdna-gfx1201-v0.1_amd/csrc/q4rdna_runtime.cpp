@@ -616,8 +616,8 @@ namespace {
 // stack (2,304 items of 192 groups x 64 rows, 9,792 of 64 groups x 128
 // rows, 512 workgroups) a round-robin deal leaves the most-loaded workgroup
 // 53 units of 64 groups x 64 rows against a mean of 51.75; this one 52.
-// Returns offsets[workgroups + 1], then the item lists, each in increasing
-// item order.
+// Returns per workgroup the offset of its list (workgroups + 1 offsets)
+// and the lists, each in increasing item order.
 std::vector<uint32_t> deal_items(const std::vector<uint32_t> &cost, uint32_t workgroups) {
     std::vector<std::vector<uint32_t>> own(workgroups);
     std::vector<uint64_t> load(workgroups, 0);
@@ -817,7 +817,20 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
                 cost[item] = row_tiles * chunk_g + q4rdna::kItemEndTiles;
             }
         }
-        deal = deal_items(cost, workgroups);
+        // The kernel's form: the offsets (padded to 8 bytes), then per item
+        // its descriptor index and its index within the descriptor.
+        const std::vector<uint32_t> lists = deal_items(cost, workgroups);
+        const uint32_t head = (workgroups + 2) & ~1u;
+        deal.assign(head + 2 * items, 0);
+        std::copy(lists.begin(), lists.begin() + workgroups + 1, deal.begin());
+        std::vector<uint32_t> owner(items);
+        for (uint32_t i = 0; i < count; ++i)
+            for (uint32_t item = host[i].item_begin; item < host[i + 1].item_begin; ++item) owner[item] = i;
+        for (uint64_t k = 0; k < items; ++k) {
+            const uint32_t item = lists[workgroups + 1 + k];
+            deal[head + 2 * k] = owner[item];
+            deal[head + 2 * k + 1] = item - host[owner[item]].item_begin;
+        }
     }
     const uint64_t deal_off = (table_off + table_bytes + 255) & ~uint64_t(255);
     const uint64_t tail_off = (deal_off + deal.size() * sizeof(uint32_t) + 255) & ~uint64_t(255);
