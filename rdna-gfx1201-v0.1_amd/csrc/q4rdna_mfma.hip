@@ -269,6 +269,10 @@ struct ItemOut {
     uint32_t rows, block, part, per, chunks, streams;
 };
 
+// One item's reduction buffer: [0] W, [1] the SwiGLU gate of a one-item
+// block, or the two row blocks of a pair item.
+using Red = float[2][kWaves][kStepGroups][kBlockRows];
+
 // The useful lanes publish their 16 rows; thread t < 64 then sums row t's 16
 // (wave, group) partials in a fixed order and finishes the item: y = sum
 // (+ add), or the part is published and the block's last part to arrive sums
@@ -277,15 +281,16 @@ struct ItemOut {
 // GLU: the item streamed W into acc and the SwiGLU gate into gacc (a block
 // with one item); y = (sum + add) * silu(gate sum), the arrival chain's
 // epilogue without the chain.
-template <bool GLU, class SH>
-__device__ __forceinline__ void finish_item(SH &sh, const ItemOut &o, const float (&acc)[16],
+// `last` is the workgroup's word for the arrival result.
+template <bool GLU>
+__device__ __forceinline__ void finish_item(Red &red, uint32_t &last, const ItemOut &o, const float (&acc)[16],
                                             const float (&gacc)[16], const LaneRole &ln, int wave) {
     if (ln.useful) {
-        float *dst = &sh.red[0][wave][ln.gB][32 * ln.T + 16 * ln.h];
+        float *dst = &red[0][wave][ln.gB][32 * ln.T + 16 * ln.h];
 #pragma unroll
         for (int n = 0; n < 16; ++n) dst[n] = acc[n];
         if constexpr (GLU) {
-            float *gdst = &sh.red[1][wave][ln.gB][32 * ln.T + 16 * ln.h];
+            float *gdst = &red[1][wave][ln.gB][32 * ln.T + 16 * ln.h];
 #pragma unroll
             for (int n = 0; n < 16; ++n) gdst[n] = gacc[n];
         }
@@ -298,12 +303,12 @@ __device__ __forceinline__ void finish_item(SH &sh, const ItemOut &o, const floa
 #pragma unroll
         for (int w = 0; w < kWaves; ++w)
 #pragma unroll
-            for (int g = 0; g < kStepGroups; ++g) v += sh.red[0][w][g][threadIdx.x];
+            for (int g = 0; g < kStepGroups; ++g) v += red[0][w][g][threadIdx.x];
         if constexpr (GLU) {
 #pragma unroll
             for (int w = 0; w < kWaves; ++w)
 #pragma unroll
-                for (int g = 0; g < kStepGroups; ++g) gv += sh.red[1][w][g][threadIdx.x];
+                for (int g = 0; g < kStepGroups; ++g) gv += red[1][w][g][threadIdx.x];
         }
     }
     if (o.per == 1) {
@@ -317,9 +322,9 @@ __device__ __forceinline__ void finish_item(SH &sh, const ItemOut &o, const floa
     if (mine) store_agent(&o.partial[static_cast<size_t>(o.part) * o.rows + row], v);
     wait_stores();
     __syncthreads();
-    if (threadIdx.x == 0) sh.last = (add_agent(&o.counters[o.block], 1u) == o.per - 1) ? 1u : 0u;
+    if (threadIdx.x == 0) last = (add_agent(&o.counters[o.block], 1u) == o.per - 1) ? 1u : 0u;
     __syncthreads();
-    if (sh.last == 0u) return;
+    if (last == 0u) return;
     if (mine) {
         float u = load_agent(&o.partial[row]);
         for (uint32_t k = 1; k < o.chunks; ++k) u += load_agent(&o.partial[static_cast<size_t>(k) * o.rows + row]);
@@ -335,11 +340,13 @@ __device__ __forceinline__ void finish_item(SH &sh, const ItemOut &o, const floa
     if (threadIdx.x == 0) store_agent(&o.counters[o.block], 0u);
 }
 
+// The reduction buffers alternate by item parity, so an item needs one
+// workgroup barrier: the next item's writes go to the other buffer, and the
+// one after that's writes follow that item's barrier, which the waves still
+// summing this item reach only once they are done.
 struct Shared {
     uint8_t stage[kWaves][kStageBytes];
-    // [0] W, [1] the SwiGLU gate of a one-item block, or the two row blocks
-    // of a pair item
-    float red[2][kWaves][kStepGroups][kBlockRows];
+    Red red[2];
     uint32_t last;
 };
 
@@ -347,11 +354,11 @@ struct Shared {
 // 128 * o.block): acc0 / acc1 hold the blocks' sums in the useful lanes;
 // thread t < 128 sums row t's 16 (wave, group) partials in the fixed order
 // and writes y (+ add).
-__device__ __forceinline__ void finish_pair(Shared &sh, const ItemOut &o, const float (&acc0)[16],
+__device__ __forceinline__ void finish_pair(Red &red, const ItemOut &o, const float (&acc0)[16],
                                             const float (&acc1)[16], const LaneRole &ln, int wave) {
     if (ln.useful) {
-        float *dst0 = &sh.red[0][wave][ln.gB][32 * ln.T + 16 * ln.h];
-        float *dst1 = &sh.red[1][wave][ln.gB][32 * ln.T + 16 * ln.h];
+        float *dst0 = &red[0][wave][ln.gB][32 * ln.T + 16 * ln.h];
+        float *dst1 = &red[1][wave][ln.gB][32 * ln.T + 16 * ln.h];
 #pragma unroll
         for (int n = 0; n < 16; ++n) {
             dst0[n] = acc0[n];
@@ -365,7 +372,7 @@ __device__ __forceinline__ void finish_pair(Shared &sh, const ItemOut &o, const 
 #pragma unroll
         for (int w = 0; w < kWaves; ++w)
 #pragma unroll
-            for (int g = 0; g < kStepGroups; ++g) v += sh.red[rb][w][g][r];
+            for (int g = 0; g < kStepGroups; ++g) v += red[rb][w][g][r];
         const uint32_t row = o.block * 2 * kBlockRows + threadIdx.x;
         if (row < o.rows) {
             if (o.add != nullptr) v += ((gptr_cf32)o.add)[row];
@@ -527,6 +534,7 @@ __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ 
     ItemCtx cur = locate(entry[k]);
     WaveRegs pre;
     bool have_pre = false;
+    uint32_t parity = 0;
     for (;;) {
         // The next entry is read now, so that only its descriptor's loads
         // stand between this item's last step and the next item's loads.
@@ -551,13 +559,14 @@ __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ 
                 have_pre = true;
             }
         }
+        Red &red = sh.red[parity];
+        parity ^= 1;
         if (cur.kind == kPairPass)
-            finish_pair(sh, cur.o, acc, acc1, ln, wave);
+            finish_pair(red, cur.o, acc, acc1, ln, wave);
         else if (BOTH && cur.kind == kBothPass)
-            finish_item<true>(sh, cur.o, acc, acc1, ln, wave);
+            finish_item<true>(red, sh.last, cur.o, acc, acc1, ln, wave);
         else
-            finish_item<false>(sh, cur.o, acc, acc1, ln, wave);
-        __syncthreads();  // the item's LDS reduction is read before the next item writes it
+            finish_item<false>(red, sh.last, cur.o, acc, acc1, ln, wave);
         if (k >= end) break;
         cur = next;
     }
