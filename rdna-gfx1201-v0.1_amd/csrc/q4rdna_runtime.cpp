@@ -608,28 +608,40 @@ int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, cons
 namespace {
 
 // Deal of a single-vector sweep's items to its workgroups.  cost[i] is item
-// i's weight in the sweep (tiles streamed plus the item end).  Items go in
-// order, longest GEMV first, each to the least-loaded workgroup; then moves
-// and swaps of one item between the most-loaded workgroup and a lighter one
-// lower the most-loaded while any does (each strictly lowers the sum of
-// squared loads, so this ends; it is capped besides).  On the Qwen3-8B
-// stack (2,304 items of 192 groups x 64 rows, 9,792 of 64 groups x 128
-// rows, 512 workgroups) a round-robin deal leaves the most-loaded workgroup
-// 53 units of 64 groups x 64 rows against a mean of 51.75; this one 52.
+// i's weight in the sweep (tiles streamed plus the item end); weight[b] is
+// workgroup b's time per unit of cost (1024 = 1).  Items go in order,
+// longest GEMV first, each to the workgroup that would finish it first;
+// then moves and swaps of one item between the latest workgroup and an
+// earlier one bring the latest forward while any does (each lowers the
+// sorted vector of finish times, so this ends; it is capped besides).  On
+// the Qwen3-8B stack (2,304 items of 192 groups x 64 rows, 9,792 of 64
+// groups x 128 rows, 512 workgroups, equal weights) a round-robin deal
+// leaves the most-loaded workgroup 53 units of 64 groups x 64 rows against
+// a mean of 51.75; this one 52.
 // Returns per workgroup the offset of its list (workgroups + 1 offsets)
 // and the lists, each in increasing item order.
-std::vector<uint32_t> deal_items(const std::vector<uint32_t> &cost, uint32_t workgroups) {
+std::vector<uint32_t> deal_items(const std::vector<uint32_t> &cost, const std::vector<uint32_t> &weight) {
+    const uint32_t workgroups = static_cast<uint32_t>(weight.size());
     std::vector<std::vector<uint32_t>> own(workgroups);
     std::vector<uint64_t> load(workgroups, 0);
+    auto finish = [&](uint32_t b, uint64_t l) { return l * weight[b]; };
+    // One heap of workgroups per distinct weight, least loaded on top.
     using Slot = std::pair<uint64_t, uint32_t>;
-    std::priority_queue<Slot, std::vector<Slot>, std::greater<Slot>> lightest;
-    for (uint32_t b = 0; b < workgroups; ++b) lightest.push({0, b});
+    using Heap = std::priority_queue<Slot, std::vector<Slot>, std::greater<Slot>>;
+    std::map<uint32_t, Heap> lightest;
+    for (uint32_t b = 0; b < workgroups; ++b) lightest[weight[b]].push({0, b});
     for (uint32_t i = 0; i < cost.size(); ++i) {
-        const uint32_t b = lightest.top().second;
-        lightest.pop();
+        Heap *best = nullptr;
+        uint64_t best_t = UINT64_MAX;
+        for (auto &kv : lightest) {
+            const uint64_t t = (kv.second.top().first + cost[i]) * kv.first;
+            if (t < best_t) best_t = t, best = &kv.second;
+        }
+        const uint32_t b = best->top().second;
+        best->pop();
         own[b].push_back(i);
         load[b] += cost[i];
-        lightest.push({load[b], b});
+        best->push({load[b], b});
     }
     // One item of each distinct cost a workgroup holds (the candidates of a
     // move; which item of a cost moves does not change any load).
@@ -642,25 +654,28 @@ std::vector<uint32_t> deal_items(const std::vector<uint32_t> &cost, uint32_t wor
         }
         return k;
     };
-    std::vector<uint32_t> by_load(workgroups);
+    std::vector<uint32_t> by_time(workgroups);
     for (uint32_t round = 0; round < 4 * workgroups; ++round) {
-        const uint32_t a = static_cast<uint32_t>(std::max_element(load.begin(), load.end()) - load.begin());
-        for (uint32_t b = 0; b < workgroups; ++b) by_load[b] = b;
-        std::sort(by_load.begin(), by_load.end(), [&](uint32_t x, uint32_t y) { return load[x] < load[y]; });
+        uint32_t a = 0;
+        for (uint32_t b = 1; b < workgroups; ++b)
+            if (finish(b, load[b]) > finish(a, load[a])) a = b;
+        const uint64_t t_a = finish(a, load[a]);
+        for (uint32_t b = 0; b < workgroups; ++b) by_time[b] = b;
+        std::sort(by_time.begin(), by_time.end(),
+                  [&](uint32_t x, uint32_t y) { return finish(x, load[x]) < finish(y, load[y]); });
         const std::vector<uint32_t> ka = kinds(a);
-        uint64_t best_max = load[a];
+        uint64_t best_max = t_a;
         uint32_t best_b = 0, best_pa = 0, best_pb = 0;
         bool found = false;
-        for (uint32_t b : by_load) {
-            const uint64_t gap = load[a] - load[b];
-            if (gap <= 1) break;
+        for (uint32_t b : by_time) {
+            if (b == a || finish(b, load[b]) >= t_a) break;
             std::vector<uint32_t> kb = kinds(b);
             kb.push_back(UINT32_MAX);  // a move with nothing in return
             for (uint32_t pa : ka)
                 for (uint32_t pb : kb) {
                     const uint64_t give = cost[own[a][pa]], take = pb == UINT32_MAX ? 0 : cost[own[b][pb]];
-                    if (give <= take || give - take >= gap) continue;
-                    const uint64_t m = std::max(load[a] - (give - take), load[b] + (give - take));
+                    if (give <= take) continue;
+                    const uint64_t m = std::max(finish(a, load[a] - (give - take)), finish(b, load[b] + (give - take)));
                     if (m < best_max) {
                         best_max = m;
                         best_b = b;
@@ -819,7 +834,24 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
         }
         // The kernel's form: the offsets (padded to 8 bytes), then per item
         // its descriptor index and its index within the descriptor.
-        const std::vector<uint32_t> lists = deal_items(cost, workgroups);
+        // Of the two workgroups a CU holds, the one dispatched first (b <
+        // CUs, as workgroups are dispatched in order) wins the CU's
+        // arbitration and streams faster.  With equal loads on the Qwen3-8B
+        // stack, workgroups b >= CUs finished 20 us after the others (mean
+        // 526.9 against 506.4 us, per-workgroup clock reads), so the CU ran
+        // its second workgroup alone at the end.  Swept on one box, a weight
+        // of 1.074 for the second slot ended both together and gave the
+        // shortest step (1.0 / 1.039 / 1.074 / 1.123 / 1.172: 553.6 /
+        // 550.3 / 549.4 / 553.6 / 557.1 us).
+        const uint32_t cus = cu_count(device);
+        uint32_t second_slot = 1100;
+        if (const char *env = std::getenv("Q4RDNA_PLAN_SLOT_WEIGHT")) {  // tuning sweeps only
+            const int v = std::atoi(env);
+            if (v >= 512 && v <= 4096) second_slot = static_cast<uint32_t>(v);
+        }
+        std::vector<uint32_t> weight(workgroups, 1024);
+        for (uint32_t b = cus; b < workgroups; ++b) weight[b] = second_slot;
+        const std::vector<uint32_t> lists = deal_items(cost, weight);
         const uint32_t head = (workgroups + 2) & ~1u;
         deal.assign(head + 2 * items, 0);
         std::copy(lists.begin(), lists.begin() + workgroups + 1, deal.begin());
