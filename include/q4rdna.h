@@ -191,7 +191,10 @@ typedef struct q4rdna_gemv_desc {
 
 typedef struct q4rdna_plan q4rdna_plan;
 
-/* Build a plan for `count` descriptors (uploads the descriptor table once). */
+/* Build a plan for `count` descriptors (uploads the descriptor table once).
+ * Single-vector plans also fix here which workgroup runs which item: a
+ * load-balancing deal computed on the host, about 2 ms for the 252-tensor
+ * Qwen3-8B stack and 0.2 s for 100,000 items. */
 int q4rdna_plan_create(const q4rdna_gemv_desc *descs, uint32_t count, int device,
                        q4rdna_plan **out);
 /* Batched plan: every descriptor's x holds n activation vectors of
