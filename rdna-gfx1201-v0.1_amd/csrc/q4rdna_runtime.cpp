@@ -853,11 +853,11 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
         for (uint32_t b = cus; b < workgroups; ++b) weight[b] = second_slot;
         // Workgroup b runs on XCD b % 8 (workgroups are dealt to the eight
         // XCDs in turn), and the XCDs stream at slightly different rates:
-        // per-workgroup clock reads on two boxes put XCDs 3 and 5 earliest
-        // and 0 and 6 latest, in the same order, 5-8 us apart at the end of
-        // a 523 us mean.  These are the two boxes' mean time per unit, XCD
-        // by XCD, relative to their average.
-        uint32_t xw[8] = {1030, 1023, 1024, 1015, 1028, 1019, 1030, 1023};
+        // per-workgroup clock reads on three boxes put XCDs 3 and 5
+        // earliest, 5-8 us ahead of the latest at the end of a 523 us mean.
+        // These are the three boxes' mean time per unit, XCD by XCD,
+        // relative to their average.
+        uint32_t xw[8] = {1029, 1023, 1027, 1015, 1028, 1019, 1028, 1023};
         if (const char *env = std::getenv("Q4RDNA_PLAN_XCD_WEIGHTS")) {  // tuning sweeps only
             uint32_t v[8];
             if (std::sscanf(env, "%u,%u,%u,%u,%u,%u,%u,%u", &v[0], &v[1], &v[2], &v[3], &v[4], &v[5], &v[6], &v[7]) ==
