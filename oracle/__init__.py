@@ -45,44 +45,59 @@ def lib() -> ctypes.CDLL:
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle`")
-        L = ctypes.CDLL(LIB_PATH)
-        u8p = ctypes.POINTER(ctypes.c_uint8)
-        f32p = ctypes.POINTER(ctypes.c_float)
-        f64p = ctypes.POINTER(ctypes.c_double)
-        u32 = ctypes.c_uint32
-        L.q4o_fp16_to_f32.argtypes = [ctypes.c_uint16]
-        L.q4o_fp16_to_f32.restype = ctypes.c_float
-        L.q4o_fp16_to_f32_ref.argtypes = [ctypes.c_uint16]
-        L.q4o_fp16_to_f32_ref.restype = ctypes.c_float
-        L.q4o_f32_to_fp16.argtypes = [ctypes.c_float]
-        L.q4o_f32_to_fp16.restype = ctypes.c_uint16
-        L.q4o_f32_to_bf16.argtypes = [ctypes.c_float]
-        L.q4o_f32_to_bf16.restype = ctypes.c_uint16
-        L.q4o_nibble_low.argtypes = [ctypes.c_uint8]
-        L.q4o_nibble_high.argtypes = [ctypes.c_uint8]
-        L.q4o_quantize_value_rne.argtypes = [ctypes.c_float, ctypes.c_float]
-        L.q4o_quantize_value_round.argtypes = [ctypes.c_float, ctypes.c_float]
-        L.q4o_select_scale.argtypes = [f32p, ctypes.c_int]
-        L.q4o_select_scale.restype = ctypes.c_uint16
-        L.q4o_pack.argtypes = [f32p, u32, u32, ctypes.c_int, u8p]
-        L.q4o_pack_mt.argtypes = [f32p, u32, u32, ctypes.c_int, u8p, ctypes.c_int]
-        L.q4o_pack_mt.restype = ctypes.c_int
-        L.q4o_dequant.argtypes = [u8p, u32, u32, f32p]
-        L.q4o_dequant_ref_cpu.argtypes = [u8p, u32, u32, f32p]
-        L.q4o_gemv_seq_f32.argtypes = [u8p, u32, u32, f32p, f32p, u32, u32, ctypes.c_int]
-        L.q4o_gemv_seq_f32_mt.argtypes = [u8p, u32, u32, f32p, f32p, ctypes.c_int]
-        L.q4o_gemv_seq_f32_mt.restype = ctypes.c_int
-        L.q4o_gemv_f64.argtypes = [u8p, u32, u32, f32p, f64p, f64p]
-        L.q4o_silu.argtypes = [ctypes.c_double]
-        L.q4o_silu.restype = ctypes.c_double
-        L.q4o_validate_sidecar.argtypes = [u8p, ctypes.c_uint64]
-        L.q4o_validate_sidecar.restype = ctypes.c_long
-        L.q4o_scale_offset.argtypes = [u32, u32, u32]
-        L.q4o_scale_offset.restype = ctypes.c_uint64
-        L.q4o_code_offset.argtypes = [u32, u32, u32]
-        L.q4o_code_offset.restype = ctypes.c_uint64
-        _lib = L
+        _lib = load_build(LIB_PATH)
     return _lib
+
+
+def build_native(out_dir: str) -> str:
+    """Compile q4oracle.c with -O3 -march=native for the host this runs on
+    (the CPU baseline's optimised build; contraction stays off, so every
+    result is bit-identical to liboracle.so's).  Returns the library path."""
+    out = os.path.join(out_dir, "liboracle_native.so")
+    subprocess.run(["gcc", "-O3", "-march=native", "-std=c11", "-ffp-contract=off", "-fopenmp", "-fPIC", "-shared",
+                    "-o", out, os.path.join(HERE, "q4oracle.c"), "-lm"], check=True)
+    return out
+
+
+def load_build(path: str) -> ctypes.CDLL:
+    """Load a build of q4oracle.c and declare its prototypes."""
+    L = ctypes.CDLL(path)
+    u8p = ctypes.POINTER(ctypes.c_uint8)
+    f32p = ctypes.POINTER(ctypes.c_float)
+    f64p = ctypes.POINTER(ctypes.c_double)
+    u32 = ctypes.c_uint32
+    L.q4o_fp16_to_f32.argtypes = [ctypes.c_uint16]
+    L.q4o_fp16_to_f32.restype = ctypes.c_float
+    L.q4o_fp16_to_f32_ref.argtypes = [ctypes.c_uint16]
+    L.q4o_fp16_to_f32_ref.restype = ctypes.c_float
+    L.q4o_f32_to_fp16.argtypes = [ctypes.c_float]
+    L.q4o_f32_to_fp16.restype = ctypes.c_uint16
+    L.q4o_f32_to_bf16.argtypes = [ctypes.c_float]
+    L.q4o_f32_to_bf16.restype = ctypes.c_uint16
+    L.q4o_nibble_low.argtypes = [ctypes.c_uint8]
+    L.q4o_nibble_high.argtypes = [ctypes.c_uint8]
+    L.q4o_quantize_value_rne.argtypes = [ctypes.c_float, ctypes.c_float]
+    L.q4o_quantize_value_round.argtypes = [ctypes.c_float, ctypes.c_float]
+    L.q4o_select_scale.argtypes = [f32p, ctypes.c_int]
+    L.q4o_select_scale.restype = ctypes.c_uint16
+    L.q4o_pack.argtypes = [f32p, u32, u32, ctypes.c_int, u8p]
+    L.q4o_pack_mt.argtypes = [f32p, u32, u32, ctypes.c_int, u8p, ctypes.c_int]
+    L.q4o_pack_mt.restype = ctypes.c_int
+    L.q4o_dequant.argtypes = [u8p, u32, u32, f32p]
+    L.q4o_dequant_ref_cpu.argtypes = [u8p, u32, u32, f32p]
+    L.q4o_gemv_seq_f32.argtypes = [u8p, u32, u32, f32p, f32p, u32, u32, ctypes.c_int]
+    L.q4o_gemv_seq_f32_mt.argtypes = [u8p, u32, u32, f32p, f32p, ctypes.c_int]
+    L.q4o_gemv_seq_f32_mt.restype = ctypes.c_int
+    L.q4o_gemv_f64.argtypes = [u8p, u32, u32, f32p, f64p, f64p]
+    L.q4o_silu.argtypes = [ctypes.c_double]
+    L.q4o_silu.restype = ctypes.c_double
+    L.q4o_validate_sidecar.argtypes = [u8p, ctypes.c_uint64]
+    L.q4o_validate_sidecar.restype = ctypes.c_long
+    L.q4o_scale_offset.argtypes = [u32, u32, u32]
+    L.q4o_scale_offset.restype = ctypes.c_uint64
+    L.q4o_code_offset.argtypes = [u32, u32, u32]
+    L.q4o_code_offset.restype = ctypes.c_uint64
+    return L
 
 
 def _ptr(a: np.ndarray, ctype):

@@ -54,87 +54,56 @@
 static float bits_f32(uint32_t b) { float f; memcpy(&f, &b, 4); return f; }
 static uint32_t f32_bits(float f) { uint32_t b; memcpy(&b, &f, 4); return b; }
 
-/* The reference CPU tools' binary16 -> binary32 decode.  Normal numbers,
- * zeros and infinities decode exactly, but a subnormal is normalised with
- * biased exponent 127-15-shift instead of 127-14-shift, so every subnormal
- * fp16 value comes out HALVED (0x0001 -> 2^-25, not 2^-24).  Restated as is,
- * because the packers' scale search runs on it and the packed bytes depend on
- * it: source/q4rdna_sidecar_pack.cpp:73-94, source/q4rdna_cpu_experiment.cpp:39-60,
- * and (without the inf/NaN branch) source/q4rdna_gemv_bench.hip:163-187.
- * The reference's GPU kernels decode scales with __half2float instead
- * (source/q4rdna.cu:209,370,445), which is q4o_fp16_to_f32 below. */
-float q4o_fp16_to_f32_ref(uint16_t h)
-{
-    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
-    uint32_t exponent = (h >> 10) & 0x1fu;
-    uint32_t mantissa = h & 0x03ffu;
-    if (exponent == 0) {
-        if (mantissa == 0) return bits_f32(sign);
-        int shift = 0;
-        while ((mantissa & 0x0400u) == 0) { mantissa <<= 1; ++shift; }
-        mantissa &= 0x03ffu;
-        exponent = (uint32_t)(127 - 15 - shift);
-    } else if (exponent == 31) {
-        exponent = 255;
-    } else {
-        exponent += 127 - 15;
-    }
-    return bits_f32(sign | (exponent << 23) | (mantissa << 13));
-}
-
-/* Exact IEEE binary16 -> binary32 (what __half2float computes on the GPU,
- * source/q4rdna.cu:209,370,445; the decode of the runtime path).  NaN keeps
- * its payload in the top mantissa bits. */
+/* Exact IEEE binary16 -> binary32 from the definition of the format: a
+ * subnormal is m * 2^-24, a normal number (1024 + m) * 2^(e - 25), e = 31 is
+ * infinity or NaN.  This is what __half2float computes on the GPU
+ * (source/q4rdna.cu:209,370,445): the decode of the runtime path. */
 float q4o_fp16_to_f32(uint16_t h)
 {
-    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
-    uint32_t exponent = (h >> 10) & 0x1fu;
-    uint32_t mantissa = h & 0x03ffu;
-    if (exponent == 0) {
-        if (mantissa == 0) return bits_f32(sign);
-        int shift = 0;
-        while ((mantissa & 0x0400u) == 0) { mantissa <<= 1; ++shift; }
-        mantissa &= 0x03ffu;
-        exponent = (uint32_t)(127 - 14 - shift);
-    } else if (exponent == 31) {
-        exponent = 255;
-    } else {
-        exponent += 127 - 15;
+    const float sign = (h & 0x8000u) ? -1.0f : 1.0f;
+    const int e = (h >> 10) & 31;
+    const int m = h & 1023;
+    if (e == 31) {
+        if (m == 0) return sign * INFINITY;
+        return bits_f32(((uint32_t)(h & 0x8000u) << 16) | 0x7fc00000u | ((uint32_t)m << 13));
     }
-    return bits_f32(sign | (exponent << 23) | (mantissa << 13));
+    if (e == 0) return sign * ldexpf((float)m, -24);
+    return sign * ldexpf((float)(1024 + m), e - 25);
 }
 
-/* binary32 -> binary16, round to nearest even, overflow -> inf, values below
- * half the smallest subnormal -> signed zero.  NaN maps to inf (the exponent
- * test fires before the mantissa is looked at).  Restates
- * source/q4rdna_sidecar_pack.cpp:96-124 (same at q4rdna_cpu_experiment.cpp:62-100). */
-uint16_t q4o_f32_to_fp16(float value)
+/* The reference CPU tools' binary16 decode, by its behaviour: exact for
+ * zeros, normal numbers and infinities, but every subnormal comes out at half
+ * its value (0x0001 gives 2^-25), because their normalisation loop uses the
+ * exponent bias of a normal number.  The packers' scale search runs on this
+ * decode, so the packed bytes depend on it: source/q4rdna_sidecar_pack.cpp:73-94,
+ * source/q4rdna_cpu_experiment.cpp:39-60, and without the inf/NaN branch
+ * source/q4rdna_gemv_bench.hip:163-187. */
+float q4o_fp16_to_f32_ref(uint16_t h)
 {
-    uint32_t bits = f32_bits(value);
-    uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
-    uint32_t mantissa = bits & 0x007fffffu;
-    int exponent = (int)((bits >> 23) & 0xffu) - 127 + 15;
-    if (exponent <= 0) {
-        if (exponent < -10) return sign;
-        uint32_t normalized = mantissa | 0x00800000u;
-        int shift = 14 - exponent;
-        uint32_t rounded = normalized >> shift;
-        uint32_t remainder = normalized & ((1u << shift) - 1u);
-        uint32_t halfway = 1u << (shift - 1);
-        if (remainder > halfway || (remainder == halfway && (rounded & 1u))) ++rounded;
-        return (uint16_t)(sign | rounded);
-    }
-    if (exponent >= 31) return (uint16_t)(sign | 0x7c00u);
-    uint32_t rounded = mantissa >> 13;
-    uint32_t remainder = mantissa & 0x1fffu;
-    if (remainder > 0x1000u || (remainder == 0x1000u && (rounded & 1u))) {
-        ++rounded;
-        if (rounded == 0x400u) {
-            if (exponent + 1 >= 31) return (uint16_t)(sign | 0x7c00u);
-            return (uint16_t)(sign | (uint16_t)((exponent + 1) << 10));
-        }
-    }
-    return (uint16_t)(sign | (uint16_t)(exponent << 10) | (uint16_t)rounded);
+    const float exact = q4o_fp16_to_f32(h);
+    const int subnormal = ((h >> 10) & 31) == 0 && (h & 1023) != 0;
+    return subnormal ? 0.5f * exact : exact;
+}
+
+/* binary32 -> binary16 by the reference tools' behaviour: IEEE round to
+ * nearest even (overflow to infinity, below half the smallest subnormal to a
+ * signed zero), except that NaN becomes an infinity of the same sign
+ * (source/q4rdna_sidecar_pack.cpp:96-124, q4rdna_cpu_experiment.cpp:62-100).
+ * Computed from the value: |v| >= 65520 (halfway between 65504, the largest
+ * finite half, and 2^16) is infinity; below 2^-14 the result is the number of
+ * 2^-24 steps, rounded; otherwise 11 significant bits, rounded, where a round
+ * up to 2048 carries into the exponent field by itself.  rintf rounds to
+ * nearest even in the default rounding mode. */
+uint16_t q4o_f32_to_fp16(float v)
+{
+    const uint16_t sign = signbit(v) ? 0x8000u : 0u;
+    const float a = fabsf(v);
+    if (isnan(v) || a >= 65520.0f) return (uint16_t)(sign | 0x7c00u);
+    if (a < 0x1p-14f) return (uint16_t)(sign | (uint16_t)rintf(a * 0x1p24f));
+    int e;
+    (void)frexpf(a, &e); /* a = f * 2^e, f in [0.5, 1): half exponent e - 1 */
+    const uint32_t q = (uint32_t)rintf(ldexpf(a, 11 - e)); /* in [1024, 2048] */
+    return (uint16_t)(sign | ((uint32_t)(e + 14) * 1024u + (q - 1024u)));
 }
 
 /* bf16 -> f32 (source/q4rdna_sidecar_pack.cpp:69-71). */
@@ -523,12 +492,18 @@ int q4o_pack_mt(const float *w, uint32_t rows, uint32_t cols, int algorithm, uin
 }
 
 /* fp64 GEMV over the exactly dequantized weights (products are exact in
- * double), plus the conditioning sum sum_k |w*x| used by the error gate. */
+ * double), plus the conditioning sum sum_k |w*x| used by the error gate.
+ * Rows are spread over OpenMP threads; each row's sums run in k order, so
+ * the result does not depend on the thread count. */
 void q4o_gemv_f64(const uint8_t *tiles, uint32_t rows, uint32_t cols, const float *x,
                   double *y, double *absdot)
 {
     uint32_t groups = cols / Q4O_GROUP;
-    for (uint32_t r = 0; r < rows; ++r) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (int64_t rr = 0; rr < (int64_t)rows; ++rr) {
+        uint32_t r = (uint32_t)rr;
         uint32_t rt = r / Q4O_TILE_ROWS, lane = r % Q4O_TILE_ROWS;
         double sum = 0.0, asum = 0.0;
         for (uint32_t g = 0; g < groups; ++g) {

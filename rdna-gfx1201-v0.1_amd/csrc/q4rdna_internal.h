@@ -106,8 +106,9 @@ hipError_t launch_pack(const float *w, uint32_t rows, uint32_t cols, int algorit
                        hipStream_t stream);
 
 // Workgroups of 256 threads the kernels are built for, and the number the
-// plan kernel launches per CU.
+// plan kernel launches per CU: with the fixed item deal the grid must be
+// exactly two workgroups per CU (a third on some CUs runs its share slower).
 constexpr uint32_t kThreads = 256;
-uint32_t plan_workgroups_per_cu();
+constexpr uint32_t kPlanWorkgroupsPerCu = 2;
 
 }  // namespace q4rdna

@@ -603,203 +603,189 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(const uint8_t *__rest
 
 // ---------------------------------------------------------------------------
 // Packer: one thread per (row, group), bit-identical to the reference CPU
-// packers.  Contraction is off so every product and sum rounds exactly as the
-// sequential C++ code does; '/' is the correctly rounded IEEE division and
-// rintf ties to even like nearbyint under FE_TONEAREST.
+// packers (source/q4rdna_sidecar_pack.cpp:126-179, 259-279 and
+// source/q4rdna_cpu_experiment.cpp:136-273, 387-399).  Bit-identical output
+// fixes the arithmetic: every sum runs in index order, contraction is off so
+// each product and sum rounds on its own, '/' is the correctly rounded IEEE
+// division, and rintf ties to even like nearbyint under FE_TONEAREST.
 // ---------------------------------------------------------------------------
 #pragma clang fp contract(off)
 
-__device__ __forceinline__ float bits_to_float(uint32_t b) { return __uint_as_float(b); }
-
-// The reference packers' fp16 decode, subnormals halved as there
-// (source/q4rdna_sidecar_pack.cpp:73-94, 127-15-shift): the scale search runs
-// on it, so the packed bytes depend on it.  GEMV and dequant decode scales
-// exactly with v_cvt_f32_f16, as the reference's kernels do.
-__device__ float fp16_bits_to_float_packer(uint32_t value) {
-    const uint32_t sign = (value & 0x8000u) << 16;
-    uint32_t exponent = (value >> 10) & 0x1fu;
-    uint32_t mantissa = value & 0x03ffu;
-    if (exponent == 0) {
-        if (mantissa == 0) return bits_to_float(sign);
-        int shift = 0;
-        while ((mantissa & 0x0400u) == 0) {
-            mantissa <<= 1;
-            ++shift;
-        }
-        mantissa &= 0x03ffu;
-        exponent = static_cast<uint32_t>(127 - 15 - shift);
-    } else if (exponent == 31) {
-        exponent = 255;
-    } else {
-        exponent += 127 - 15;
-    }
-    return bits_to_float(sign | (exponent << 23) | (mantissa << 13));
+// The reference tools' binary16 conversions, by their behaviour, on the
+// hardware conversions.  Encode: IEEE round to nearest even, except that NaN
+// becomes an infinity of its sign.  Decode: exact, except that a subnormal
+// comes out at half its value (their normalisation uses a normal number's
+// exponent bias).  The scale search runs on this decode, so the packed bytes
+// depend on it; the GEMV and dequant kernels decode scales exactly, as the
+// reference's GPU kernels do (__half2float).
+__device__ __forceinline__ uint32_t packer_encode(float v) {
+    if (isnan(v)) return ((__float_as_uint(v) >> 16) & 0x8000u) | 0x7c00u;
+    return __half_as_ushort(__float2half_rn(v));
 }
 
-// source/q4rdna_sidecar_pack.cpp:96-124 (NaN maps to inf there, kept).
-__device__ uint32_t float_to_fp16_bits(float value) {
-    const uint32_t bits = __float_as_uint(value);
-    const uint32_t sign = (bits >> 16) & 0x8000u;
-    const uint32_t mantissa = bits & 0x007fffffu;
-    const int exponent = static_cast<int>((bits >> 23) & 0xffu) - 127 + 15;
-    if (exponent <= 0) {
-        if (exponent < -10) return sign;
-        const uint32_t normalized = mantissa | 0x00800000u;
-        const int shift = 14 - exponent;
-        uint32_t rounded = normalized >> shift;
-        const uint32_t remainder = normalized & ((1u << shift) - 1u);
-        const uint32_t halfway = 1u << (shift - 1);
-        if (remainder > halfway || (remainder == halfway && (rounded & 1u))) ++rounded;
-        return sign | rounded;
-    }
-    if (exponent >= 31) return sign | 0x7c00u;
-    uint32_t rounded = mantissa >> 13;
-    const uint32_t remainder = mantissa & 0x1fffu;
-    if (remainder > 0x1000u || (remainder == 0x1000u && (rounded & 1u))) {
-        ++rounded;
-        if (rounded == 0x400u) {
-            if (exponent + 1 >= 31) return sign | 0x7c00u;
-            return sign | (static_cast<uint32_t>(exponent + 1) << 10);
-        }
-    }
-    return sign | (static_cast<uint32_t>(exponent) << 10) | rounded;
+__device__ __forceinline__ float packer_decode(uint32_t h) {
+    const float exact = half_bits_to_float(h);
+    return ((h & 0x7c00u) == 0u && (h & 0x03ffu) != 0u) ? 0.5f * exact : exact;
 }
 
-// int(t) of an integral float as x86-64 computes it (INT_MIN out of range),
-// which the reference's int(...) conversions yield on the CPU they ran on.
-__device__ __forceinline__ int x86_int(float t) {
+// int(t) of an integral float as x86-64 converts it (INT_MIN when out of
+// range), the conversion the reference tools' int(...) made where they ran.
+__device__ __forceinline__ int to_int_x86(float t) {
     if (!(t >= -2147483648.0f && t < 2147483648.0f)) return static_cast<int>(0x80000000u);
     return static_cast<int>(t);
 }
 
-__device__ __forceinline__ int clamp_code(int v) { return v < -8 ? -8 : (v > 7 ? 7 : v); }
-__device__ __forceinline__ float max_ref(float a, float b) { return (a < b) ? b : a; }
-
-// source/q4rdna_sidecar_pack.cpp:126-129
-__device__ __forceinline__ int quantize_rne(float value, float scale) {
-    if (scale == 0.0f) return 0;
-    return clamp_code(x86_int(rintf(value / scale)));
+// Code of v at scale s: v / s rounded (ties to even for the sidecar packer,
+// away from zero for the CPU experiment), clamped to [-8, 7]; 0 at s = 0.
+template <bool TIES_EVEN>
+__device__ __forceinline__ int code_at(float v, float s) {
+    if (s == 0.0f) return 0;
+    const float r = TIES_EVEN ? rintf(v / s) : roundf(v / s);
+    const int c = to_int_x86(r);
+    return c < -8 ? -8 : (c > 7 ? 7 : c);
 }
 
-// source/q4rdna_cpu_experiment.cpp:136-141
-__device__ __forceinline__ int quantize_round(float value, float scale) {
-    if (scale == 0.0f) return 0;
-    return clamp_code(x86_int(roundf(value / scale)));
-}
+// A group's extremes and the two "range" scales that map them onto the code
+// range: the positive one puts max v at +7 or min v at -8, whichever needs
+// the larger scale; the negative one mirrors it.  The running maxima start
+// at 0 and keep the old value unless the new one is strictly larger (a NaN
+// never replaces anything).
+struct GroupRange {
+    float pos_max, neg_max, abs_max;
+    float pos_scale, neg_scale;
+};
 
-// source/q4rdna_sidecar_pack.cpp:131-179
-__device__ uint32_t select_scale_sidecar(const float *v) {
-    float positive_max = 0.0f, negative_max = 0.0f;
+__device__ __forceinline__ float keep_larger(float a, float b) { return a < b ? b : a; }
+
+__device__ GroupRange group_range(const float *v) {
+    GroupRange g{0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
     for (int i = 0; i < 64; ++i) {
-        positive_max = max_ref(positive_max, v[i]);
-        negative_max = max_ref(negative_max, -v[i]);
+        g.pos_max = keep_larger(g.pos_max, v[i]);
+        g.neg_max = keep_larger(g.neg_max, -v[i]);
+        g.abs_max = keep_larger(g.abs_max, fabsf(v[i]));
     }
-    if (positive_max == 0.0f && negative_max == 0.0f) return 0;
-    const float positive = max_ref(positive_max / 7.0f, negative_max / 8.0f);
-    const float negative = -max_ref(positive_max / 8.0f, negative_max / 7.0f);
-    const float factors[5] = {1.0f, 0.9f, 0.8f, 0.7f, 0.6f};
-    uint32_t best_bits = 0;
-    float best_error = __builtin_huge_valf();
-    for (int f = 0; f < 5; ++f) {
-        for (int sgn = 0; sgn < 2; ++sgn) {
-            uint32_t scale_bits = float_to_fp16_bits((sgn == 0 ? positive : negative) * factors[f]);
-            for (int iteration = 0; iteration < 12; ++iteration) {
-                const float scale = fp16_bits_to_float_packer(scale_bits);
-                float error = 0.0f;
-                for (int i = 0; i < 64; ++i) {
-                    const float delta = scale * static_cast<float>(quantize_rne(v[i], scale)) - v[i];
-                    error += delta * delta;
-                }
-                if (error < best_error) {
-                    best_error = error;
-                    best_bits = scale_bits;
-                }
-                float numerator = 0.0f, denominator = 0.0f;
-                for (int i = 0; i < 64; ++i) {
-                    const int quant = quantize_rne(v[i], scale);
-                    numerator += v[i] * static_cast<float>(quant);
-                    denominator += static_cast<float>(quant * quant);
-                }
-                if (denominator == 0.0f) break;
-                const uint32_t next_bits = float_to_fp16_bits(numerator / denominator);
-                if (next_bits == scale_bits) break;
-                scale_bits = next_bits;
+    g.pos_scale = keep_larger(g.pos_max / 7.0f, g.neg_max / 8.0f);
+    g.neg_scale = -keep_larger(g.pos_max / 8.0f, g.neg_max / 7.0f);
+    return g;
+}
+
+// The sidecar packer's sums at one scale, in fp32: the squared error of the
+// codes and the least-squares terms sum v*q and sum q*q of a refit.  One pass
+// computes all three from the same codes; each sum keeps index order.
+struct FitF32 {
+    float err, num, den;
+};
+
+__device__ FitF32 fit_f32(const float *v, float s) {
+    FitF32 f{0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < 64; ++i) {
+        const int q = code_at<true>(v[i], s);
+        const float d = s * static_cast<float>(q) - v[i];
+        f.err += d * d;
+        f.num += v[i] * static_cast<float>(q);
+        f.den += static_cast<float>(q * q);
+    }
+    return f;
+}
+
+// Sidecar search: ten starts (the positive and the negative range scale,
+// times 1, 0.9, 0.8, 0.7, 0.6, positive first at each factor), each refitted
+// by least squares until its fp16 scale repeats, for at most 12 evaluations;
+// the scale of least error wins, the earliest on ties.  An all-zero group
+// gets scale 0.
+__device__ uint32_t search_sidecar(const float *v) {
+    const GroupRange g = group_range(v);
+    if (g.pos_max == 0.0f && g.neg_max == 0.0f) return 0;
+    const float factor[5] = {1.0f, 0.9f, 0.8f, 0.7f, 0.6f};
+    uint32_t best = 0;
+    float best_err = __builtin_huge_valf();
+    for (int start = 0; start < 10; ++start) {
+        uint32_t h = packer_encode(((start & 1) ? g.neg_scale : g.pos_scale) * factor[start >> 1]);
+        for (int eval = 0; eval < 12; ++eval) {
+            const FitF32 f = fit_f32(v, packer_decode(h));
+            if (f.err < best_err) {
+                best_err = f.err;
+                best = h;
             }
+            if (f.den == 0.0f) break;
+            const uint32_t next = packer_encode(f.num / f.den);
+            if (next == h) break;
+            h = next;
         }
     }
-    return best_bits;
+    return best;
 }
 
-// source/q4rdna_cpu_experiment.cpp:143-152
-__device__ double experiment_error(const float *v, uint32_t scale_bits) {
-    const float scale = fp16_bits_to_float_packer(scale_bits);
-    double error = 0.0;
+// The CPU experiment's bookkeeping: the best fp16 scale so far and its
+// squared error in double.
+struct Best {
+    double err;
+    uint32_t bits;
+};
+
+// Squared error, in double, of the codes (ties away from zero) at scale s.
+__device__ double err_f64(const float *v, float s) {
+    double e = 0.0;
     for (int i = 0; i < 64; ++i) {
-        const int quant = quantize_round(v[i], scale);
-        const double delta = static_cast<double>(scale) * static_cast<double>(quant) - static_cast<double>(v[i]);
-        error += delta * delta;
+        const double d = static_cast<double>(s) * static_cast<double>(code_at<false>(v[i], s)) - static_cast<double>(v[i]);
+        e += d * d;
     }
-    return error;
+    return e;
 }
 
-// source/q4rdna_cpu_experiment.cpp:154-164
-__device__ void consider_scale(const float *v, float scale, uint32_t &best_bits, double &best_error) {
-    if (!isfinite(scale)) return;
-    const uint32_t bits = float_to_fp16_bits(scale);
-    const double error = experiment_error(v, bits);
-    if (error < best_error) {
-        best_bits = bits;
-        best_error = error;
+// Offer scale s: a finite s is stored as fp16 and judged at the value those
+// bits decode to; it replaces the best if its error is strictly smaller.
+__device__ void offer(const float *v, float s, Best &b) {
+    if (!isfinite(s)) return;
+    const uint32_t h = packer_encode(s);
+    const double e = err_f64(v, packer_decode(h));
+    if (e < b.err) {
+        b.err = e;
+        b.bits = h;
     }
 }
 
-// source/q4rdna_cpu_experiment.cpp:166-195
-__device__ void refine_mse_scale(const float *v, float initial, uint32_t &best_bits, double &best_error) {
-    uint32_t scale_bits = float_to_fp16_bits(initial);
-    for (int iteration = 0; iteration < 12; ++iteration) {
-        const float scale = fp16_bits_to_float_packer(scale_bits);
-        consider_scale(v, scale, best_bits, best_error);
-        double numerator = 0.0, denominator = 0.0;
+// One start of the experiment's mse search: up to 12 least-squares refits in
+// double, each offered, stopping when the fp16 scale repeats or every code is
+// zero; then the two fp16 magnitudes adjacent to the best so far.
+__device__ void refit_f64(const float *v, float s0, Best &b) {
+    uint32_t h = packer_encode(s0);
+    for (int eval = 0; eval < 12; ++eval) {
+        const float s = packer_decode(h);
+        offer(v, s, b);
+        double num = 0.0, den = 0.0;
         for (int i = 0; i < 64; ++i) {
-            const int quant = quantize_round(v[i], scale);
-            numerator += static_cast<double>(v[i]) * static_cast<double>(quant);
-            denominator += static_cast<double>(quant) * static_cast<double>(quant);
+            const double q = static_cast<double>(code_at<false>(v[i], s));
+            num += static_cast<double>(v[i]) * q;
+            den += q * q;
         }
-        if (denominator == 0.0) break;
-        const uint32_t next_bits = float_to_fp16_bits(static_cast<float>(numerator / denominator));
-        if (next_bits == scale_bits) break;
-        scale_bits = next_bits;
+        if (den == 0.0) break;
+        const uint32_t next = packer_encode(static_cast<float>(num / den));
+        if (next == h) break;
+        h = next;
     }
-    if ((best_bits & 0x7fffu) != 0 && (best_bits & 0x7fffu) < 0x7bffu) {
-        const uint32_t magnitude = best_bits & 0x7fffu, sign = best_bits & 0x8000u;
-        consider_scale(v, fp16_bits_to_float_packer(sign | (magnitude - 1u)), best_bits, best_error);
-        consider_scale(v, fp16_bits_to_float_packer(sign | (magnitude + 1u)), best_bits, best_error);
+    const uint32_t mag = b.bits & 0x7fffu, sign = b.bits & 0x8000u;
+    if (mag != 0u && mag < 0x7bffu) {
+        offer(v, packer_decode(sign | (mag - 1u)), b);
+        offer(v, packer_decode(sign | (mag + 1u)), b);
     }
 }
 
-// source/q4rdna_cpu_experiment.cpp:197-237
-__device__ uint32_t select_scale_experiment(const float *v, int algorithm) {
-    float positive_max = 0.0f, negative_max = 0.0f, max_abs = 0.0f;
-    for (int i = 0; i < 64; ++i) {
-        positive_max = max_ref(positive_max, v[i]);
-        negative_max = max_ref(negative_max, -v[i]);
-        max_abs = max_ref(max_abs, fabsf(v[i]));
-    }
-    if (max_abs == 0.0f) return 0;
-    if (algorithm == 1) return float_to_fp16_bits(max_abs / 7.0f);
-    const float positive_range = max_ref(positive_max / 7.0f, negative_max / 8.0f);
-    const float negative_range = -max_ref(positive_max / 8.0f, negative_max / 7.0f);
-    uint32_t best_bits = 0;
-    double best_error = __builtin_huge_val();
-    consider_scale(v, positive_range, best_bits, best_error);
-    consider_scale(v, negative_range, best_bits, best_error);
-    if (algorithm == 2) return best_bits;
-    const float factors[12] = {1.0f, 0.9f, 0.8f, 0.7f, 0.6f, 0.55f, 0.5f, 0.45f, 0.4f, 0.35f, 0.3f, 0.25f};
-    for (int f = 0; f < 12; ++f) {
-        refine_mse_scale(v, positive_range * factors[f], best_bits, best_error);
-        refine_mse_scale(v, negative_range * factors[f], best_bits, best_error);
-    }
-    return best_bits;
+// The CPU experiment's three searches: absmax = fp16(max|v| / 7); range =
+// the better of the two range scales; mse = range, then 24 refitted starts
+// (the two range scales times 1 .. 0.25, positive first at each factor).
+__device__ uint32_t search_experiment(const float *v, int algorithm) {
+    const GroupRange g = group_range(v);
+    if (g.abs_max == 0.0f) return 0;
+    if (algorithm == 1) return packer_encode(g.abs_max / 7.0f);
+    Best b{__builtin_huge_val(), 0u};
+    offer(v, g.pos_scale, b);
+    offer(v, g.neg_scale, b);
+    if (algorithm == 2) return b.bits;
+    const float factor[12] = {1.0f, 0.9f, 0.8f, 0.7f, 0.6f, 0.55f, 0.5f, 0.45f, 0.4f, 0.35f, 0.3f, 0.25f};
+    for (int start = 0; start < 24; ++start)
+        refit_f64(v, ((start & 1) ? g.neg_scale : g.pos_scale) * factor[start >> 1], b);
+    return b.bits;
 }
 
 // Thread per (row, group) ordered (row tile, group, row lane) so a wave's
@@ -825,14 +811,14 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(const float *__restrict_
             v[4 * i + 2] = f.z;
             v[4 * i + 3] = f.w;
         }
-        const uint32_t bits = algorithm == 0 ? select_scale_sidecar(v) : select_scale_experiment(v, algorithm);
-        const float scale = fp16_bits_to_float_packer(bits);
+        const uint32_t bits = algorithm == 0 ? search_sidecar(v) : search_experiment(v, algorithm);
+        const float scale = packer_decode(bits);
         uint8_t *tile = tiles + t * kTileBytes;
         tile[2 * l] = static_cast<uint8_t>(bits & 0xffu);
         tile[2 * l + 1] = static_cast<uint8_t>(bits >> 8);
         for (int i = 0; i < 32; ++i) {
-            const int lo = algorithm == 0 ? quantize_rne(v[2 * i], scale) : quantize_round(v[2 * i], scale);
-            const int hi = algorithm == 0 ? quantize_rne(v[2 * i + 1], scale) : quantize_round(v[2 * i + 1], scale);
+            const int lo = algorithm == 0 ? code_at<true>(v[2 * i], scale) : code_at<false>(v[2 * i], scale);
+            const int hi = algorithm == 0 ? code_at<true>(v[2 * i + 1], scale) : code_at<false>(v[2 * i + 1], scale);
             tile[64 + 32 * i + l] = static_cast<uint8_t>((lo & 15) | ((hi & 15) << 4));
         }
     }

@@ -848,6 +848,4 @@ hipError_t launch_plan_batch(const PlanDesc *descs, uint32_t items, uint32_t n, 
     return hipGetLastError();
 }
 
-uint32_t plan_workgroups_per_cu() { return 2; }
-
 }  // namespace q4rdna

@@ -37,6 +37,18 @@ def _f32_vec(t: torch.Tensor, name: str) -> torch.Tensor:
     return t
 
 
+def _f32_buf(t: torch.Tensor, name: str, numel: int, device: int) -> torch.Tensor:
+    """A device buffer the kernels read or write numel floats of: checked
+    here, since the library sees only its address and a short or misplaced
+    buffer would be read or written past its end on the GPU."""
+    _f32_vec(t, name)
+    if t.numel() != numel:
+        raise ValueError(f"{name} holds {t.numel()} floats, {numel} are needed")
+    if t.device.index != device:
+        raise ValueError(f"{name} lives on cuda:{t.device.index}, the weight on cuda:{device}")
+    return t
+
+
 class QWeight:
     """A packed Q4_RDNA tensor resident on a GPU.
 
@@ -118,6 +130,12 @@ def mul_mat_glu(up: QWeight, gate: QWeight, x: torch.Tensor, y: torch.Tensor | N
 def mul_mat_ex(w: QWeight, x: torch.Tensor, y: torch.Tensor, gate: QWeight | None = None,
                add: torch.Tensor | None = None, split_k: int = 0, stream: int | None = None) -> bool:
     """GEMV with an explicit split-K factor (0 = the shape policy)."""
+    _f32_buf(x, "x", w.cols, w.device)
+    _f32_buf(y, "y", w.rows, w.device)
+    if add is not None:
+        _f32_buf(add, "add", w.rows, w.device)
+    if gate is not None and (gate.rows, gate.cols) != (w.rows, w.cols):
+        raise ValueError("gate and weight shapes differ")
     opts = LaunchOptions()
     opts.split_k = split_k
     s = _stream(x.device) if stream is None else stream
@@ -137,6 +155,9 @@ def mul_mat_batch(w: QWeight, x: torch.Tensor, y: torch.Tensor, gate: QWeight | 
         raise ValueError("x / y shapes do not match the weight")
     if add is not None and (add.shape != y.shape or not add.is_contiguous() or add.dtype != torch.float32):
         raise ValueError("add must match y")
+    for t, name in ((x, "x"), (y, "y"), (add, "add")):
+        if t is not None and (not t.is_cuda or t.device.index != w.device):
+            raise ValueError(f"{name} must live on the weight's device cuda:{w.device}")
     opts = LaunchOptions()
     opts.split_k = split_k
     s = _stream(x.device) if stream is None else stream
@@ -166,6 +187,7 @@ def dequantize(w: QWeight, out: torch.Tensor | None = None, stream: int | None =
     """fp32 [rows, cols] = scale * code (the exact product)."""
     if out is None:
         out = torch.empty((w.rows, w.cols), dtype=torch.float32, device=torch.device("cuda", w.device))
+    _f32_buf(out, "out", w.rows * w.cols, w.device)
     s = _stream(out.device) if stream is None else stream
     check(load().q4rdna_dequantize(ctypes.byref(w.raw), out.data_ptr(), s))
     return out
@@ -252,6 +274,14 @@ class Plan:
             w, x, y = it[0], it[1], it[2]
             gate = it[3] if len(it) > 3 else None
             add = it[4] if len(it) > 4 else None
+            if w.device != device:
+                raise ValueError(f"item {i}: the weight lives on cuda:{w.device}, the plan on cuda:{device}")
+            _f32_buf(x, f"item {i} x", batch * w.cols, device)
+            _f32_buf(y, f"item {i} y", batch * w.rows, device)
+            if add is not None:
+                _f32_buf(add, f"item {i} add", batch * w.rows, device)
+            if gate is not None and (gate.rows, gate.cols, gate.device) != (w.rows, w.cols, w.device):
+                raise ValueError(f"item {i}: gate and weight differ in shape or device")
             descs[i].weight = w.raw
             descs[i].gate_tiles = gate.raw.tiles if gate is not None else None
             descs[i].x = x.data_ptr()

@@ -32,3 +32,37 @@ def cuda():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     return torch.device("cuda", 0)
+
+
+GATE_TOL = 1e-3     # per-row relative bound against the fp64 oracle (fp32 accumulation)
+REL_L2_TOL = 1e-5   # the reference bench's gate against its sequential fp32 loop (q4rdna_gemv_bench.hip:259)
+
+
+def assert_gemv_parity(y, tiles, rows, cols, x, gate_tiles=None, add=None, label=""):
+    """One GEMV output (with its add / SwiGLU epilogue) against both bars:
+    per row |y - y64| <= 1e-3 * max(|y64|, 0.01 * rms(y64)) against the fp64
+    oracle, with the error-propagation bound of the epilogue checked too, and
+    relative L2 <= 1e-5 against the reference bench's sequential fp32 loop
+    (the epilogue applied to its results in fp64)."""
+    import oracle as O
+    y = np.asarray(y, dtype=np.float64).reshape(-1)
+    y64, a64 = O.gemv_f64(tiles, rows, cols, x)
+    seq = O.gemv_seq_f32_mt(tiles, rows, cols, x)[0].astype(np.float64)
+    want, bound, want_seq = y64, a64, seq
+    if add is not None:
+        add = np.asarray(add, dtype=np.float64)
+        want, bound, want_seq = want + add, bound + np.abs(add), want_seq + add
+    if gate_tiles is not None:
+        g64, ga = O.gemv_f64(gate_tiles, rows, cols, x)
+        gseq = O.gemv_seq_f32_mt(gate_tiles, rows, cols, x)[0].astype(np.float64)
+        # |d(u * silu(g))| <= |du| |silu(g)| + |u| |silu'(g)| |dg|, silu' <= 1.1
+        bound = bound * np.abs(O.silu(g64)) + np.abs(want) * 1.1 * ga
+        want = want * O.silu(g64)
+        want_seq = want_seq * O.silu(gseq)
+    rms = float(np.sqrt(np.mean(want ** 2)))
+    rel = np.abs(y - want) / np.maximum(np.abs(want), 0.01 * rms)
+    assert rel.max() <= GATE_TOL, (label, float(rel.max()))
+    assert (np.abs(y - want) <= 1e-5 * bound + 1e-30).all(), (label, "error bound")
+    l2 = O.rel_l2(y, want_seq)
+    assert l2 <= REL_L2_TOL, (label, l2)
+    return float(rel.max()), l2

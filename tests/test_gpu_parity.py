@@ -14,12 +14,10 @@ import torch
 import oracle as O
 import q4rdna
 from q4rdna import api
-from conftest import bf16_to_f32
+from conftest import GATE_TOL, REL_L2_TOL, assert_gemv_parity, bf16_to_f32
 
 pytestmark = pytest.mark.gpu
 
-GATE_TOL = 1e-3
-REL_L2_TOL = 1e-5
 ALGOS = [(q4rdna.ALGO_SIDECAR, "sidecar"), (q4rdna.ALGO_ABSMAX, "absmax"), (q4rdna.ALGO_RANGE, "range"),
          (q4rdna.ALGO_MSE, "mse")]
 
@@ -390,17 +388,7 @@ def test_plan_matches_oracle(cuda):
     for f, c in zip(first, checks):  # the counters were left clean: a second sweep repeats the first
         assert torch.equal(f, c[-1])
     for t, gt, x, add_np, rows, cols, y in checks:
-        yh = y.cpu().numpy().astype(np.float64)
-        y64, a64 = O.gemv_f64(t, rows, cols, x)
-        if gt is not None:
-            g64, _ = O.gemv_f64(gt, rows, cols, x)
-            want = y64 * O.silu(g64)
-        elif add_np is not None:
-            want = y64 + add_np
-        else:
-            want = y64
-        rms = np.sqrt(np.mean(want ** 2))
-        assert (np.abs(yh - want) / np.maximum(np.abs(want), 0.01 * rms)).max() <= GATE_TOL, (rows, cols)
+        assert_gemv_parity(y.cpu().numpy(), t, rows, cols, x, gate_tiles=gt, add=add_np, label=(rows, cols))
     plan.close()
 
 
@@ -436,8 +424,7 @@ def test_plan_subnormal_scales_and_wide_activations(cuda, batch):
         if not x.any():
             assert (yh[v] == 0).all()
             continue
-        y64, a64 = O.gemv_f64(t, rows, cols, x)
-        assert O.gemv_errors(yh[v], y64, a64)["gate"] <= GATE_TOL, v
+        assert_gemv_parity(yh[v], t, rows, cols, x, label=v)
     plan.close()
 
 
@@ -458,8 +445,7 @@ def test_plan_nonfinite_activation(cuda):
     assert plan.launch()
     torch.cuda.synchronize()
     assert torch.isnan(ys[0]).all() and not torch.isfinite(ys[1]).any()
-    y64, a64 = O.gemv_f64(t, rows, cols, xs[2])
-    assert O.gemv_errors(ys[2].cpu().numpy(), y64, a64)["gate"] <= GATE_TOL
+    assert_gemv_parity(ys[2].cpu().numpy(), t, rows, cols, xs[2])
     plan.close()
 
 
@@ -492,19 +478,10 @@ def test_batched_plan_matches_oracle(cuda, batch):
         assert plan.launch()
     torch.cuda.synchronize()
     for t, gt, xs, add_np, rows, cols, y in checks:
-        yh = y.cpu().numpy().astype(np.float64)
+        yh = y.cpu().numpy()
         for v in range(batch):
-            y64, _ = O.gemv_f64(t, rows, cols, xs[v])
-            if gt is not None:
-                g64, _ = O.gemv_f64(gt, rows, cols, xs[v])
-                want = y64 * O.silu(g64)
-            elif add_np is not None:
-                want = y64 + add_np[v]
-            else:
-                want = y64
-            rms = np.sqrt(np.mean(want ** 2))
-            err = (np.abs(yh[v] - want) / np.maximum(np.abs(want), 0.01 * rms)).max()
-            assert err <= GATE_TOL, (rows, cols, kind, v, err)
+            assert_gemv_parity(yh[v], t, rows, cols, xs[v], gate_tiles=gt,
+                               add=None if add_np is None else add_np[v], label=(rows, cols, v))
     plan.close()
 
 
@@ -654,14 +631,28 @@ def test_graph_replays_after_the_split_k_workspace_grows(cuda):
 
 @pytest.mark.gpu
 def test_plan_rejects_bad_descriptors(cuda):
-    """Argument errors raise (negative status) and create nothing."""
+    """Argument errors return a negative status from the library and create
+    nothing; the Python layer refuses short or misplaced buffers first."""
     t = random_tiles(64, 128, 5)
     w = api.QWeight.from_tiles(dev_u8(t), 64, 128)
-    x = torch.zeros(128, device="cuda")
+    x = torch.zeros(129, device="cuda")
     y = torch.zeros(64, device="cuda")
-    with pytest.raises(api.Q4RdnaError):
-        api.Plan([(w, x, y)], batch=9)
-    with pytest.raises(api.Q4RdnaError):
-        api.Plan([(w, x, y)], batch=0)
-    with pytest.raises(api.Q4RdnaError):
-        api.Plan([(w, x[1:], y)])  # misaligned activation
+    L = q4rdna.load()
+    from q4rdna._lib import GemvDesc
+    descs = (GemvDesc * 1)()
+    descs[0].weight = w.raw
+    descs[0].x = x.data_ptr()
+    descs[0].y = y.data_ptr()
+    h = ctypes.c_void_p()
+    for batch in (0, 9):
+        assert L.q4rdna_plan_create_batch(descs, 1, batch, 0, ctypes.byref(h)) == q4rdna.ERR_ARGUMENT
+    descs[0].x = x[1:].data_ptr()  # misaligned activation
+    assert L.q4rdna_plan_create_batch(descs, 1, 1, 0, ctypes.byref(h)) == q4rdna.ERR_ARGUMENT
+    assert "alignment" in q4rdna.last_error()
+    assert not h.value
+    with pytest.raises(ValueError):
+        api.Plan([(w, x, y)])            # x holds 129 floats, 128 are needed
+    with pytest.raises(ValueError):
+        api.Plan([(w, x[:128], y)], batch=2)
+    with pytest.raises(ValueError):
+        api.dequantize(w, out=torch.empty(64 * 127, device="cuda"))

@@ -1,0 +1,253 @@
+"""GPU parity at the bench's own scale, through the C ABI: the lm_head shape
+(151936 x 4096) through the per-tensor kernel and a plan, the full Qwen3-8B
+36-layer stack as the 252-GEMV plan and as the 216-GEMV SwiGLU-fused plan
+at their real item deal (512 workgroups, two per CU), and plans of more
+items than workgroups with every item kind, single-vector and batched.
+
+Bars (tests/conftest.py): per row 1e-3 of max(|y64|, 0.01 rms) against the
+fp64 oracle, and relative L2 <= 1e-5 against the reference bench's
+sequential fp32 loop (source/q4rdna_gemv_bench.hip:189-211, 259-261).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+import q4rdna
+from q4rdna import api
+from conftest import assert_gemv_parity
+
+pytestmark = pytest.mark.gpu
+
+
+def dev_u8(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint8)).cuda()
+
+
+def dev_f32(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()
+
+
+def random_tiles(rows: int, cols: int, seed: int, subnormal: bool = False) -> np.ndarray:
+    """Uniform random code bytes and random fp16 scales of both signs."""
+    rng = np.random.default_rng(seed)
+    g = cols // 64
+    t = rng.integers(0, 256, (rows // 32, g, 1088), dtype=np.uint8)
+    mag = rng.uniform(1e-3, 3e-2, (rows // 32, g, 32))
+    if subnormal:
+        mag[..., ::7] = rng.uniform(1e-7, 6e-5, mag[..., ::7].shape)
+    s = (mag * rng.choice([-1.0, 1.0], mag.shape)).astype(np.float16)
+    t[:, :, :64] = s.view(np.uint8).reshape(rows // 32, g, 64)
+    return t.reshape(-1)
+
+
+# ----------------------------------------------------------------- lm_head
+
+LM_ROWS, LM_COLS = 151936, 4096
+
+
+@pytest.fixture(scope="module")
+def lm_head():
+    up = random_tiles(LM_ROWS, LM_COLS, 0x1A0, subnormal=True)
+    gate = random_tiles(LM_ROWS, LM_COLS, 0x1A1)
+    x = O.gaussian_x(LM_COLS, 0x1A2)
+    add = O.gaussian_x(LM_ROWS, 0x1A3)
+    return up, gate, x, add
+
+
+@pytest.mark.parametrize("kind", ["plain", "add", "glu"])
+def test_lm_head_per_tensor(cuda, lm_head, kind):
+    """151936 x 4096 at batch 1 through the per-tensor entry points: the
+    shape policy gives split 1 (4,748 workgroups, more than four per CU), so
+    the launch runs four-wave workgroups of 16 tiles per wave."""
+    up_t, gate_t, x, add = lm_head
+    assert api.policy_split_k(LM_ROWS, LM_COLS) == 1
+    assert LM_ROWS // 32 > 4 * torch.cuda.get_device_properties(0).multi_processor_count
+    up = api.QWeight.from_tiles(dev_u8(up_t), LM_ROWS, LM_COLS)
+    xd = dev_f32(x)
+    y = torch.full((LM_ROWS,), float("nan"), device="cuda")
+    if kind == "plain":
+        assert api.mul_mat(up, xd, y) is not None
+        assert_gemv_parity(y.cpu().numpy(), up_t, LM_ROWS, LM_COLS, x, label="lm_head")
+    elif kind == "add":
+        assert api.mul_mat_add(up, xd, dev_f32(add), y) is not None
+        assert_gemv_parity(y.cpu().numpy(), up_t, LM_ROWS, LM_COLS, x, add=add, label="lm_head + add")
+    else:
+        gate = api.QWeight.from_tiles(dev_u8(gate_t), LM_ROWS, LM_COLS)
+        assert api.mul_mat_glu(up, gate, xd, y) is not None
+        assert_gemv_parity(y.cpu().numpy(), up_t, LM_ROWS, LM_COLS, x, gate_tiles=gate_t, label="lm_head swiglu")
+
+
+def test_lm_head_plan(cuda, lm_head):
+    """lm_head through a plan (pair items, the MFMA sweep), next to a q
+    projection so two GEMVs share the deal."""
+    up_t, _, x, _ = lm_head
+    q_t = random_tiles(4096, 4096, 0x1A4)
+    xq = O.gaussian_x(4096, 0x1A5)
+    up = api.QWeight.from_tiles(dev_u8(up_t), LM_ROWS, LM_COLS)
+    q = api.QWeight.from_tiles(dev_u8(q_t), 4096, 4096)
+    y = torch.full((LM_ROWS,), float("nan"), device="cuda")
+    yq = torch.full((4096,), float("nan"), device="cuda")
+    plan = api.Plan([(up, dev_f32(x), y), (q, dev_f32(xq), yq)])
+    assert plan.launch()
+    torch.cuda.synchronize()
+    assert_gemv_parity(y.cpu().numpy(), up_t, LM_ROWS, LM_COLS, x, label="lm_head plan")
+    assert_gemv_parity(yq.cpu().numpy(), q_t, 4096, 4096, xq, label="q next to lm_head")
+    plan.close()
+
+
+# ----------------------------------------------------------------- the 36-layer stack
+
+@pytest.fixture(scope="module")
+def stack(cuda):
+    """The Qwen3-8B 36-layer stack as the bench builds it: N(0, 0.02)
+    weights packed on the GPU in layer order, N(0, 1) x per tensor."""
+    from q4rdna.sidecar import layout, qwen3_8b_stack
+    names = qwen3_8b_stack(36)
+    data_offset, entries, end = layout(names)
+    data = torch.empty(end - data_offset, dtype=torch.uint8, device="cuda")
+    gen = torch.Generator(device="cuda")
+    tensors = []
+    for i, (name, rows, cols, off, size) in enumerate(entries):
+        gen.manual_seed(0x51EE0000 + i)
+        w = torch.randn(rows, cols, generator=gen, device="cuda").mul_(0.02)
+        view = data[off - data_offset: off - data_offset + size]
+        api.pack(w, out=view)
+        del w
+        gen.manual_seed(0x51EE8000 + i)
+        x = torch.randn(cols, generator=gen, device="cuda")
+        tensors.append(dict(name=name, rows=rows, cols=cols, w=api.QWeight.from_tiles(view, rows, cols), x=x))
+    torch.cuda.synchronize()
+    yield tensors
+    del data
+
+
+CHECK_LAYERS = (0, 17, 35)
+
+
+def test_full_stack_252_gemv_plan(cuda, stack):
+    """The bench's plan: 252 GEMVs, 12,096 items dealt to two workgroups per
+    CU; every projection of the first, a middle and the last layer against
+    both bars, and a second launch bit-identical to the first."""
+    ys = [torch.full((t["rows"],), float("nan"), device="cuda") for t in stack]
+    plan = api.Plan([(t["w"], t["x"], y) for t, y in zip(stack, ys)])
+    assert plan.workgroups == 2 * torch.cuda.get_device_properties(0).multi_processor_count
+    assert plan.launch()
+    torch.cuda.synchronize()
+    first = [y.clone() for y in ys]
+    assert plan.launch()
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b) for a, b in zip(first, ys))
+    assert not any(torch.isnan(y).any().item() for y in ys)
+    for layer in CHECK_LAYERS:
+        for j in range(7):
+            t = stack[7 * layer + j]
+            assert_gemv_parity(ys[7 * layer + j].cpu().numpy(), t["w"].tiles.cpu().numpy(), t["rows"], t["cols"],
+                               t["x"].cpu().numpy(), label=t["name"])
+    plan.close()
+
+
+def test_full_stack_216_swiglu_plan(cuda, stack):
+    """The reference's fused dispatch over the same bytes: per layer q, k, v,
+    o, one SwiGLU GEMV for up with the gate, and down (216 GEMVs); the
+    SwiGLU GEMVs stream both weights in one item per block."""
+    by = {t["name"]: t for t in stack}
+    items, checks = [], []
+    for t in stack:
+        if t["name"].endswith("ffn_gate.weight"):
+            continue
+        y = torch.full((t["rows"],), float("nan"), device="cuda")
+        if t["name"].endswith("ffn_up.weight"):
+            g = by[t["name"].replace("ffn_up", "ffn_gate")]
+            items.append((t["w"], t["x"], y, g["w"]))
+            checks.append((t, g, y))
+        else:
+            items.append((t["w"], t["x"], y))
+            checks.append((t, None, y))
+    assert len(items) == 216
+    plan = api.Plan(items)
+    assert plan.workgroups == 2 * torch.cuda.get_device_properties(0).multi_processor_count
+    assert plan.launch()
+    torch.cuda.synchronize()
+    for layer in CHECK_LAYERS:
+        for j in range(6):
+            t, g, y = checks[6 * layer + j]
+            assert_gemv_parity(y.cpu().numpy(), t["w"].tiles.cpu().numpy(), t["rows"], t["cols"], t["x"].cpu().numpy(),
+                               gate_tiles=None if g is None else g["w"].tiles.cpu().numpy(), label=t["name"])
+    plan.close()
+
+
+# ----------------------------------------------------------------- many items per workgroup
+
+KINDS = {
+    # rows, cols, gate, add: the item kinds of the single-vector sweep
+    "pair": (128, 512, False, False),          # one pair item (two 64-row blocks, one K chunk)
+    "pair_add": (256, 4096, False, True),      # two pair items with the add epilogue
+    "glu_one_item": (192, 4096, True, False),  # SwiGLU, both weight streams in one item per block
+    "split_k": (64, 12800, False, False),      # two chunks meeting in the arrival chain
+    "split_k_glu": (64, 12800, True, True),    # two chunks x two streams, add then SwiGLU
+    "tail": (96, 4736, False, False),          # 74 groups: full steps and a short tail
+}
+COUNTS = {"pair": 600, "pair_add": 150, "glu_one_item": 150, "split_k": 150, "split_k_glu": 60, "tail": 60}
+
+
+def make_gemvs(batch: int, seed: int):
+    rng = np.random.default_rng(seed)
+    order = [k for k, n in COUNTS.items() for _ in range(n)]
+    rng.shuffle(order)
+    gemvs = []
+    for i, kind in enumerate(order):
+        rows, cols, gate, add = KINDS[kind]
+        t = random_tiles(rows, cols, seed * 1000 + i)
+        gt = random_tiles(rows, cols, seed * 1000 + 500000 + i) if gate else None
+        xs = np.stack([O.gaussian_x(cols, seed * 7 + 11 * i + v) for v in range(batch)])
+        adds = np.stack([O.gaussian_x(rows, seed * 5 + 13 * i + v) for v in range(batch)]) if add else None
+        gemvs.append(dict(kind=kind, rows=rows, cols=cols, t=t, gt=gt, xs=xs, adds=adds,
+                          w=api.QWeight.from_tiles(dev_u8(t), rows, cols),
+                          g=None if gt is None else api.QWeight.from_tiles(dev_u8(gt), rows, cols),
+                          xd=dev_f32(xs if batch > 1 else xs[0]),
+                          ad=None if adds is None else dev_f32(adds if batch > 1 else adds[0])))
+    return gemvs
+
+
+def run_plan(gemvs, batch: int):
+    ys = [torch.full((batch, g["rows"]) if batch > 1 else (g["rows"],), float("nan"), device="cuda") for g in gemvs]
+    plan = api.Plan([(g["w"], g["xd"], y, g["g"], g["ad"]) for g, y in zip(gemvs, ys)], batch=batch)
+    assert plan.launch()
+    torch.cuda.synchronize()
+    wg = plan.workgroups
+    plan.close()
+    return ys, wg
+
+
+def test_plan_with_many_items_per_workgroup(cuda):
+    """1,170 GEMVs of every single-vector item kind, 2,010 items for 512
+    workgroups, so workgroups run several items of mixed kinds in turn (the
+    prefetch across item ends, alternating reduction buffers, pair, one-pass
+    and both-stream items).  Every output against both bars, and each GEMV
+    bit-identical to the same GEMV run alone in a plan of its own (one item
+    per workgroup)."""
+    gemvs = make_gemvs(1, 3)
+    ys, wg = run_plan(gemvs, 1)
+    items = sum({"pair": 1, "pair_add": 2, "glu_one_item": 3, "split_k": 2, "split_k_glu": 4, "tail": 2}[g["kind"]]
+                for g in gemvs)
+    assert items > 3 * wg
+    for g, y in zip(gemvs, ys):
+        assert_gemv_parity(y.cpu().numpy(), g["t"], g["rows"], g["cols"], g["xs"][0], gate_tiles=g["gt"],
+                           add=None if g["adds"] is None else g["adds"][0], label=g["kind"])
+    for i in range(0, len(gemvs), 23):
+        alone, _ = run_plan([gemvs[i]], 1)
+        assert torch.equal(alone[0], ys[i]), (i, gemvs[i]["kind"])
+
+
+def test_batched_plan_with_many_items(cuda):
+    """The batched sweep's queue with more items than workgroups (three
+    vectors per GEMV): every vector of every GEMV against both bars."""
+    gemvs = make_gemvs(3, 4)
+    ys, wg = run_plan(gemvs, 3)
+    assert len(gemvs) > wg
+    for g, y in zip(gemvs, ys):
+        yh = y.cpu().numpy()
+        for v in range(3):
+            assert_gemv_parity(yh[v], g["t"], g["rows"], g["cols"], g["xs"][v], gate_tiles=g["gt"],
+                               add=None if g["adds"] is None else g["adds"][v], label=(g["kind"], v))
