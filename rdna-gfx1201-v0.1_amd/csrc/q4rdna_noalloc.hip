@@ -1,0 +1,95 @@
+// q4rdna_mul_mat_ex_noalloc: q4rdna_mul_mat_ex with its split-K workspace in
+// a fixed device array instead of memory the library allocates, for callers
+// that cannot allocate (code under HIP graph capture, tight serving loops,
+// harnesses that forbid hipMalloc).
+//
+// The array, `scratch`, holds Q4RDNA_NOALLOC_PARTIAL_FLOATS fp32 partial
+// sums followed by Q4RDNA_NOALLOC_COUNTERS arrival counters; every GPU the
+// library runs on holds its own copy until the process ends.  In host code
+// the name `scratch` is only a stand-in for the symbol: the device address of
+// a GPU's copy comes from hipGetSymbolAddress with that GPU current, once per
+// GPU, and only that address is ever passed to a kernel.
+//
+// Counters must be zero when a launch starts.  They are zero when the code
+// object is loaded, the first call on a GPU clears them once more with a fill
+// kernel on its stream, and every launch leaves them zero (the last
+// workgroup of a row tile resets its counter).  Partial sums need no
+// clearing: every launch writes the ones it reads.  Every call on a GPU
+// shares that GPU's array, so calls that overlap on one GPU race: issue them
+// on one stream, or order them with events.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <mutex>
+
+#include "q4rdna.h"
+#include "q4rdna_internal.h"
+#include "q4rdna_runtime.h"
+
+namespace {
+
+constexpr size_t kPartialBytes = static_cast<size_t>(Q4RDNA_NOALLOC_PARTIAL_FLOATS) * sizeof(float);
+constexpr size_t kScratchBytes = kPartialBytes + static_cast<size_t>(Q4RDNA_NOALLOC_COUNTERS) * sizeof(uint32_t);
+static_assert(kPartialBytes % 256 == 0, "the counters start 256-byte aligned");
+
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+__global__ __launch_bounds__(256) void clear_counters(uint32_t *__restrict__ counters, uint32_t count) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x) counters[i] = 0u;
+}
+
+// Device address of each GPU's copy of `scratch`, looked up on the first
+// call on that GPU (a fixed table: nothing is allocated).
+constexpr int kMaxDevices = 64;
+std::atomic<uint8_t *> g_scratch[kMaxDevices];
+std::mutex g_setup;
+
+int scratch_of(int device, hipStream_t stream, uint8_t **out) {
+    if (device < 0 || device >= kMaxDevices)
+        return q4rdna::set_error(Q4RDNA_ERR_ARGUMENT, "device %d is outside the no-alloc table", device);
+    uint8_t *p = g_scratch[device].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> lock(g_setup);
+        p = g_scratch[device].load(std::memory_order_relaxed);
+        if (p == nullptr) {
+            // The weight's device is the current device (checked by the
+            // caller), so this is that GPU's copy.
+            hipError_t e = hipGetSymbolAddress(reinterpret_cast<void **>(&p), HIP_SYMBOL(scratch));
+            if (e != hipSuccess || p == nullptr)
+                return q4rdna::set_error(Q4RDNA_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+            hipLaunchKernelGGL(clear_counters, dim3(Q4RDNA_NOALLOC_COUNTERS / 256), dim3(256), 0, stream,
+                               reinterpret_cast<uint32_t *>(p + kPartialBytes), Q4RDNA_NOALLOC_COUNTERS);
+            e = hipGetLastError();
+            if (e != hipSuccess) return q4rdna::set_error(Q4RDNA_ERR_HIP, "counter clear: %s", hipGetErrorString(e));
+            g_scratch[device].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return Q4RDNA_OK;
+}
+
+}  // namespace
+
+extern "C" int q4rdna_mul_mat_ex_noalloc(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x,
+                                         const float *add, float *y, const q4rdna_launch_options *options,
+                                         void *stream) {
+    uint32_t split = 0;
+    int rc = q4rdna::check_mul_mat_ex(w, gate, x, add, y, options, &split);
+    if (rc != Q4RDNA_OK) return rc;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (split == 1)
+        return q4rdna::launch_gemv_in(w, gate ? gate->tiles : nullptr, x, add, y, 1, nullptr, nullptr, s);
+    size_t partial_floats = 0, counters = 0;
+    q4rdna::gemv_workspace_need(w, gate != nullptr, split, &partial_floats, &counters);
+    if (partial_floats > Q4RDNA_NOALLOC_PARTIAL_FLOATS || counters > Q4RDNA_NOALLOC_COUNTERS)
+        return q4rdna::set_error(Q4RDNA_ERR_ARGUMENT,
+                                 "%ux%u at split %u needs %zu partial floats and %zu counters; the no-alloc "
+                                 "scratch holds %u and %u",
+                                 w->rows, w->columns, split, partial_floats, counters,
+                                 static_cast<unsigned>(Q4RDNA_NOALLOC_PARTIAL_FLOATS),
+                                 static_cast<unsigned>(Q4RDNA_NOALLOC_COUNTERS));
+    uint8_t *base = nullptr;
+    if ((rc = scratch_of(w->device, s, &base)) != Q4RDNA_OK) return rc;
+    return q4rdna::launch_gemv_in(w, gate ? gate->tiles : nullptr, x, add, y, split, reinterpret_cast<float *>(base),
+                                  reinterpret_cast<uint32_t *>(base + kPartialBytes), s);
+}

@@ -31,6 +31,8 @@ ALGO_MSE = 3
 
 GLU_SWIGLU = 0
 MAX_BATCH = 8
+NOALLOC_PARTIAL_FLOATS = 1 << 20
+NOALLOC_COUNTERS = 16384
 
 # Every symbol include/q4rdna.h declares.
 EXPORTS = (
@@ -38,7 +40,7 @@ EXPORTS = (
     "q4rdna_sidecar_open_memory", "q4rdna_sidecar_close", "q4rdna_sidecar_count", "q4rdna_sidecar_entry",
     "q4rdna_find", "q4rdna_weight_from_device", "q4rdna_default_sidecar", "q4rdna_scope_allows",
     "q4rdna_mul_mat", "q4rdna_mul_mat_add", "q4rdna_mul_mat_glu", "q4rdna_mul_mat_ex", "q4rdna_mul_mat_batch",
-    "q4rdna_policy_split_k", "q4rdna_plan_create", "q4rdna_plan_create_batch", "q4rdna_plan_launch",
+    "q4rdna_policy_split_k", "q4rdna_mul_mat_ex_noalloc", "q4rdna_plan_create", "q4rdna_plan_create_batch", "q4rdna_plan_launch",
     "q4rdna_plan_prepare",
     "q4rdna_plan_sweep", "q4rdna_plan_destroy",
     "q4rdna_plan_workgroups", "q4rdna_pack", "q4rdna_dequantize",
@@ -101,6 +103,7 @@ def load() -> ctypes.CDLL:
         "q4rdna_mul_mat_ex": (i32, [WP, WP, vp, vp, vp, ctypes.POINTER(LaunchOptions), vp]),
         "q4rdna_mul_mat_batch": (i32, [WP, WP, vp, u32, vp, vp, ctypes.POINTER(LaunchOptions), vp]),
         "q4rdna_policy_split_k": (u32, [u32, u32, i32]),
+        "q4rdna_mul_mat_ex_noalloc": (i32, [WP, WP, vp, vp, vp, ctypes.POINTER(LaunchOptions), vp]),
         "q4rdna_plan_create": (i32, [ctypes.POINTER(GemvDesc), u32, i32, ctypes.POINTER(vp)]),
         "q4rdna_plan_create_batch": (i32, [ctypes.POINTER(GemvDesc), u32, u32, i32, ctypes.POINTER(vp)]),
         "q4rdna_plan_launch": (i32, [vp, vp]),

@@ -1,0 +1,130 @@
+"""q4rdna_mul_mat_ex_noalloc through the C ABI: the allocation-free variant
+of q4rdna_mul_mat_ex, whose split-K workspace is a fixed per-GPU device
+array.  Its outputs must equal q4rdna_mul_mat_ex's at the same split bit for
+bit (same kernels, same summation order), on consecutive calls with the
+second smaller than the first, with every epilogue; a launch that needs more
+than the array holds is refused and touches nothing; and calls captured into
+a HIP graph replay correctly."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+import q4rdna
+from q4rdna import _lib, api
+from conftest import assert_gemv_parity
+
+pytestmark = pytest.mark.gpu
+
+
+def random_tiles(rows: int, cols: int, seed: int) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    g = cols // 64
+    t = rng.integers(0, 256, (rows // 32, g, 1088), dtype=np.uint8)
+    s = (rng.uniform(1e-3, 3e-2, (rows // 32, g, 32)) * rng.choice([-1.0, 1.0], (rows // 32, g, 32))).astype(np.float16)
+    t[:, :, :64] = s.view(np.uint8).reshape(rows // 32, g, 64)
+    return t.reshape(-1)
+
+
+def weight(rows, cols, seed):
+    t = random_tiles(rows, cols, seed)
+    return t, api.QWeight.from_tiles(torch.from_numpy(t).cuda(), rows, cols)
+
+
+def call(fn, w, gate, x, add, y, split, stream):
+    opts = _lib.LaunchOptions()
+    opts.split_k = split
+    return fn(ctypes.byref(w.raw), ctypes.byref(gate.raw) if gate is not None else None, x.data_ptr(),
+              None if add is None else add.data_ptr(), y.data_ptr(), ctypes.byref(opts), stream)
+
+
+CASES = [
+    # rows, cols, split, gate, add: a larger launch, then a smaller one
+    (4096, 12288, 6, True, True),
+    (1024, 4096, 4, False, False),
+    (4096, 4096, 2, False, True),
+    (96, 8192, 16, True, False),
+]
+
+
+def test_noalloc_equals_mul_mat_ex(cuda):
+    L = q4rdna.load()
+    s = torch.cuda.current_stream().cuda_stream
+    for i, (rows, cols, split, with_gate, with_add) in enumerate(CASES):
+        t, w = weight(rows, cols, 10 + i)
+        gt, g = weight(rows, cols, 20 + i) if with_gate else (None, None)
+        x_np = O.gaussian_x(cols, 30 + i)
+        add_np = O.gaussian_x(rows, 40 + i) if with_add else None
+        x = torch.from_numpy(x_np).cuda()
+        add = None if add_np is None else torch.from_numpy(add_np).cuda()
+        y_ref = torch.full((rows,), float("nan"), device="cuda")
+        y_na = torch.full((rows,), float("nan"), device="cuda")
+        assert call(L.q4rdna_mul_mat_ex, w, g, x, add, y_ref, split, s) == q4rdna.OK
+        assert call(L.q4rdna_mul_mat_ex_noalloc, w, g, x, add, y_na, split, s) == q4rdna.OK, q4rdna.last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(y_na, y_ref), (rows, cols, split)
+        assert_gemv_parity(y_na.cpu().numpy(), t, rows, cols, x_np, gate_tiles=gt, add=add_np, label=(rows, cols))
+
+
+def test_noalloc_refuses_what_does_not_fit(cuda):
+    """151936 x 4096 at split 8 needs 1,215,488 partial floats, more than the
+    1,048,576 the array holds: refused, nothing launched."""
+    L = q4rdna.load()
+    rows, cols = 151936, 4096
+    w = api.QWeight.from_tiles(torch.zeros(api.packed_size(rows, cols), dtype=torch.uint8, device="cuda"), rows, cols)
+    x = torch.zeros(cols, device="cuda")
+    y = torch.full((rows,), 7.0, device="cuda")
+    rc = call(L.q4rdna_mul_mat_ex_noalloc, w, None, x, None, y, 8, torch.cuda.current_stream().cuda_stream)
+    assert rc == q4rdna.ERR_ARGUMENT
+    assert "no-alloc scratch" in q4rdna.last_error()
+    torch.cuda.synchronize()
+    assert (y == 7.0).all()
+    # split 1 needs no workspace at all and runs at any size
+    rc = call(L.q4rdna_mul_mat_ex_noalloc, w, None, x, None, y, 1, torch.cuda.current_stream().cuda_stream)
+    assert rc == q4rdna.OK
+    torch.cuda.synchronize()
+    assert (y == 0.0).all()
+
+
+def test_noalloc_calls_replay_from_a_hip_graph(cuda):
+    """Two allocation-free launches captured into one graph (after a first
+    call has set the GPU up), replayed with new activations and eager work in
+    between: every replay equals the eager results bit for bit."""
+    L = q4rdna.load()
+    t1, w1 = weight(4096, 4096, 50)
+    t2, w2 = weight(1024, 12288, 51)
+    x1 = torch.empty(4096, device="cuda")
+    x2 = torch.empty(12288, device="cuda")
+    y1 = torch.empty(4096, device="cuda")
+    y2 = torch.empty(1024, device="cuda")
+    st = torch.cuda.Stream()
+
+    def work():
+        assert call(L.q4rdna_mul_mat_ex_noalloc, w1, None, x1, None, y1, 2, st.cuda_stream) == q4rdna.OK
+        assert call(L.q4rdna_mul_mat_ex_noalloc, w2, None, x2, None, y2, 6, st.cuda_stream) == q4rdna.OK
+
+    with torch.cuda.stream(st):
+        x1.normal_()
+        x2.normal_()
+        work()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        work()
+    for rep in range(3):
+        with torch.cuda.stream(st):
+            x1.normal_()
+            x2.normal_()
+            work()
+        st.synchronize()
+        want = [y1.clone(), y2.clone()]
+        y1.fill_(float("nan"))
+        y2.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(st):
+            g.replay()
+        st.synchronize()
+        assert torch.equal(y1, want[0]) and torch.equal(y2, want[1]), rep
+    assert_gemv_parity(y2.cpu().numpy(), t2, 1024, 12288, x2.cpu().numpy(), label="graph replay")
