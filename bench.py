@@ -570,6 +570,131 @@ def tensor_table(seed: int):
     return rows_out
 
 
+def layer_chain(tensors, replays: int, check_layers=(0, 17, 35)):
+    """The stack as a decoder runs it: layer l+1's input depends on layer l,
+    so every projection waits for the one before.  Per layer: q, k, v on
+    x_l; o on q's output plus the residual x_l (o's real input is the
+    attention output, a step outside this path) giving h; gate/up SwiGLU on
+    h; down on that plus the residual h, giving x_{l+1}.  Two dispatches over
+    the same weights, each captured into one HIP graph of all 36 layers and
+    replayed:
+      reference  the reference's hooks: q, k, v, o(+add), gate/up SwiGLU,
+                 down(+add) as six per-tensor launches (VALU kernel)
+      grouped    q/k/v as one group launch sharing x (burst kernel), then
+                 o(+add), gate/up SwiGLU and down(+add) through the
+                 per-tensor entry points: four launches
+      burst      the same four launches all on the burst kernel
+                 (activation converted in the kernel)
+    Parity: every launch of layers `check_layers` against the fp64 oracle
+    on the inputs it actually read."""
+    import numpy as np
+    import torch
+    import oracle as O
+    from q4rdna import _lib, api
+
+    by = {t["name"]: t for t in tensors}
+    layers = len(tensors) // 7
+
+    def w(l, part):
+        return by[f"blk.{l}.{part}.weight"]["w"]
+
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x51EEC000)
+    x0 = torch.randn(4096, generator=gen, device=dev)
+
+    def buffers():
+        b = []
+        for l in range(layers):
+            b.append(dict(q=torch.empty(4096, device=dev), k=torch.empty(1024, device=dev),
+                          v=torch.empty(1024, device=dev), h=torch.empty(4096, device=dev),
+                          act=torch.empty(12288, device=dev), out=torch.empty(4096, device=dev)))
+        return b
+
+    def run(dispatch, bufs, stream):
+        for l in range(layers):
+            b = bufs[l]
+            x = x0 if l == 0 else bufs[l - 1]["out"]
+            if dispatch == "reference":
+                api.mul_mat(w(l, "attn_q"), x, b["q"], stream=stream)
+                api.mul_mat(w(l, "attn_k"), x, b["k"], stream=stream)
+                api.mul_mat(w(l, "attn_v"), x, b["v"], stream=stream)
+                api.mul_mat_add(w(l, "attn_output"), b["q"], x, b["h"], stream=stream)
+                api.mul_mat_glu(w(l, "ffn_up"), w(l, "ffn_gate"), b["h"], b["act"], stream=stream)
+                api.mul_mat_add(w(l, "ffn_down"), b["act"], b["h"], b["out"], stream=stream)
+            elif dispatch == "grouped":
+                api.mul_mat_group([(w(l, "attn_q"), b["q"]), (w(l, "attn_k"), b["k"]), (w(l, "attn_v"), b["v"])], x,
+                                  stream=stream)
+                api.mul_mat_add(w(l, "attn_output"), b["q"], x, b["h"], stream=stream)
+                api.mul_mat_glu(w(l, "ffn_up"), w(l, "ffn_gate"), b["h"], b["act"], stream=stream)
+                api.mul_mat_add(w(l, "ffn_down"), b["act"], b["h"], b["out"], stream=stream)
+            else:
+                api.mul_mat_group([(w(l, "attn_q"), b["q"]), (w(l, "attn_k"), b["k"]), (w(l, "attn_v"), b["v"])], x,
+                                  stream=stream)
+                api.mul_mat_ex(w(l, "attn_output"), b["q"], b["h"], add=x, kernel=_lib.KERNEL_BURST, stream=stream)
+                api.mul_mat_group([(w(l, "ffn_up"), b["act"], w(l, "ffn_gate"))], b["h"], stream=stream)
+                api.mul_mat_ex(w(l, "ffn_down"), b["act"], b["out"], add=b["h"], kernel=_lib.KERNEL_BURST,
+                               stream=stream)
+
+    out = {}
+    for dispatch in ("reference", "grouped", "burst"):
+        bufs = buffers()
+        st = torch.cuda.Stream()
+        with torch.cuda.stream(st):
+            run(dispatch, bufs, st.cuda_stream)  # eager: allocates the stream's split-K workspace
+        torch.cuda.synchronize()
+        # Parity on the eager run: each launch against the oracle on its own inputs.
+        worst = 0.0
+        for l in check_layers:
+            if l >= layers:
+                continue
+            b = bufs[l]
+            x = (x0 if l == 0 else bufs[l - 1]["out"]).cpu().numpy()
+            q, h, act = b["q"].cpu().numpy(), b["h"].cpu().numpy(), b["act"].cpu().numpy()
+
+            def gate_of(y, part, xin, add=None, gate_part=None):
+                t = by[f"blk.{l}.{part}.weight"]
+                y64, a64 = O.gemv_f64(t["w"].tiles.cpu().numpy(), t["rows"], t["cols"], xin)
+                want, bound = y64, a64
+                if add is not None:
+                    want, bound = want + add.astype(np.float64), bound + np.abs(add)
+                if gate_part is not None:
+                    g = by[f"blk.{l}.{gate_part}.weight"]
+                    g64, ga = O.gemv_f64(g["w"].tiles.cpu().numpy(), g["rows"], g["cols"], xin)
+                    want = want * O.silu(g64)
+                rms = float(np.sqrt(np.mean(want ** 2)))
+                return float(np.max(np.abs(y.astype(np.float64) - want) / np.maximum(np.abs(want), 0.01 * rms)))
+
+            worst = max(worst, gate_of(q, "attn_q", x), gate_of(b["k"].cpu().numpy(), "attn_k", x),
+                        gate_of(b["v"].cpu().numpy(), "attn_v", x), gate_of(h, "attn_output", q, add=x),
+                        gate_of(act, "ffn_up", h, gate_part="ffn_gate"),
+                        gate_of(b["out"].cpu().numpy(), "ffn_down", act, add=h))
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=st):
+            run(dispatch, bufs, st.cuda_stream)
+        with torch.cuda.stream(st):
+            for _ in range(3):
+                graph.replay()
+            a = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            a.record(st)
+            for _ in range(replays):
+                graph.replay()
+            e.record(st)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(e) * 1000.0 / (replays * layers)
+        layer_bytes = sum(algorithmic_bytes(by[f"blk.0.{p}.weight"]["rows"], by[f"blk.0.{p}.weight"]["cols"])
+                          for p in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"))
+        out[dispatch] = dict(launches_per_layer=6 if dispatch == "reference" else 4, us_per_layer=round(us, 2),
+                             gb_per_s=round(layer_bytes / us / 1e3, 1), pct_of_peak=round(layer_bytes / us / 1e3 / 80, 2),
+                             parity_gate_max=worst)
+        log(f"[layer] {dispatch}: {us:.2f} us per layer ({out[dispatch]['gb_per_s']} GB/s), parity gate {worst:.2e}")
+        del graph, bufs
+    out["layers"] = layers
+    out["target_us_per_layer_at_70pct"] = 18.36
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -591,6 +716,10 @@ def main() -> int:
     ap.add_argument("--batches", type=str, default="",
                     help="comma-separated batch sizes (e.g. 2,4,8): time the stack with that many activation "
                          "vectors per GEMV and print one JSON line with the table instead of the stack bench")
+    ap.add_argument("--layer-chain", action="store_true",
+                    help="the stack as dependent decoder layers (q/k/v -> o -> gate/up -> down, 36 layers, HIP graph): "
+                         "us per layer for the reference's per-tensor dispatch and for the burst dispatch; prints one "
+                         "JSON line instead of the stack bench")
     ap.add_argument("--tensors", action="store_true",
                     help="per-tensor launch figures (projection shapes, lm_head, long-K split sweep with "
                          "outlier groups); prints one JSON line with the table instead of the stack bench")
@@ -609,6 +738,9 @@ def main() -> int:
 
     tensors, _data = build_stack(args.layers, args.seed)
     stack_bytes = sum(algorithmic_bytes(t["rows"], t["cols"]) for t in tensors)
+    if args.layer_chain:
+        print(json.dumps({"layer_chain": layer_chain(tensors, max(args.steps, 20))}), flush=True)
+        return 0
     if args.batches:
         sizes = [int(v) for v in args.batches.split(",") if v]
         print(json.dumps({"batched": batch_table(tensors, sizes, args.steps, args.warmup, args.seed)}), flush=True)

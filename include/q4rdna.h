@@ -145,12 +145,20 @@ int q4rdna_mul_mat_add(const q4rdna_weight *w, const float *x, int64_t x_ne0, co
 int q4rdna_mul_mat_glu(const q4rdna_weight *up, const q4rdna_weight *gate, const float *x,
                        int64_t x_ne0, int glu_op, float *y, int64_t y_ne0, void *stream);
 
-/* Launch options for sweeps: split_k = number of K chunks reduced across
- * workgroups (0 = the shape policy, the reference's launch policy at
- * source/q4rdna.cu:578-680 and its LLAMA_Q4_RDNA_COOP override :579-584). */
+/* Launch options: split_k = number of K chunks reduced across workgroups of
+ * the VALU kernel (0 = the shape policy, the reference's launch policy at
+ * source/q4rdna.cu:578-680 and its LLAMA_Q4_RDNA_COOP override :579-584);
+ * kernel = which per-tensor kernel runs (Q4RDNA_KERNEL_*; 0 = the shape
+ * policy); burst_steps = K chunk of a burst unit in 16-group steps (1 or 2,
+ * 0 = the shape policy).  Zero-initialised options mean "policy" throughout. */
+#define Q4RDNA_KERNEL_POLICY 0
+#define Q4RDNA_KERNEL_VALU 1  /* split-K VALU kernel (split_k applies) */
+#define Q4RDNA_KERNEL_BURST 2 /* int8-MFMA burst kernel (burst_steps applies) */
 typedef struct q4rdna_launch_options {
     uint32_t split_k;
-    uint32_t reserved[7];
+    uint32_t kernel;
+    uint32_t burst_steps;
+    uint32_t reserved[5];
 } q4rdna_launch_options;
 
 /* q4rdna_mul_mat / _add / _glu with explicit options (add, gate may be NULL). */
@@ -171,6 +179,26 @@ int q4rdna_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const f
 int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x, uint32_t n,
                          const float *add, float *y, const q4rdna_launch_options *options,
                          void *stream);
+
+/* Several GEMVs that share one activation, in one launch: y_i = W_i x
+ * (+ add_i), or with gate_tiles y_i = (W_i x + add_i) * silu(G_i x) -- e.g.
+ * q, k and v of a decoder layer, or its gate and up projections.  count =
+ * 1..Q4RDNA_MAX_GROUP; every weight has K = x_ne0 columns (else
+ * NOT_APPLICABLE) and lives on the current device; gate_tiles is given for
+ * every descriptor or for none, each of its weight's shape; no y may overlap
+ * x.  x is converted once per workgroup in the kernel (no separate prepare
+ * launch).  The split-K scratch is the stream's, as for q4rdna_mul_mat.  No
+ * reference counterpart: the reference launches one kernel per projection
+ * and fuses only gate/up (source/q4rdna.cu:736-741,769-793). */
+#define Q4RDNA_MAX_GROUP 8
+typedef struct q4rdna_group_desc {
+    q4rdna_weight weight;      /* W (the up projection for SwiGLU) */
+    const uint8_t *gate_tiles; /* SwiGLU gate tiles of W's shape, or NULL */
+    const float *add;          /* [rows] or NULL */
+    float *y;                  /* [rows] */
+} q4rdna_group_desc;
+int q4rdna_mul_mat_group(const q4rdna_group_desc *descs, uint32_t count, const float *x, int64_t x_ne0,
+                         const q4rdna_launch_options *options, void *stream);
 
 /* Split-K factor the shape policy picks for rows x columns on `device`. */
 uint32_t q4rdna_policy_split_k(uint32_t rows, uint32_t columns, int device);

@@ -100,6 +100,34 @@ hipError_t launch_prep_batch(const PlanDesc *descs, const uint32_t *owner, uint3
                              hipStream_t stream);
 hipError_t launch_plan_batch(const PlanDesc *descs, uint32_t items, uint32_t n, uint32_t workgroups, uint32_t *sched,
                              hipStream_t stream);
+// A burst launch: up to kMaxBurst GEMVs that share one activation x of
+// `cols` floats, all of K = cols.  A unit is (GEMV, 64-row block, K chunk of
+// 16 * steps groups), one workgroup each, units numbered GEMV by GEMV from
+// unit_begin, block-major then chunk; `chunks` chunks per block.  With
+// gate != nullptr (every GEMV of a launch, or none) a unit streams the gate
+// tiles of its block too and the epilogue is SwiGLU.  When chunks > 1 the
+// units of a block meet in partial[stream][chunk][rows] through
+// counters[block] (zero between launches, left zero).
+constexpr uint32_t kMaxBurst = 8;
+constexpr uint32_t kBurstStepGroups = 16;  // groups of one 64-row workgroup step (four waves of four groups)
+struct BurstGemv {
+    const uint8_t *w;
+    const uint8_t *gate;
+    const float *add;
+    float *y;
+    float *partial;
+    uint32_t *counters;
+    uint32_t rows;
+    uint32_t unit_begin;
+};
+struct BurstArgs {
+    BurstGemv g[kMaxBurst];
+    const float *x;
+    uint32_t count, cols, chunks, units;
+};
+// steps = 1 or 2 (K chunk of 16 or 32 groups per unit).
+hipError_t launch_burst(const BurstArgs &args, uint32_t steps, hipStream_t stream);
+
 hipError_t launch_dequant(const uint8_t *w, uint32_t rows, uint32_t cols, float *out,
                           hipStream_t stream);
 hipError_t launch_pack(const float *w, uint32_t rows, uint32_t cols, int algorithm, uint8_t *tiles,

@@ -13,7 +13,7 @@
 // Counters must be zero when a launch starts.  They are zero when the code
 // object is loaded, the first call on a GPU clears them once more with a fill
 // kernel on its stream, and every launch leaves them zero (the last
-// workgroup of a row tile resets its counter).  Partial sums need no
+// workgroup to arrive at a row tile or 64-row block resets its counter).  Partial sums need no
 // clearing: every launch writes the ones it reads.  Every call on a GPU
 // shares that GPU's array, so calls that overlap on one GPU race: issue them
 // on one stream, or order them with events.
@@ -73,23 +73,21 @@ int scratch_of(int device, hipStream_t stream, uint8_t **out) {
 extern "C" int q4rdna_mul_mat_ex_noalloc(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x,
                                          const float *add, float *y, const q4rdna_launch_options *options,
                                          void *stream) {
-    uint32_t split = 0;
-    int rc = q4rdna::check_mul_mat_ex(w, gate, x, add, y, options, &split);
+    q4rdna::TensorLaunch L{};
+    int rc = q4rdna::check_mul_mat_ex(w, gate, x, add, y, options, &L);
     if (rc != Q4RDNA_OK) return rc;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (split == 1)
-        return q4rdna::launch_gemv_in(w, gate ? gate->tiles : nullptr, x, add, y, 1, nullptr, nullptr, s);
-    size_t partial_floats = 0, counters = 0;
-    q4rdna::gemv_workspace_need(w, gate != nullptr, split, &partial_floats, &counters);
-    if (partial_floats > Q4RDNA_NOALLOC_PARTIAL_FLOATS || counters > Q4RDNA_NOALLOC_COUNTERS)
+    const uint8_t *gt = gate ? gate->tiles : nullptr;
+    if (L.partial_floats == 0 && L.counters == 0) return q4rdna::launch_tensor_in(L, w, gt, x, add, y, nullptr, nullptr, s);
+    if (L.partial_floats > Q4RDNA_NOALLOC_PARTIAL_FLOATS || L.counters > Q4RDNA_NOALLOC_COUNTERS)
         return q4rdna::set_error(Q4RDNA_ERR_ARGUMENT,
-                                 "%ux%u at split %u needs %zu partial floats and %zu counters; the no-alloc "
-                                 "scratch holds %u and %u",
-                                 w->rows, w->columns, split, partial_floats, counters,
+                                 "%ux%u needs %zu partial floats and %zu counters; the no-alloc scratch holds %u "
+                                 "and %u",
+                                 w->rows, w->columns, L.partial_floats, L.counters,
                                  static_cast<unsigned>(Q4RDNA_NOALLOC_PARTIAL_FLOATS),
                                  static_cast<unsigned>(Q4RDNA_NOALLOC_COUNTERS));
     uint8_t *base = nullptr;
     if ((rc = scratch_of(w->device, s, &base)) != Q4RDNA_OK) return rc;
-    return q4rdna::launch_gemv_in(w, gate ? gate->tiles : nullptr, x, add, y, split, reinterpret_cast<float *>(base),
-                                  reinterpret_cast<uint32_t *>(base + kPartialBytes), s);
+    return q4rdna::launch_tensor_in(L, w, gt, x, add, y, reinterpret_cast<float *>(base),
+                                    reinterpret_cast<uint32_t *>(base + kPartialBytes), s);
 }

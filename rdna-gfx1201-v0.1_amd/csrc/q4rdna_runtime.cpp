@@ -175,21 +175,19 @@ uint32_t resolve_split(const q4rdna_weight *w, uint32_t split) {
     return std::max<uint32_t>(split, 1);
 }
 
-int launch_one(const q4rdna_weight *w, const uint8_t *gate, const float *x, const float *add, float *y,
-               uint32_t split, hipStream_t stream) {
-    split = resolve_split(w, split);
+// Per-tensor launch with the stream's split-K workspace.
+int launch_one(const q4rdna::TensorLaunch &launch, const q4rdna_weight *w, const uint8_t *gate, const float *x,
+               const float *add, float *y, hipStream_t stream) {
     float *partial = nullptr;
     uint32_t *counters = nullptr;
-    if (split > 1) {
-        size_t pf = 0, cc = 0;
-        q4rdna::gemv_workspace_need(w, gate != nullptr, split, &pf, &cc);
+    if (launch.partial_floats > 0 || launch.counters > 0) {
         Workspace *ws = nullptr;
-        int rc = get_workspace(w->device, stream, pf, cc, &ws);
+        int rc = get_workspace(w->device, stream, launch.partial_floats, launch.counters, &ws);
         if (rc != Q4RDNA_OK) return rc;
         partial = ws->partial;
         counters = ws->counters;
     }
-    return q4rdna::launch_gemv_in(w, gate, x, add, y, split, partial, counters, stream);
+    return q4rdna::launch_tensor_in(launch, w, gate, x, add, y, partial, counters, stream);
 }
 
 // Preconditions shared by the GEMV entry points.  NOT_APPLICABLE mirrors the
@@ -211,10 +209,37 @@ int check_io(const float *x, const float *y) {
 
 }  // namespace
 
+namespace {
+
+// Burst units of 16 * steps groups: one step while that leaves at most
+// three units per CU, else two (fewer, longer units and shorter arrival
+// chains where there is plenty of parallelism).
+uint32_t burst_steps_policy(uint64_t blocks, uint32_t groups, uint32_t cus) {
+    const uint64_t units1 = blocks * ((groups + q4rdna::kBurstStepGroups - 1) / q4rdna::kBurstStepGroups);
+    return units1 > 3ull * cus && groups > q4rdna::kBurstStepGroups ? 2u : 1u;
+}
+
+uint32_t burst_chunks(uint32_t groups, uint32_t steps) {
+    const uint32_t chunk = q4rdna::kBurstStepGroups * steps;
+    return (groups + chunk - 1) / chunk;
+}
+
+uint32_t blocks_of(uint32_t rows) { return (rows + q4rdna::kBlockRows - 1) / q4rdna::kBlockRows; }
+
+// Which kernel serves a per-tensor launch when the caller leaves it to the
+// policy.
+uint32_t tensor_kernel_policy(const q4rdna_weight *w, bool gate) {
+    (void)w;
+    (void)gate;
+    return Q4RDNA_KERNEL_VALU;
+}
+
+}  // namespace
+
 namespace q4rdna {
 
 int check_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x, const float *add,
-                     const float *y, const q4rdna_launch_options *options, uint32_t *split) {
+                     const float *y, const q4rdna_launch_options *options, TensorLaunch *launch) {
     int rc = check_weight(w);
     if (rc != Q4RDNA_OK) return rc;
     if (gate != nullptr) {
@@ -226,37 +251,67 @@ int check_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const fl
     if (add != nullptr && !aligned(add, 4)) return set_error(Q4RDNA_ERR_ARGUMENT, "misaligned add");
     const uint32_t s = options ? options->split_k : 0;
     if (s > kMaxSplit) return set_error(Q4RDNA_ERR_ARGUMENT, "split_k %u exceeds %u", s, kMaxSplit);
-    *split = resolve_split(w, s);
+    uint32_t kernel = options ? options->kernel : Q4RDNA_KERNEL_POLICY;
+    const uint32_t steps = options ? options->burst_steps : 0;
+    if (kernel > Q4RDNA_KERNEL_BURST) return set_error(Q4RDNA_ERR_ARGUMENT, "unknown kernel %u", kernel);
+    if (steps > 2) return set_error(Q4RDNA_ERR_ARGUMENT, "burst_steps %u is outside 0..2", steps);
+    // An explicit split names the VALU kernel's factor.
+    if (kernel == Q4RDNA_KERNEL_POLICY) kernel = s != 0 ? Q4RDNA_KERNEL_VALU : tensor_kernel_policy(w, gate != nullptr);
+    TensorLaunch L{};
+    L.kernel = kernel;
+    const uint32_t groups = w->columns / kGroup;
+    if (kernel == Q4RDNA_KERNEL_VALU) {
+        L.split = resolve_split(w, s);
+        if (L.split > 1) {
+            L.partial_floats = static_cast<size_t>(L.split) * w->rows * (gate ? 2 : 1);
+            L.counters = w->rows / kTileRows;
+        }
+    } else {
+        L.steps = gate != nullptr ? 1u : (steps != 0 ? steps : burst_steps_policy(blocks_of(w->rows), groups, cu_count(w->device)));
+        L.chunks = burst_chunks(groups, L.steps);
+        if (L.chunks > 1) {
+            L.partial_floats = static_cast<size_t>(L.chunks) * w->rows * (gate ? 2 : 1);
+            L.counters = blocks_of(w->rows);
+        }
+    }
+    *launch = L;
     return Q4RDNA_OK;
 }
 
-void gemv_workspace_need(const q4rdna_weight *w, bool gate, uint32_t split, size_t *partial_floats,
-                         size_t *counters) {
-    *partial_floats = split > 1 ? static_cast<size_t>(split) * w->rows * (gate ? 2 : 1) : 0;
-    *counters = split > 1 ? w->rows / kTileRows : 0;
-}
-
-int launch_gemv_in(const q4rdna_weight *w, const uint8_t *gate, const float *x, const float *add, float *y,
-                   uint32_t split, float *partial, uint32_t *counters, hipStream_t stream) {
-    GemvArgs args{};
-    args.w = w->tiles;
-    args.gate = gate;
-    args.x = x;
-    args.add = add;
-    args.y = y;
-    args.rows = w->rows;
-    args.cols = w->columns;
-    args.split = split;
-    // Eight waves per workgroup while the launch is latency-bound (at most
-    // four workgroups per CU); with more, four waves of up to 16 tiles keep
-    // more bytes in flight per CU (151936x4096: 60 us against 68).
-    const uint64_t workgroups = static_cast<uint64_t>(w->rows / kTileRows) * split;
-    args.short_waves = workgroups <= 4ull * cu_count(w->device) ? 8u : 4u;
-    if (split > 1) {
-        args.partial = partial;
-        args.counters = counters;
+int launch_tensor_in(const TensorLaunch &launch, const q4rdna_weight *w, const uint8_t *gate, const float *x,
+                     const float *add, float *y, float *partial, uint32_t *counters, hipStream_t stream) {
+    hipError_t e;
+    if (launch.kernel == Q4RDNA_KERNEL_BURST) {
+        BurstArgs args{};
+        args.g[0] = BurstGemv{w->tiles, gate, add, y, partial, counters, w->rows, 0};
+        args.x = x;
+        args.count = 1;
+        args.cols = w->columns;
+        args.chunks = launch.chunks;
+        args.units = blocks_of(w->rows) * launch.chunks;
+        e = launch_burst(args, launch.steps, stream);
+    } else {
+        GemvArgs args{};
+        args.w = w->tiles;
+        args.gate = gate;
+        args.x = x;
+        args.add = add;
+        args.y = y;
+        args.rows = w->rows;
+        args.cols = w->columns;
+        args.split = launch.split;
+        // Eight waves per workgroup while the launch is latency-bound (at
+        // most four workgroups per CU); with more, four waves of up to 16
+        // tiles keep more bytes in flight per CU (151936x4096: 60 us
+        // against 68).
+        const uint64_t workgroups = static_cast<uint64_t>(w->rows / kTileRows) * launch.split;
+        args.short_waves = workgroups <= 4ull * cu_count(w->device) ? 8u : 4u;
+        if (launch.split > 1) {
+            args.partial = partial;
+            args.counters = counters;
+        }
+        e = launch_gemv(args, stream);
     }
-    hipError_t e = launch_gemv(args, stream);
     if (e != hipSuccess) return hip_fail(e, "GEMV launch");
     return Q4RDNA_OK;
 }
@@ -489,8 +544,9 @@ int q4rdna_mul_mat(const q4rdna_weight *w, const float *x, int64_t x_ne0, float 
     if (x_ne0 != static_cast<int64_t>(w->columns) || y_ne0 != static_cast<int64_t>(w->rows))
         return set_error(Q4RDNA_NOT_APPLICABLE, "shape mismatch: x %lld (K %u), y %lld (M %u)",
                     static_cast<long long>(x_ne0), w->columns, static_cast<long long>(y_ne0), w->rows);
-    if ((rc = check_io(x, y)) != Q4RDNA_OK) return rc;
-    return launch_one(w, nullptr, x, nullptr, y, 0, static_cast<hipStream_t>(stream));
+    q4rdna::TensorLaunch L{};
+    if ((rc = q4rdna::check_mul_mat_ex(w, nullptr, x, nullptr, y, nullptr, &L)) != Q4RDNA_OK) return rc;
+    return launch_one(L, w, nullptr, x, nullptr, y, static_cast<hipStream_t>(stream));
 }
 
 int q4rdna_mul_mat_add(const q4rdna_weight *w, const float *x, int64_t x_ne0, const float *add, int64_t add_ne,
@@ -500,9 +556,10 @@ int q4rdna_mul_mat_add(const q4rdna_weight *w, const float *x, int64_t x_ne0, co
     if (x_ne0 != static_cast<int64_t>(w->columns) || y_ne0 != static_cast<int64_t>(w->rows) ||
         add_ne != static_cast<int64_t>(w->rows))
         return set_error(Q4RDNA_NOT_APPLICABLE, "shape mismatch");
-    if ((rc = check_io(x, y)) != Q4RDNA_OK) return rc;
-    if (add == nullptr || !aligned(add, 4)) return set_error(Q4RDNA_ERR_ARGUMENT, "NULL or misaligned add");
-    return launch_one(w, nullptr, x, add, y, 0, static_cast<hipStream_t>(stream));
+    if (add == nullptr) return set_error(Q4RDNA_ERR_ARGUMENT, "NULL add");
+    q4rdna::TensorLaunch L{};
+    if ((rc = q4rdna::check_mul_mat_ex(w, nullptr, x, add, y, nullptr, &L)) != Q4RDNA_OK) return rc;
+    return launch_one(L, w, nullptr, x, add, y, static_cast<hipStream_t>(stream));
 }
 
 int q4rdna_mul_mat_glu(const q4rdna_weight *up, const q4rdna_weight *gate, const float *x, int64_t x_ne0, int glu_op,
@@ -515,16 +572,88 @@ int q4rdna_mul_mat_glu(const q4rdna_weight *up, const q4rdna_weight *gate, const
         return set_error(Q4RDNA_NOT_APPLICABLE, "up and gate shapes differ");
     if (x_ne0 != static_cast<int64_t>(up->columns) || y_ne0 != static_cast<int64_t>(up->rows))
         return set_error(Q4RDNA_NOT_APPLICABLE, "shape mismatch");
-    if ((rc = check_io(x, y)) != Q4RDNA_OK) return rc;
-    return launch_one(up, gate->tiles, x, nullptr, y, 0, static_cast<hipStream_t>(stream));
+    q4rdna::TensorLaunch L{};
+    if ((rc = q4rdna::check_mul_mat_ex(up, gate, x, nullptr, y, nullptr, &L)) != Q4RDNA_OK) return rc;
+    return launch_one(L, up, gate->tiles, x, nullptr, y, static_cast<hipStream_t>(stream));
 }
 
 int q4rdna_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x, const float *add, float *y,
                       const q4rdna_launch_options *options, void *stream) {
-    uint32_t split = 0;
-    int rc = q4rdna::check_mul_mat_ex(w, gate, x, add, y, options, &split);
+    q4rdna::TensorLaunch L{};
+    int rc = q4rdna::check_mul_mat_ex(w, gate, x, add, y, options, &L);
     if (rc != Q4RDNA_OK) return rc;
-    return launch_one(w, gate ? gate->tiles : nullptr, x, add, y, split, static_cast<hipStream_t>(stream));
+    return launch_one(L, w, gate ? gate->tiles : nullptr, x, add, y, static_cast<hipStream_t>(stream));
+}
+
+int q4rdna_mul_mat_group(const q4rdna_group_desc *descs, uint32_t count, const float *x, int64_t x_ne0,
+                         const q4rdna_launch_options *options, void *stream) {
+    if (descs == nullptr || count == 0 || count > Q4RDNA_MAX_GROUP)
+        return set_error(Q4RDNA_ERR_ARGUMENT, "group of %u GEMVs is outside 1..%d", count, Q4RDNA_MAX_GROUP);
+    if (x == nullptr || !aligned(x, 4)) return set_error(Q4RDNA_ERR_ARGUMENT, "NULL or misaligned activation");
+    const bool glu = descs[0].gate_tiles != nullptr;
+    int rc;
+    uint64_t blocks = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        const q4rdna_group_desc &d = descs[i];
+        if ((rc = check_weight(&d.weight)) != Q4RDNA_OK) return rc;
+        if (x_ne0 != static_cast<int64_t>(d.weight.columns))
+            return set_error(Q4RDNA_NOT_APPLICABLE, "descriptor %u: x holds %lld floats, K is %u", i,
+                             static_cast<long long>(x_ne0), d.weight.columns);
+        if ((d.gate_tiles != nullptr) != glu)
+            return set_error(Q4RDNA_ERR_ARGUMENT, "gate tiles must be given for every descriptor or for none");
+        if (glu && !aligned(d.gate_tiles, 16)) return set_error(Q4RDNA_ERR_ARGUMENT, "descriptor %u: misaligned gate", i);
+        if (d.y == nullptr || !aligned(d.y, 4) || (d.add != nullptr && !aligned(d.add, 4)))
+            return set_error(Q4RDNA_ERR_ARGUMENT, "descriptor %u: NULL or misaligned output or add", i);
+        const uintptr_t y0 = reinterpret_cast<uintptr_t>(d.y), y1 = y0 + 4ull * d.weight.rows;
+        const uintptr_t x0 = reinterpret_cast<uintptr_t>(x), x1 = x0 + 4ull * d.weight.columns;
+        if (y0 < x1 && x0 < y1) return set_error(Q4RDNA_ERR_ARGUMENT, "descriptor %u: y overlaps x", i);
+        blocks += blocks_of(d.weight.rows);
+    }
+    const uint32_t groups = descs[0].weight.columns / kGroup;
+    uint32_t steps = options ? options->burst_steps : 0;
+    if (steps > 2) return set_error(Q4RDNA_ERR_ARGUMENT, "burst_steps %u is outside 0..2", steps);
+    if (glu) steps = 1;
+    if (steps == 0) steps = burst_steps_policy(blocks, groups, cu_count(descs[0].weight.device));
+    const uint32_t chunks = burst_chunks(groups, steps);
+    if (blocks * chunks > 0x7fffffffull) return set_error(Q4RDNA_ERR_ARGUMENT, "group too large");
+    const uint32_t streams = glu ? 2u : 1u;
+    size_t partial_floats = 0, counters = 0;
+    if (chunks > 1)
+        for (uint32_t i = 0; i < count; ++i) {
+            partial_floats += static_cast<size_t>(chunks) * streams * descs[i].weight.rows;
+            counters += blocks_of(descs[i].weight.rows);
+        }
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    float *partial = nullptr;
+    uint32_t *counter_base = nullptr;
+    if (chunks > 1) {
+        Workspace *ws = nullptr;
+        if ((rc = get_workspace(descs[0].weight.device, s, partial_floats, counters, &ws)) != Q4RDNA_OK) return rc;
+        partial = ws->partial;
+        counter_base = ws->counters;
+    }
+    q4rdna::BurstArgs args{};
+    args.x = x;
+    args.count = count;
+    args.cols = descs[0].weight.columns;
+    args.chunks = chunks;
+    uint32_t units = 0;
+    size_t poff = 0, coff = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        const q4rdna_group_desc &d = descs[i];
+        args.g[i] = q4rdna::BurstGemv{d.weight.tiles, d.gate_tiles, d.add, d.y,
+                                      chunks > 1 ? partial + poff : nullptr, chunks > 1 ? counter_base + coff : nullptr,
+                                      d.weight.rows, units};
+        units += blocks_of(d.weight.rows) * chunks;
+        if (chunks > 1) {
+            poff += static_cast<size_t>(chunks) * streams * d.weight.rows;
+            coff += blocks_of(d.weight.rows);
+        }
+    }
+    args.units = units;
+    hipError_t e = q4rdna::launch_burst(args, steps, s);
+    if (e != hipSuccess) return hip_fail(e, "group GEMV launch");
+    return Q4RDNA_OK;
 }
 
 int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x, uint32_t n,
@@ -549,8 +678,12 @@ int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, cons
     const uint32_t need = (groups + stage - 1) / stage;
     if (n == 1 || need > std::min(groups, kMaxSplit)) {
         const size_t M = w->rows, K = w->columns;
+        q4rdna_launch_options one{};
+        one.split_k = split;
+        q4rdna::TensorLaunch L{};
+        if ((rc = q4rdna::check_mul_mat_ex(w, gate, x, add, y, &one, &L)) != Q4RDNA_OK) return rc;
         for (uint32_t v = 0; v < n; ++v)
-            if ((rc = launch_one(w, gt, x + v * K, add ? add + v * M : nullptr, y + v * M, split, s)) != Q4RDNA_OK)
+            if ((rc = launch_one(L, w, gt, x + v * K, add ? add + v * M : nullptr, y + v * M, s)) != Q4RDNA_OK)
                 return rc;
         return Q4RDNA_OK;
     }

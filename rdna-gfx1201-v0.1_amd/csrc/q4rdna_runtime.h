@@ -13,20 +13,29 @@ namespace q4rdna {
 // Record `fmt` as the calling thread's last error; returns `code`.
 int set_error(int code, const char *fmt, ...);
 
-// Validate q4rdna_mul_mat_ex's arguments (the same statuses as that entry
-// point) and resolve the split-K factor it launches with.
-int check_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x, const float *add,
-                     const float *y, const q4rdna_launch_options *options, uint32_t *split);
+// How a per-tensor GEMV launches: the kernel (Q4RDNA_KERNEL_VALU or
+// Q4RDNA_KERNEL_BURST), the VALU kernel's split-K factor or the burst
+// kernel's steps per unit and chunks per block, and the workspace it needs
+// (fp32 partials and arrival counters; none when the K dimension is not
+// split).
+struct TensorLaunch {
+    uint32_t kernel;
+    uint32_t split;
+    uint32_t steps;
+    uint32_t chunks;
+    size_t partial_floats;
+    size_t counters;
+};
 
-// Workspace a per-tensor launch with that split needs: fp32 partials and
-// arrival counters (none when split == 1).
-void gemv_workspace_need(const q4rdna_weight *w, bool gate, uint32_t split, size_t *partial_floats,
-                         size_t *counters);
+// Validate q4rdna_mul_mat_ex's arguments (the same statuses as that entry
+// point) and resolve how it launches.
+int check_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x, const float *add,
+                     const float *y, const q4rdna_launch_options *options, TensorLaunch *launch);
 
 // Launch a validated per-tensor GEMV with a caller-provided workspace of at
-// least gemv_workspace_need() (ignored when split == 1); counters zero on
-// entry, left zero.
-int launch_gemv_in(const q4rdna_weight *w, const uint8_t *gate, const float *x, const float *add, float *y,
-                   uint32_t split, float *partial, uint32_t *counters, hipStream_t stream);
+// least launch.partial_floats floats and launch.counters counters (ignored
+// when both are zero); counters zero on entry, left zero.
+int launch_tensor_in(const TensorLaunch &launch, const q4rdna_weight *w, const uint8_t *gate, const float *x,
+                     const float *add, float *y, float *partial, uint32_t *counters, hipStream_t stream);
 
 }  // namespace q4rdna

@@ -40,7 +40,7 @@ EXPORTS = (
     "q4rdna_sidecar_open_memory", "q4rdna_sidecar_close", "q4rdna_sidecar_count", "q4rdna_sidecar_entry",
     "q4rdna_find", "q4rdna_weight_from_device", "q4rdna_default_sidecar", "q4rdna_scope_allows",
     "q4rdna_mul_mat", "q4rdna_mul_mat_add", "q4rdna_mul_mat_glu", "q4rdna_mul_mat_ex", "q4rdna_mul_mat_batch",
-    "q4rdna_policy_split_k", "q4rdna_mul_mat_ex_noalloc", "q4rdna_plan_create", "q4rdna_plan_create_batch", "q4rdna_plan_launch",
+    "q4rdna_policy_split_k", "q4rdna_mul_mat_ex_noalloc", "q4rdna_mul_mat_group", "q4rdna_plan_create", "q4rdna_plan_create_batch", "q4rdna_plan_launch",
     "q4rdna_plan_prepare",
     "q4rdna_plan_sweep", "q4rdna_plan_destroy",
     "q4rdna_plan_workgroups", "q4rdna_pack", "q4rdna_dequantize",
@@ -60,8 +60,19 @@ class Weight(ctypes.Structure):
                 ("device", ctypes.c_int32), ("reserved", ctypes.c_uint32)]
 
 
+KERNEL_POLICY = 0
+KERNEL_VALU = 1
+KERNEL_BURST = 2
+MAX_GROUP = 8
+
+
 class LaunchOptions(ctypes.Structure):
-    _fields_ = [("split_k", ctypes.c_uint32), ("reserved", ctypes.c_uint32 * 7)]
+    _fields_ = [("split_k", ctypes.c_uint32), ("kernel", ctypes.c_uint32), ("burst_steps", ctypes.c_uint32),
+                ("reserved", ctypes.c_uint32 * 5)]
+
+
+class GroupDesc(ctypes.Structure):
+    _fields_ = [("weight", Weight), ("gate_tiles", ctypes.c_void_p), ("add", ctypes.c_void_p), ("y", ctypes.c_void_p)]
 
 
 class GemvDesc(ctypes.Structure):
@@ -104,6 +115,7 @@ def load() -> ctypes.CDLL:
         "q4rdna_mul_mat_batch": (i32, [WP, WP, vp, u32, vp, vp, ctypes.POINTER(LaunchOptions), vp]),
         "q4rdna_policy_split_k": (u32, [u32, u32, i32]),
         "q4rdna_mul_mat_ex_noalloc": (i32, [WP, WP, vp, vp, vp, ctypes.POINTER(LaunchOptions), vp]),
+        "q4rdna_mul_mat_group": (i32, [ctypes.POINTER(GroupDesc), u32, vp, i64, ctypes.POINTER(LaunchOptions), vp]),
         "q4rdna_plan_create": (i32, [ctypes.POINTER(GemvDesc), u32, i32, ctypes.POINTER(vp)]),
         "q4rdna_plan_create_batch": (i32, [ctypes.POINTER(GemvDesc), u32, u32, i32, ctypes.POINTER(vp)]),
         "q4rdna_plan_launch": (i32, [vp, vp]),

@@ -128,8 +128,11 @@ def mul_mat_glu(up: QWeight, gate: QWeight, x: torch.Tensor, y: torch.Tensor | N
 
 
 def mul_mat_ex(w: QWeight, x: torch.Tensor, y: torch.Tensor, gate: QWeight | None = None,
-               add: torch.Tensor | None = None, split_k: int = 0, stream: int | None = None) -> bool:
-    """GEMV with an explicit split-K factor (0 = the shape policy)."""
+               add: torch.Tensor | None = None, split_k: int = 0, stream: int | None = None,
+               kernel: int = _lib.KERNEL_POLICY, burst_steps: int = 0) -> bool:
+    """GEMV with explicit launch options: split_k for the VALU kernel (0 =
+    the shape policy), kernel (KERNEL_VALU / KERNEL_BURST, 0 = the policy),
+    burst_steps (1 or 2, 0 = the policy)."""
     _f32_buf(x, "x", w.cols, w.device)
     _f32_buf(y, "y", w.rows, w.device)
     if add is not None:
@@ -138,6 +141,8 @@ def mul_mat_ex(w: QWeight, x: torch.Tensor, y: torch.Tensor, gate: QWeight | Non
         raise ValueError("gate and weight shapes differ")
     opts = LaunchOptions()
     opts.split_k = split_k
+    opts.kernel = kernel
+    opts.burst_steps = burst_steps
     s = _stream(x.device) if stream is None else stream
     return check(load().q4rdna_mul_mat_ex(ctypes.byref(w.raw), ctypes.byref(gate.raw) if gate else None,
                                           x.data_ptr(), _ptr(add), y.data_ptr(), ctypes.byref(opts), s))
@@ -164,6 +169,33 @@ def mul_mat_batch(w: QWeight, x: torch.Tensor, y: torch.Tensor, gate: QWeight | 
     return check(load().q4rdna_mul_mat_batch(ctypes.byref(w.raw), ctypes.byref(gate.raw) if gate else None,
                                              x.data_ptr(), x.shape[0], _ptr(add), y.data_ptr(),
                                              ctypes.byref(opts), s))
+
+
+def mul_mat_group(items: Sequence[tuple], x: torch.Tensor, burst_steps: int = 0, stream: int | None = None) -> bool:
+    """GEMVs sharing one activation x in one launch.  items: (weight, y) or
+    (weight, y, gate_weight_or_None, add_or_None); every weight has
+    x.numel() columns.  Returns False when not applicable."""
+    if not 1 <= len(items) <= _lib.MAX_GROUP:
+        raise ValueError(f"a group holds 1..{_lib.MAX_GROUP} GEMVs")
+    descs = (_lib.GroupDesc * len(items))()
+    for i, it in enumerate(items):
+        w, y = it[0], it[1]
+        gate = it[2] if len(it) > 2 else None
+        add = it[3] if len(it) > 3 else None
+        _f32_buf(x, "x", w.cols, w.device)
+        _f32_buf(y, f"item {i} y", w.rows, w.device)
+        if add is not None:
+            _f32_buf(add, f"item {i} add", w.rows, w.device)
+        if gate is not None and (gate.rows, gate.cols, gate.device) != (w.rows, w.cols, w.device):
+            raise ValueError(f"item {i}: gate and weight differ in shape or device")
+        descs[i].weight = w.raw
+        descs[i].gate_tiles = gate.raw.tiles if gate is not None else None
+        descs[i].add = _ptr(add)
+        descs[i].y = y.data_ptr()
+    opts = LaunchOptions()
+    opts.burst_steps = burst_steps
+    s = _stream(x.device) if stream is None else stream
+    return check(load().q4rdna_mul_mat_group(descs, len(items), x.data_ptr(), x.numel(), ctypes.byref(opts), s))
 
 
 def policy_split_k(rows: int, cols: int, device: int = 0) -> int:
