@@ -211,12 +211,16 @@ int check_io(const float *x, const float *y) {
 
 namespace {
 
-// Burst units of 16 * steps groups: one step while that leaves at most
-// three units per CU, else two (fewer, longer units and shorter arrival
-// chains where there is plenty of parallelism).
+// Burst units of 16 * steps groups.  Two steps (half the units, half the
+// split-K arrivals) when one-step units would oversubscribe the CUs
+// moderately; one step when they fit one per CU, or when there are so many
+// that every CU runs several waves of them anyway.  Measured on MI355X
+// (graph replays): q/k/v of a layer in one group 7.9 against 8.4 us,
+// 4096x12288 12.0 against 13.0; 4096x4096 alone 6.9 against 7.4,
+// 1024x4096 6.3 against 7.1, 151936x4096 69 against 74.
 uint32_t burst_steps_policy(uint64_t blocks, uint32_t groups, uint32_t cus) {
     const uint64_t units1 = blocks * ((groups + q4rdna::kBurstStepGroups - 1) / q4rdna::kBurstStepGroups);
-    return units1 > 3ull * cus && groups > q4rdna::kBurstStepGroups ? 2u : 1u;
+    return units1 > cus && units1 <= 8ull * cus && groups > q4rdna::kBurstStepGroups ? 2u : 1u;
 }
 
 uint32_t burst_chunks(uint32_t groups, uint32_t steps) {
