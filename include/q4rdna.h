@@ -206,18 +206,21 @@ uint32_t q4rdna_policy_split_k(uint32_t rows, uint32_t columns, int device);
 /* q4rdna_mul_mat_ex that allocates nothing.  No counterpart in the
  * reference: it is for callers that cannot allocate (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  The split-K
- * partial sums and arrival counters live in a fixed per-GPU device array of
- * Q4RDNA_NOALLOC_PARTIAL_FLOATS floats and Q4RDNA_NOALLOC_COUNTERS counters
- * (4.06 MiB, held by every GPU the library runs on until the process ends);
- * a launch that would need more (split_k * rows, doubled with a gate, above
- * the floats, or rows / 32 above the counters) returns Q4RDNA_ERR_ARGUMENT
- * and launches nothing.  Arguments, statuses and results are those of
+ * workspace lives in a fixed per-GPU device array of
+ * Q4RDNA_NOALLOC_PARTIAL_FLOATS partial sums, Q4RDNA_NOALLOC_COUNTERS arrival
+ * counters and Q4RDNA_NOALLOC_SLOTS two-chunk exchange slots (8.06 MiB, held
+ * by every GPU the library runs on until the process ends).  A launch that
+ * would need more returns Q4RDNA_ERR_ARGUMENT and launches nothing: at
+ * split_k 2, rows (doubled with a gate) above the slots; at larger splits,
+ * split_k * rows (doubled with a gate) above the partial sums or rows / 32
+ * above the counters.  Arguments, statuses and results are those of
  * q4rdna_mul_mat_ex (bit-identical at the same split).  Every call on a GPU
  * shares that GPU's array: calls that overlap on one GPU race, so issue them
  * on one stream or order them with events.  The first call on a GPU looks
- * the array up and clears its counters with a kernel on `stream`. */
+ * the array up and sets its counters and slots with a kernel on `stream`. */
 #define Q4RDNA_NOALLOC_PARTIAL_FLOATS (1u << 20)
 #define Q4RDNA_NOALLOC_COUNTERS 16384u
+#define Q4RDNA_NOALLOC_SLOTS (1u << 20)
 int q4rdna_mul_mat_ex_noalloc(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x,
                               const float *add, float *y, const q4rdna_launch_options *options,
                               void *stream);

@@ -11,10 +11,18 @@ constexpr uint32_t kGroup = 64;
 constexpr uint32_t kTileRows = 32;
 constexpr uint32_t kTileBytes = 1088;
 
+// Exchange slots of two-chunk split-K launches: every word holds kSlotEmpty
+// (a signaling-NaN pattern) between launches; a partial with those bits is
+// sent as kSlotQuietNan.
+constexpr uint32_t kSlotEmpty = 0x7fa5a5a5u;
+constexpr uint32_t kSlotQuietNan = 0x7fc00000u;
+
 // One GEMV launch.  gate != nullptr selects SwiGLU, add != nullptr the bias
-// epilogue.  split > 1 reduces K chunks across workgroups through
-// partial[split * rows (x2 with gate)] and counters[rows / 32], which must be
-// zero on entry and are left zero.
+// epilogue.  split == 2 (gemv_kernel) reduces the two K chunks through
+// slots[rows (x2 with gate)], kSlotEmpty on entry and left so.  Other splits
+// > 1 reduce K chunks across workgroups through partial[split * rows (x2
+// with gate)] and counters[rows / 32], which must be zero on entry and are
+// left zero.
 struct GemvArgs {
     const uint8_t *w;
     const uint8_t *gate;
@@ -26,6 +34,7 @@ struct GemvArgs {
     uint32_t split;
     float *partial;
     uint32_t *counters;
+    uint32_t *slots;
     uint32_t short_waves;  // 8 or 4: waves per workgroup for K chunks of at most 64 groups
     uint32_t vectors;      // launch_gemv_multi: activation vectors (x [vectors][cols], y/add [vectors][rows])
 };
@@ -105,9 +114,11 @@ hipError_t launch_plan_batch(const PlanDesc *descs, uint32_t items, uint32_t n, 
 // 16 * steps groups), one workgroup each, units numbered GEMV by GEMV from
 // unit_begin, block-major then chunk; `chunks` chunks per block.  With
 // gate != nullptr (every GEMV of a launch, or none) a unit streams the gate
-// tiles of its block too and the epilogue is SwiGLU.  When chunks > 1 the
-// units of a block meet in partial[stream][chunk][rows] through
-// counters[block] (zero between launches, left zero).
+// tiles of its block too and the epilogue is SwiGLU.  With chunks == 2 the
+// two units of a row meet in slots[rows (x2 with gate)] (kSlotEmpty between
+// launches, left so); with more, the units of a block meet in
+// partial[stream][chunk][rows] through counters[block] (zero between
+// launches, left zero).
 constexpr uint32_t kMaxBurst = 8;
 constexpr uint32_t kBurstStepGroups = 16;  // groups of one 64-row workgroup step (four waves of four groups)
 struct BurstGemv {
@@ -117,6 +128,7 @@ struct BurstGemv {
     float *y;
     float *partial;
     uint32_t *counters;
+    uint32_t *slots;
     uint32_t rows;
     uint32_t unit_begin;
 };

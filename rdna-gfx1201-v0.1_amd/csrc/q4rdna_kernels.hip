@@ -325,14 +325,20 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs args) {
     const uint32_t rt = logical / split, s = logical % split;
     const uint32_t g_begin = static_cast<uint32_t>((static_cast<uint64_t>(s) * groups) / split);
     const uint32_t g_end = static_cast<uint32_t>((static_cast<uint64_t>(s + 1) * groups) / split);
+    const uint32_t row = rt * kTileRows + (threadIdx.x & 31);
     float v = 0.f, gv = 0.f;
     if constexpr (T == 0)
         tile_row_partial<GATE>(sh, args.w, args.gate, args.x, args.cols, rt, g_begin, g_end, v, gv);
     else
         tile_row_partial_short<GATE, T, W>(sh, args.w, args.gate, args.x, args.cols, rt, g_begin, g_end, v, gv);
-    const uint32_t row = rt * kTileRows + (threadIdx.x & 31);
     if (split == 1) {
         if (threadIdx.x < 32) args.y[row] = epilogue<GATE, ADD>(v, gv, args.add, row);
+        return;
+    }
+    if (split == 2) {
+        // The row's second chunk to arrive finishes it.
+        if (threadIdx.x < 32 && exchange_pair<GATE>(args.slots, row, v, gv))
+            args.y[row] = epilogue<GATE, ADD>(v, gv, args.add, row);
         return;
     }
     // Split K: publish this chunk's partials with device-scope stores, wait

@@ -919,10 +919,11 @@ struct BurstShared {
 
 // A unit's end: the useful lanes publish their rows; thread t < 64 sums row
 // t's 16 (wave, group) partials in the fixed order.  One chunk: y = (sum +
-// add), times silu(gate sum) for SwiGLU.  Several: the sums (and gate sums)
-// are published with device-scope stores, drained before the block's
-// arrival count, and the last unit of the block to arrive sums the chunks in
-// chunk order and applies the epilogue.
+// add), times silu(gate sum) for SwiGLU.  Two: the row's sums meet in its
+// exchange slot and the second to arrive applies the epilogue.  More: the
+// sums (and gate sums) are published with device-scope stores, drained
+// before the block's arrival count, and the last unit of the block to
+// arrive sums the chunks in chunk order and applies the epilogue.
 template <bool GLU>
 __device__ __forceinline__ void burst_finish(Red &red, uint32_t &last, const BurstGemv &G, uint32_t block,
                                              uint32_t chunk, uint32_t chunks, const float (&acc)[16],
@@ -953,8 +954,8 @@ __device__ __forceinline__ void burst_finish(Red &red, uint32_t &last, const Bur
                 for (int g = 0; g < kStepGroups; ++g) gv += red[1][w][g][threadIdx.x];
         }
     }
-    if (chunks == 1) {
-        if (mine) {
+    if (chunks <= 2) {
+        if (mine && (chunks == 1 || exchange_pair<GLU>(G.slots, row, v, gv))) {
             if (G.add != nullptr) v += ((gptr_cf32)G.add)[row];
             if constexpr (GLU) v *= silu(gv);
             *((gptr_f32)G.y + row) = v;

@@ -4,19 +4,20 @@
 // harnesses that forbid hipMalloc).
 //
 // The array, `scratch`, holds Q4RDNA_NOALLOC_PARTIAL_FLOATS fp32 partial
-// sums followed by Q4RDNA_NOALLOC_COUNTERS arrival counters; every GPU the
+// sums, then Q4RDNA_NOALLOC_COUNTERS arrival counters, then
+// Q4RDNA_NOALLOC_SLOTS exchange slots of two-chunk launches; every GPU the
 // library runs on holds its own copy until the process ends.  In host code
 // the name `scratch` is only a stand-in for the symbol: the device address of
 // a GPU's copy comes from hipGetSymbolAddress with that GPU current, once per
 // GPU, and only that address is ever passed to a kernel.
 //
-// Counters must be zero when a launch starts.  They are zero when the code
-// object is loaded, the first call on a GPU clears them once more with a fill
-// kernel on its stream, and every launch leaves them zero (the last
-// workgroup to arrive at a row tile or 64-row block resets its counter).  Partial sums need no
-// clearing: every launch writes the ones it reads.  Every call on a GPU
-// shares that GPU's array, so calls that overlap on one GPU race: issue them
-// on one stream, or order them with events.
+// Counters must be zero and slots kSlotEmpty when a launch starts.  The first
+// call on a GPU sets both with a fill kernel on its stream, and every launch
+// leaves them so (the last workgroup to arrive at a row tile or 64-row block
+// resets its counter; the second chunk to reach a slot empties it).  Partial
+// sums need no clearing: every launch writes the ones it reads.  Every call
+// on a GPU shares that GPU's array, so calls that overlap on one GPU race:
+// issue them on one stream, or order them with events.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -29,13 +30,20 @@
 namespace {
 
 constexpr size_t kPartialBytes = static_cast<size_t>(Q4RDNA_NOALLOC_PARTIAL_FLOATS) * sizeof(float);
-constexpr size_t kScratchBytes = kPartialBytes + static_cast<size_t>(Q4RDNA_NOALLOC_COUNTERS) * sizeof(uint32_t);
-static_assert(kPartialBytes % 256 == 0, "the counters start 256-byte aligned");
+constexpr size_t kCounterBytes = static_cast<size_t>(Q4RDNA_NOALLOC_COUNTERS) * sizeof(uint32_t);
+constexpr size_t kSlotBytes = static_cast<size_t>(Q4RDNA_NOALLOC_SLOTS) * sizeof(uint32_t);
+constexpr size_t kScratchBytes = kPartialBytes + kCounterBytes + kSlotBytes;
+static_assert(kPartialBytes % 256 == 0 && kCounterBytes % 256 == 0, "the counters and slots start 256-byte aligned");
 
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
-__global__ __launch_bounds__(256) void clear_counters(uint32_t *__restrict__ counters, uint32_t count) {
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x) counters[i] = 0u;
+// Counters to zero, slots to kSlotEmpty (a fill kernel, not a memset, so a
+// caller may capture the first call into a graph).
+__global__ __launch_bounds__(256) void init_scratch(uint32_t *__restrict__ counters, uint32_t *__restrict__ slots) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < Q4RDNA_NOALLOC_COUNTERS; i += gridDim.x * blockDim.x)
+        counters[i] = 0u;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < Q4RDNA_NOALLOC_SLOTS; i += gridDim.x * blockDim.x)
+        slots[i] = q4rdna::kSlotEmpty;
 }
 
 // Device address of each GPU's copy of `scratch`, looked up on the first
@@ -57,10 +65,11 @@ int scratch_of(int device, hipStream_t stream, uint8_t **out) {
             hipError_t e = hipGetSymbolAddress(reinterpret_cast<void **>(&p), HIP_SYMBOL(scratch));
             if (e != hipSuccess || p == nullptr)
                 return q4rdna::set_error(Q4RDNA_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
-            hipLaunchKernelGGL(clear_counters, dim3(Q4RDNA_NOALLOC_COUNTERS / 256), dim3(256), 0, stream,
-                               reinterpret_cast<uint32_t *>(p + kPartialBytes), Q4RDNA_NOALLOC_COUNTERS);
+            hipLaunchKernelGGL(init_scratch, dim3(256), dim3(256), 0, stream,
+                               reinterpret_cast<uint32_t *>(p + kPartialBytes),
+                               reinterpret_cast<uint32_t *>(p + kPartialBytes + kCounterBytes));
             e = hipGetLastError();
-            if (e != hipSuccess) return q4rdna::set_error(Q4RDNA_ERR_HIP, "counter clear: %s", hipGetErrorString(e));
+            if (e != hipSuccess) return q4rdna::set_error(Q4RDNA_ERR_HIP, "scratch set-up: %s", hipGetErrorString(e));
             g_scratch[device].store(p, std::memory_order_release);
         }
     }
@@ -78,16 +87,20 @@ extern "C" int q4rdna_mul_mat_ex_noalloc(const q4rdna_weight *w, const q4rdna_we
     if (rc != Q4RDNA_OK) return rc;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const uint8_t *gt = gate ? gate->tiles : nullptr;
-    if (L.partial_floats == 0 && L.counters == 0) return q4rdna::launch_tensor_in(L, w, gt, x, add, y, nullptr, nullptr, s);
-    if (L.partial_floats > Q4RDNA_NOALLOC_PARTIAL_FLOATS || L.counters > Q4RDNA_NOALLOC_COUNTERS)
+    if (L.partial_floats == 0 && L.counters == 0 && L.slots == 0)
+        return q4rdna::launch_tensor_in(L, w, gt, x, add, y, nullptr, nullptr, nullptr, s);
+    if (L.partial_floats > Q4RDNA_NOALLOC_PARTIAL_FLOATS || L.counters > Q4RDNA_NOALLOC_COUNTERS ||
+        L.slots > Q4RDNA_NOALLOC_SLOTS)
         return q4rdna::set_error(Q4RDNA_ERR_ARGUMENT,
-                                 "%ux%u needs %zu partial floats and %zu counters; the no-alloc scratch holds %u "
-                                 "and %u",
-                                 w->rows, w->columns, L.partial_floats, L.counters,
+                                 "%ux%u needs %zu partial floats, %zu counters and %zu slots; the no-alloc scratch "
+                                 "holds %u, %u and %u",
+                                 w->rows, w->columns, L.partial_floats, L.counters, L.slots,
                                  static_cast<unsigned>(Q4RDNA_NOALLOC_PARTIAL_FLOATS),
-                                 static_cast<unsigned>(Q4RDNA_NOALLOC_COUNTERS));
+                                 static_cast<unsigned>(Q4RDNA_NOALLOC_COUNTERS),
+                                 static_cast<unsigned>(Q4RDNA_NOALLOC_SLOTS));
     uint8_t *base = nullptr;
     if ((rc = scratch_of(w->device, s, &base)) != Q4RDNA_OK) return rc;
     return q4rdna::launch_tensor_in(L, w, gt, x, add, y, reinterpret_cast<float *>(base),
-                                    reinterpret_cast<uint32_t *>(base + kPartialBytes), s);
+                                    reinterpret_cast<uint32_t *>(base + kPartialBytes),
+                                    reinterpret_cast<uint32_t *>(base + kPartialBytes + kCounterBytes), s);
 }

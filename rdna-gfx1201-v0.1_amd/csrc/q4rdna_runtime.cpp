@@ -109,13 +109,16 @@ int parse_index(const uint8_t *image, uint64_t image_size, uint64_t file_size, F
     return host_status(q4rdna::host::parse_index(image, image_size, file_size, header, entries, &error), error);
 }
 
-// Split-K scratch per (device, stream): partial sums and per-row-tile
-// arrival counters (kept zero between launches by the kernel itself).
+// Split-K scratch per (device, stream): partial sums, per-row-tile arrival
+// counters (kept zero between launches by the kernels) and two-chunk
+// exchange slots (kept kSlotEmpty between launches by the kernel).
 struct Workspace {
     float *partial = nullptr;
     uint32_t *counters = nullptr;
+    uint32_t *slots = nullptr;
     size_t partial_floats = 0;
     size_t counter_count = 0;
+    size_t slot_count = 0;
 };
 
 std::mutex g_ws_mu;
@@ -125,38 +128,49 @@ std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 // doubles when it grows, so few are ever retired.
 std::vector<Workspace> g_ws_retired;
 
-int get_workspace(int device, hipStream_t stream, size_t partial_floats, size_t counters, Workspace **out) {
+int get_workspace(int device, hipStream_t stream, size_t partial_floats, size_t counters, size_t slots,
+                  Workspace **out) {
     std::lock_guard<std::mutex> lock(g_ws_mu);
     Workspace &ws = g_ws[{device, stream}];
-    if (ws.partial_floats < partial_floats || ws.counter_count < counters) {
-        const size_t pf = std::max(partial_floats, 2 * ws.partial_floats);
-        const size_t cc = std::max(counters, 2 * ws.counter_count);
-        if (ws.partial != nullptr || ws.counters != nullptr) {
+    if (ws.partial_floats < partial_floats || ws.counter_count < counters || ws.slot_count < slots) {
+        // Each region at least doubles when the workspace grows (and never
+        // shrinks), so few workspaces are ever retired.
+        const size_t pf = std::max(partial_floats, ws.partial_floats < partial_floats ? 2 * ws.partial_floats : ws.partial_floats);
+        const size_t cc = std::max(counters, ws.counter_count < counters ? 2 * ws.counter_count : ws.counter_count);
+        const size_t sc = std::max(slots, ws.slot_count < slots ? 2 * ws.slot_count : ws.slot_count);
+        if (ws.partial != nullptr || ws.counters != nullptr || ws.slots != nullptr) {
             g_ws_retired.push_back(ws);
             ws = Workspace{};
         }
         float *p = nullptr;
-        uint32_t *c = nullptr;
-        hipError_t e = hipMalloc(&p, pf * sizeof(float));
-        if (e != hipSuccess) return set_error(Q4RDNA_ERR_MEMORY, "split-K workspace: %s", hipGetErrorString(e));
-        e = hipMalloc(&c, cc * sizeof(uint32_t));
+        uint32_t *c = nullptr, *sl = nullptr;
+        hipError_t e = hipSuccess;
+        if (pf > 0) e = hipMalloc(&p, pf * sizeof(float));
+        if (e == hipSuccess && cc > 0) e = hipMalloc(&c, cc * sizeof(uint32_t));
+        if (e == hipSuccess && sc > 0) e = hipMalloc(&sl, sc * sizeof(uint32_t));
         if (e != hipSuccess) {
             (void)hipFree(p);
-            return set_error(Q4RDNA_ERR_MEMORY, "split-K counters: %s", hipGetErrorString(e));
+            (void)hipFree(c);
+            (void)hipFree(sl);
+            return set_error(Q4RDNA_ERR_MEMORY, "split-K workspace: %s", hipGetErrorString(e));
         }
-        // Zeroed once, complete before any launch uses them (launches on
+        // Set once, complete before any launch uses them (launches on
         // non-blocking streams are not ordered after the null stream).
-        e = hipMemset(c, 0, cc * sizeof(uint32_t));
+        if (cc > 0) e = hipMemset(c, 0, cc * sizeof(uint32_t));
+        if (e == hipSuccess && sc > 0) e = hipMemsetD32(reinterpret_cast<hipDeviceptr_t>(sl), static_cast<int>(q4rdna::kSlotEmpty), sc);
         if (e == hipSuccess) e = hipDeviceSynchronize();
         if (e != hipSuccess) {
             (void)hipFree(p);
             (void)hipFree(c);
+            (void)hipFree(sl);
             return hip_fail(e, "hipMemset");
         }
         ws.partial = p;
         ws.counters = c;
+        ws.slots = sl;
         ws.partial_floats = pf;
         ws.counter_count = cc;
+        ws.slot_count = sc;
     }
     *out = &ws;
     return Q4RDNA_OK;
@@ -179,15 +193,16 @@ uint32_t resolve_split(const q4rdna_weight *w, uint32_t split) {
 int launch_one(const q4rdna::TensorLaunch &launch, const q4rdna_weight *w, const uint8_t *gate, const float *x,
                const float *add, float *y, hipStream_t stream) {
     float *partial = nullptr;
-    uint32_t *counters = nullptr;
-    if (launch.partial_floats > 0 || launch.counters > 0) {
+    uint32_t *counters = nullptr, *slots = nullptr;
+    if (launch.partial_floats > 0 || launch.counters > 0 || launch.slots > 0) {
         Workspace *ws = nullptr;
-        int rc = get_workspace(w->device, stream, launch.partial_floats, launch.counters, &ws);
+        int rc = get_workspace(w->device, stream, launch.partial_floats, launch.counters, launch.slots, &ws);
         if (rc != Q4RDNA_OK) return rc;
         partial = ws->partial;
         counters = ws->counters;
+        slots = ws->slots;
     }
-    return q4rdna::launch_tensor_in(launch, w, gate, x, add, y, partial, counters, stream);
+    return q4rdna::launch_tensor_in(launch, w, gate, x, add, y, partial, counters, slots, stream);
 }
 
 // Preconditions shared by the GEMV entry points.  NOT_APPLICABLE mirrors the
@@ -266,14 +281,18 @@ int check_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const fl
     const uint32_t groups = w->columns / kGroup;
     if (kernel == Q4RDNA_KERNEL_VALU) {
         L.split = resolve_split(w, s);
-        if (L.split > 1) {
+        if (L.split == 2) {
+            L.slots = static_cast<size_t>(w->rows) * (gate ? 2 : 1);
+        } else if (L.split > 2) {
             L.partial_floats = static_cast<size_t>(L.split) * w->rows * (gate ? 2 : 1);
             L.counters = w->rows / kTileRows;
         }
     } else {
         L.steps = gate != nullptr ? 1u : (steps != 0 ? steps : burst_steps_policy(blocks_of(w->rows), groups, cu_count(w->device)));
         L.chunks = burst_chunks(groups, L.steps);
-        if (L.chunks > 1) {
+        if (L.chunks == 2) {
+            L.slots = static_cast<size_t>(w->rows) * (gate ? 2 : 1);
+        } else if (L.chunks > 2) {
             L.partial_floats = static_cast<size_t>(L.chunks) * w->rows * (gate ? 2 : 1);
             L.counters = blocks_of(w->rows);
         }
@@ -283,11 +302,12 @@ int check_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const fl
 }
 
 int launch_tensor_in(const TensorLaunch &launch, const q4rdna_weight *w, const uint8_t *gate, const float *x,
-                     const float *add, float *y, float *partial, uint32_t *counters, hipStream_t stream) {
+                     const float *add, float *y, float *partial, uint32_t *counters, uint32_t *slots,
+                     hipStream_t stream) {
     hipError_t e;
     if (launch.kernel == Q4RDNA_KERNEL_BURST) {
         BurstArgs args{};
-        args.g[0] = BurstGemv{w->tiles, gate, add, y, partial, counters, w->rows, 0};
+        args.g[0] = BurstGemv{w->tiles, gate, add, y, partial, counters, slots, w->rows, 0};
         args.x = x;
         args.count = 1;
         args.cols = w->columns;
@@ -310,7 +330,9 @@ int launch_tensor_in(const TensorLaunch &launch, const q4rdna_weight *w, const u
         // against 68).
         const uint64_t workgroups = static_cast<uint64_t>(w->rows / kTileRows) * launch.split;
         args.short_waves = workgroups <= 4ull * cu_count(w->device) ? 8u : 4u;
-        if (launch.split > 1) {
+        if (launch.split == 2) {
+            args.slots = slots;
+        } else if (launch.split > 2) {
             args.partial = partial;
             args.counters = counters;
         }
@@ -621,35 +643,39 @@ int q4rdna_mul_mat_group(const q4rdna_group_desc *descs, uint32_t count, const f
     const uint32_t chunks = burst_chunks(groups, steps);
     if (blocks * chunks > 0x7fffffffull) return set_error(Q4RDNA_ERR_ARGUMENT, "group too large");
     const uint32_t streams = glu ? 2u : 1u;
-    size_t partial_floats = 0, counters = 0;
-    if (chunks > 1)
-        for (uint32_t i = 0; i < count; ++i) {
+    // Two chunks meet in exchange slots (rows x streams words per GEMV),
+    // more in partials and arrival counters.
+    size_t partial_floats = 0, counters = 0, slots = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        if (chunks == 2) {
+            slots += static_cast<size_t>(streams) * descs[i].weight.rows;
+        } else if (chunks > 2) {
             partial_floats += static_cast<size_t>(chunks) * streams * descs[i].weight.rows;
             counters += blocks_of(descs[i].weight.rows);
         }
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    float *partial = nullptr;
-    uint32_t *counter_base = nullptr;
-    if (chunks > 1) {
-        Workspace *ws = nullptr;
-        if ((rc = get_workspace(descs[0].weight.device, s, partial_floats, counters, &ws)) != Q4RDNA_OK) return rc;
-        partial = ws->partial;
-        counter_base = ws->counters;
     }
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    Workspace *ws = nullptr;
+    if (chunks > 1 &&
+        (rc = get_workspace(descs[0].weight.device, s, partial_floats, counters, slots, &ws)) != Q4RDNA_OK)
+        return rc;
     q4rdna::BurstArgs args{};
     args.x = x;
     args.count = count;
     args.cols = descs[0].weight.columns;
     args.chunks = chunks;
     uint32_t units = 0;
-    size_t poff = 0, coff = 0;
+    size_t poff = 0, coff = 0, soff = 0;
     for (uint32_t i = 0; i < count; ++i) {
         const q4rdna_group_desc &d = descs[i];
         args.g[i] = q4rdna::BurstGemv{d.weight.tiles, d.gate_tiles, d.add, d.y,
-                                      chunks > 1 ? partial + poff : nullptr, chunks > 1 ? counter_base + coff : nullptr,
-                                      d.weight.rows, units};
+                                      chunks > 2 ? ws->partial + poff : nullptr,
+                                      chunks > 2 ? ws->counters + coff : nullptr,
+                                      chunks == 2 ? ws->slots + soff : nullptr, d.weight.rows, units};
         units += blocks_of(d.weight.rows) * chunks;
-        if (chunks > 1) {
+        if (chunks == 2) {
+            soff += static_cast<size_t>(streams) * d.weight.rows;
+        } else if (chunks > 2) {
             poff += static_cast<size_t>(chunks) * streams * d.weight.rows;
             coff += blocks_of(d.weight.rows);
         }
@@ -706,7 +732,7 @@ int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, cons
     if (split > 1) {
         Workspace *ws = nullptr;
         const size_t pf = static_cast<size_t>(split) * n * w->rows * (gate ? 2 : 1);
-        if ((rc = get_workspace(w->device, s, pf, w->rows / kTileRows, &ws)) != Q4RDNA_OK) return rc;
+        if ((rc = get_workspace(w->device, s, pf, w->rows / kTileRows, 0, &ws)) != Q4RDNA_OK) return rc;
         args.partial = ws->partial;
         args.counters = ws->counters;
     }

@@ -33,6 +33,7 @@ GLU_SWIGLU = 0
 MAX_BATCH = 8
 NOALLOC_PARTIAL_FLOATS = 1 << 20
 NOALLOC_COUNTERS = 16384
+NOALLOC_SLOTS = 1 << 20
 
 # Every symbol include/q4rdna.h declares.
 EXPORTS = (

@@ -44,6 +44,7 @@ CASES = [
     # rows, cols, split, gate, add: a larger launch, then a smaller one
     (4096, 12288, 6, True, True),
     (1024, 4096, 4, False, False),
+    (12288, 4096, 2, True, False),
     (4096, 4096, 2, False, True),
     (96, 8192, 16, True, False),
 ]
@@ -70,7 +71,8 @@ def test_noalloc_equals_mul_mat_ex(cuda):
 
 def test_noalloc_refuses_what_does_not_fit(cuda):
     """151936 x 4096 at split 8 needs 1,215,488 partial floats, more than the
-    1,048,576 the array holds: refused, nothing launched."""
+    1,048,576 the array holds: refused, nothing launched.  Likewise a split-2
+    launch with more rows than exchange slots."""
     L = q4rdna.load()
     rows, cols = 151936, 4096
     w = api.QWeight.from_tiles(torch.zeros(api.packed_size(rows, cols), dtype=torch.uint8, device="cuda"), rows, cols)
@@ -86,6 +88,19 @@ def test_noalloc_refuses_what_does_not_fit(cuda):
     assert rc == q4rdna.OK
     torch.cuda.synchronize()
     assert (y == 0.0).all()
+    del w, y
+    # split 2 exchanges through one slot per row: 1,048,608 rows need more
+    # than the 1,048,576 slots
+    rows, cols = 1048608, 128
+    assert rows > _lib.NOALLOC_SLOTS
+    w = api.QWeight.from_tiles(torch.zeros(api.packed_size(rows, cols), dtype=torch.uint8, device="cuda"), rows, cols)
+    x = torch.zeros(cols, device="cuda")
+    y = torch.full((rows,), 7.0, device="cuda")
+    rc = call(L.q4rdna_mul_mat_ex_noalloc, w, None, x, None, y, 2, torch.cuda.current_stream().cuda_stream)
+    assert rc == q4rdna.ERR_ARGUMENT
+    assert "slots" in q4rdna.last_error()
+    torch.cuda.synchronize()
+    assert (y == 7.0).all()
 
 
 def test_noalloc_calls_replay_from_a_hip_graph(cuda):
