@@ -79,6 +79,55 @@ def build_stack(layers: int, seed: int):
     return tensors, data
 
 
+class KernelEvent:
+    """A HIP timing event created with hipEventDisableSystemFence, from the
+    HIP runtime torch loaded.  A default event (torch.cuda.Event) records
+    with a system-scope release: the cache write-back and invalidate it
+    costs lands inside the bracket it opens or closes, and measured 13 us
+    on top of a 535 us sweep kernel (rocprofv3 kernel trace of the same
+    run).  Without the fence the bracket reads the kernel's own duration.
+    Timing only: read it after a device synchronize."""
+    _hip = None
+    _DISABLE_SYSTEM_FENCE = 0x20000000
+
+    @classmethod
+    def _runtime(cls):
+        if cls._hip is None:
+            import ctypes
+            import torch
+            lib = ctypes.CDLL(os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so"))
+            lib.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+            lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+            lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+            lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+            cls._hip = lib
+        return cls._hip
+
+    def __init__(self):
+        import ctypes
+        self._ctypes = ctypes
+        self.ev = ctypes.c_void_p()
+        rc = self._runtime().hipEventCreateWithFlags(ctypes.byref(self.ev), self._DISABLE_SYSTEM_FENCE)
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreateWithFlags failed: {rc}")
+
+    def record(self, stream: int) -> None:
+        rc = self._hip.hipEventRecord(self.ev, stream)
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed: {rc}")
+
+    def elapsed_ms(self, end: "KernelEvent") -> float:
+        ms = self._ctypes.c_float()
+        rc = self._hip.hipEventElapsedTime(self._ctypes.byref(ms), self.ev, end.ev)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed: {rc}")
+        return ms.value
+
+    def __del__(self):
+        if self._hip is not None and self.ev:
+            self._hip.hipEventDestroy(self.ev)
+
+
 def time_plan(plan, steps: int, warmup: int, sample_every: int = 8):
     """Run warmup + timed steps; returns (wall ms per step, sweep ms list,
     prepare ms list).  Every `sample_every`-th timed step carries HIP events
@@ -91,10 +140,10 @@ def time_plan(plan, steps: int, warmup: int, sample_every: int = 8):
     # Events are made before the warmup, so the timed loop starts right after
     # the synchronize: an idle gap there has measured as ~20 slower steps.
     sampled = list(range(0, steps, sample_every))
-    ev = {i: [torch.cuda.Event(enable_timing=True) for _ in range(3)] for i in sampled}
+    ev = {i: [KernelEvent() for _ in range(3)] for i in sampled}
     for e in ev.values():
         for x in e:
-            x.record(stream)
+            x.record(s)
     for _ in range(warmup):
         plan.launch(s)
     torch.cuda.synchronize()
@@ -105,15 +154,15 @@ def time_plan(plan, steps: int, warmup: int, sample_every: int = 8):
             plan.prepare(s)
             plan.sweep(s)
             continue
-        e[0].record(stream)
+        e[0].record(s)
         plan.prepare(s)
-        e[1].record(stream)
+        e[1].record(s)
         plan.sweep(s)
-        e[2].record(stream)
+        e[2].record(s)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1000.0 / steps
-    prep = [ev[i][0].elapsed_time(ev[i][1]) for i in sampled]
-    sweep = [ev[i][1].elapsed_time(ev[i][2]) for i in sampled]
+    prep = [ev[i][0].elapsed_ms(ev[i][1]) for i in sampled]
+    sweep = [ev[i][1].elapsed_ms(ev[i][2]) for i in sampled]
     return wall_ms, sweep, prep
 
 
@@ -122,18 +171,17 @@ def cold_steps(plan, count: int):
     events around its sweep launch: the GPU's start of sustained streaming.
     Returns (sweep us per step, step us per step)."""
     import torch
-    stream = torch.cuda.current_stream()
-    s = stream.cuda_stream
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(count)]
+    s = torch.cuda.current_stream().cuda_stream
+    ev = [[KernelEvent() for _ in range(3)] for _ in range(count)]
     torch.cuda.synchronize()
     for e in ev:
-        e[0].record(stream)
+        e[0].record(s)
         plan.prepare(s)
-        e[1].record(stream)
+        e[1].record(s)
         plan.sweep(s)
-        e[2].record(stream)
+        e[2].record(s)
     torch.cuda.synchronize()
-    return [e[1].elapsed_time(e[2]) * 1000.0 for e in ev], [e[0].elapsed_time(e[2]) * 1000.0 for e in ev]
+    return [e[1].elapsed_ms(e[2]) * 1000.0 for e in ev], [e[0].elapsed_ms(e[2]) * 1000.0 for e in ev]
 
 
 def settle(plan, seconds: float) -> int:
@@ -183,14 +231,13 @@ def time_per_tensor_graph(tensors, steps: int, warmup: int):
             g.replay()
             s.synchronize()
             same = same and all(torch.equal(y, e) for y, e in zip(ys_graph, eager))
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record(s)
+        a, b = KernelEvent(), KernelEvent()
+        a.record(s.cuda_stream)
         for _ in range(steps):
             g.replay()
-        b.record(s)
+        b.record(s.cuda_stream)
     torch.cuda.synchronize()
-    return a.elapsed_time(b) * 1000.0 / steps, same
+    return a.elapsed_ms(b) * 1000.0 / steps, same
 
 
 def check_parity(tensors, picks):
@@ -328,13 +375,13 @@ def pack_figures(seed: int, sample_rows: int = 1024):
     w = outlier_weights(rows, cols, seed, frac=0.0)
     api.pack(w)
     torch.cuda.synchronize()
-    a = torch.cuda.Event(enable_timing=True)
-    b = torch.cuda.Event(enable_timing=True)
-    a.record()
+    a, b = KernelEvent(), KernelEvent()
+    cur = torch.cuda.current_stream().cuda_stream
+    a.record(cur)
     tiles = api.pack(w)
-    b.record()
+    b.record(cur)
     torch.cuda.synchronize()
-    gpu_ms = a.elapsed_time(b)
+    gpu_ms = a.elapsed_ms(b)
     sample = w[:sample_rows].cpu().numpy()
     t0 = time.perf_counter()
     ref = O.pack(sample, O.ALGO_SIDECAR)
@@ -399,25 +446,25 @@ def time_launches(launch, count: int, replays: int = 5) -> float:
     with torch.cuda.graph(graph, stream=stream):
         for i in range(count):
             launch(i)
-    a = torch.cuda.Event(enable_timing=True)
-    b = torch.cuda.Event(enable_timing=True)
-    a.record()
+    a, b = KernelEvent(), KernelEvent()
+    cur = torch.cuda.current_stream().cuda_stream
+    a.record(cur)
     graph.replay()
-    b.record()
+    b.record(cur)
     torch.cuda.synchronize()
     # About 30 ms of untimed replays first: on fresh buffers the first tens of
     # ms stream measurably slower (151936x4096: 67 us per launch, settling
     # to 60-61).
-    for _ in range(max(1, int(30.0 / max(a.elapsed_time(b), 1e-3)))):
+    for _ in range(max(1, int(30.0 / max(a.elapsed_ms(b), 1e-3)))):
         graph.replay()
     torch.cuda.synchronize()
-    a.record()
+    a.record(cur)
     for _ in range(replays):
         graph.replay()
-    b.record()
+    b.record(cur)
     torch.cuda.synchronize()
     del graph
-    return a.elapsed_time(b) * 1000.0 / (replays * count)
+    return a.elapsed_ms(b) * 1000.0 / (replays * count)
 
 
 def time_tensor(rows: int, cols: int, split: int, seed: int, reps: int = 40):
@@ -672,17 +719,22 @@ def layer_chain(tensors, replays: int, check_layers=(0, 17, 35)):
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=st):
             run(dispatch, bufs, st.cuda_stream)
+        # Untimed replays for about 0.2 s first: the GPU's clocks settle a
+        # few ms into sustained work.
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < 0.2:
+            with torch.cuda.stream(st):
+                for _ in range(5):
+                    graph.replay()
+            st.synchronize()
         with torch.cuda.stream(st):
-            for _ in range(3):
-                graph.replay()
-            a = torch.cuda.Event(enable_timing=True)
-            e = torch.cuda.Event(enable_timing=True)
-            a.record(st)
+            a, e = KernelEvent(), KernelEvent()
+            a.record(st.cuda_stream)
             for _ in range(replays):
                 graph.replay()
-            e.record(st)
+            e.record(st.cuda_stream)
         torch.cuda.synchronize()
-        us = a.elapsed_time(e) * 1000.0 / (replays * layers)
+        us = a.elapsed_ms(e) * 1000.0 / (replays * layers)
         layer_bytes = sum(algorithmic_bytes(by[f"blk.0.{p}.weight"]["rows"], by[f"blk.0.{p}.weight"]["cols"])
                           for p in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"))
         out[dispatch] = dict(launches_per_layer=6 if dispatch == "reference" else 4, us_per_layer=round(us, 2),
