@@ -627,10 +627,11 @@ def layer_chain(tensors, replays: int, check_layers=(0, 17, 35)):
     replayed:
       reference  the reference's hooks: q, k, v, o(+add), gate/up SwiGLU,
                  down(+add) as six per-tensor launches (VALU kernel)
-      grouped    q/k/v as one group launch sharing x (burst kernel), then
-                 o(+add), gate/up SwiGLU and down(+add) through the
-                 per-tensor entry points: four launches
-      burst      the same four launches all on the burst kernel
+      grouped    q/k/v as one group launch sharing x (the group policy:
+                 the VALU kernel), then o(+add), gate/up SwiGLU and
+                 down(+add) through the per-tensor entry points: four
+                 launches
+      burst      the same four launches all on the MFMA burst kernel
                  (activation converted in the kernel)
     Parity: every launch of layers `check_layers` against the fp64 oracle
     on the inputs it actually read."""
@@ -677,9 +678,10 @@ def layer_chain(tensors, replays: int, check_layers=(0, 17, 35)):
                 api.mul_mat_add(w(l, "ffn_down"), b["act"], b["h"], b["out"], stream=stream)
             else:
                 api.mul_mat_group([(w(l, "attn_q"), b["q"]), (w(l, "attn_k"), b["k"]), (w(l, "attn_v"), b["v"])], x,
-                                  stream=stream)
+                                  stream=stream, kernel=_lib.KERNEL_BURST)
                 api.mul_mat_ex(w(l, "attn_output"), b["q"], b["h"], add=x, kernel=_lib.KERNEL_BURST, stream=stream)
-                api.mul_mat_group([(w(l, "ffn_up"), b["act"], w(l, "ffn_gate"))], b["h"], stream=stream)
+                api.mul_mat_group([(w(l, "ffn_up"), b["act"], w(l, "ffn_gate"))], b["h"], stream=stream,
+                                  kernel=_lib.KERNEL_BURST)
                 api.mul_mat_ex(w(l, "ffn_down"), b["act"], b["out"], add=b["h"], kernel=_lib.KERNEL_BURST,
                                stream=stream)
 

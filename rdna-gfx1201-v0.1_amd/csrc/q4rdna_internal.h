@@ -140,6 +140,33 @@ struct BurstArgs {
 // steps = 1 or 2 (K chunk of 16 or 32 groups per unit).
 hipError_t launch_burst(const BurstArgs &args, uint32_t steps, hipStream_t stream);
 
+// A VALU group launch (gemv_kernel's arithmetic): up to kMaxBurst GEMVs
+// sharing x of `cols` floats, the row tiles of all of them numbered GEMV by
+// GEMV from tile_begin (`tiles` in all), each split into `split` K chunks of
+// at most kGroupChunkGroups groups.  The chunks of a row tile meet as in
+// gemv_kernel: split 2 in slots[rows (x2 with gate)], larger splits in
+// partial[split * rows (x2)] through counters[rows / 32].  gate is given for
+// every GEMV or for none; add may be null per GEMV.
+constexpr uint32_t kGroupChunkGroups = 64;
+struct GemvGroupEntry {
+    const uint8_t *w;
+    const uint8_t *gate;
+    const float *add;
+    float *y;
+    float *partial;
+    uint32_t *counters;
+    uint32_t *slots;
+    uint32_t rows;
+    uint32_t tile_begin;
+};
+struct GemvGroupArgs {
+    GemvGroupEntry g[kMaxBurst];
+    const float *x;
+    uint32_t count, cols, split, tiles;
+    uint32_t short_waves;  // 8 or 4, as GemvArgs::short_waves
+};
+hipError_t launch_gemv_group(const GemvGroupArgs &args, hipStream_t stream);
+
 hipError_t launch_dequant(const uint8_t *w, uint32_t rows, uint32_t cols, float *out,
                           hipStream_t stream);
 hipError_t launch_pack(const float *w, uint32_t rows, uint32_t cols, int algorithm, uint8_t *tiles,

@@ -34,6 +34,8 @@
 // waves' results in LDS in wave order, and K chunks split across
 // workgroups through a partial buffer summed in chunk order by the last
 // workgroup to arrive, so every result is bit-reproducible run to run.
+#include <type_traits>
+
 #include "q4rdna_device.h"
 
 namespace q4rdna {
@@ -314,6 +316,48 @@ __device__ __forceinline__ float epilogue(float v, float gv, const float *__rest
     return v;
 }
 
+// Where a row tile's chunk sums go (threads 0..31 hold row rt*32 + t's sum
+// v and SwiGLU gate sum gv of chunk s): split 1 writes y; split 2 meets the
+// other chunk in the row's exchange slot and the second to arrive writes y;
+// larger splits publish the chunk's partials with device-scope stores, wait
+// for them to complete, then count arrivals, and the last workgroup of the
+// row tile sums the chunks in chunk order and resets the counter.  `add` may
+// be null (ADD false makes it so at compile time).
+template <bool GATE, bool ADD>
+__device__ __forceinline__ void finish_rows(Shared &sh, float *__restrict__ y, const float *__restrict__ add,
+                                            float *__restrict__ partial, uint32_t *__restrict__ counters,
+                                            uint32_t *__restrict__ slots, uint32_t rows, uint32_t split, uint32_t s,
+                                            uint32_t rt, float v, float gv) {
+    const uint32_t row = rt * kTileRows + (threadIdx.x & 31);
+    if (split == 1) {
+        if (threadIdx.x < 32) y[row] = epilogue<GATE, ADD>(v, gv, add, row);
+        return;
+    }
+    if (split == 2) {
+        if (threadIdx.x < 32 && exchange_pair<GATE>(slots, row, v, gv)) y[row] = epilogue<GATE, ADD>(v, gv, add, row);
+        return;
+    }
+    if (threadIdx.x < 32) {
+        store_agent(&partial[static_cast<size_t>(s) * rows + row], v);
+        if constexpr (GATE) store_agent(&partial[static_cast<size_t>(split + s) * rows + row], gv);
+    }
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) sh.last = (add_agent(&counters[rt], 1u) == split - 1) ? 1u : 0u;
+    __syncthreads();
+    if (sh.last == 0u) return;
+    if (threadIdx.x < 32) {
+        float sum = load_agent(&partial[row]);
+        float gsum = GATE ? load_agent(&partial[static_cast<size_t>(split) * rows + row]) : 0.f;
+        for (uint32_t c = 1; c < split; ++c) {
+            sum += load_agent(&partial[static_cast<size_t>(c) * rows + row]);
+            if constexpr (GATE) gsum += load_agent(&partial[static_cast<size_t>(split + c) * rows + row]);
+        }
+        y[row] = epilogue<GATE, ADD>(sum, gsum, add, row);
+    }
+    if (threadIdx.x == 0) store_agent(&counters[rt], 0u);
+}
+
 // Workgroup b covers row tile rt and K chunk s of `split`, remapped so the
 // chunks of one row tile run on one XCD.
 template <bool GATE, bool ADD, int T, int W>
@@ -325,44 +369,41 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs args) {
     const uint32_t rt = logical / split, s = logical % split;
     const uint32_t g_begin = static_cast<uint32_t>((static_cast<uint64_t>(s) * groups) / split);
     const uint32_t g_end = static_cast<uint32_t>((static_cast<uint64_t>(s + 1) * groups) / split);
-    const uint32_t row = rt * kTileRows + (threadIdx.x & 31);
     float v = 0.f, gv = 0.f;
     if constexpr (T == 0)
         tile_row_partial<GATE>(sh, args.w, args.gate, args.x, args.cols, rt, g_begin, g_end, v, gv);
     else
         tile_row_partial_short<GATE, T, W>(sh, args.w, args.gate, args.x, args.cols, rt, g_begin, g_end, v, gv);
-    if (split == 1) {
-        if (threadIdx.x < 32) args.y[row] = epilogue<GATE, ADD>(v, gv, args.add, row);
-        return;
-    }
-    if (split == 2) {
-        // The row's second chunk to arrive finishes it.
-        if (threadIdx.x < 32 && exchange_pair<GATE>(args.slots, row, v, gv))
-            args.y[row] = epilogue<GATE, ADD>(v, gv, args.add, row);
-        return;
-    }
-    // Split K: publish this chunk's partials with device-scope stores, wait
-    // for them to complete, then count arrivals; the last workgroup of the
-    // row tile sums the chunks in chunk order and resets the counter.
-    if (threadIdx.x < 32) {
-        store_agent(&args.partial[static_cast<size_t>(s) * args.rows + row], v);
-        if constexpr (GATE) store_agent(&args.partial[static_cast<size_t>(split + s) * args.rows + row], gv);
-    }
-    wait_stores();
-    __syncthreads();
-    if (threadIdx.x == 0) sh.last = (add_agent(&args.counters[rt], 1u) == split - 1) ? 1u : 0u;
-    __syncthreads();
-    if (sh.last == 0u) return;
-    if (threadIdx.x < 32) {
-        float sum = load_agent(&args.partial[row]);
-        float gsum = GATE ? load_agent(&args.partial[static_cast<size_t>(split) * args.rows + row]) : 0.f;
-        for (uint32_t c = 1; c < split; ++c) {
-            sum += load_agent(&args.partial[static_cast<size_t>(c) * args.rows + row]);
-            if constexpr (GATE) gsum += load_agent(&args.partial[static_cast<size_t>(split + c) * args.rows + row]);
-        }
-        args.y[row] = epilogue<GATE, ADD>(sum, gsum, args.add, row);
-    }
-    if (threadIdx.x == 0) store_agent(&args.counters[rt], 0u);
+    finish_rows<GATE, ADD>(sh, args.y, args.add, args.partial, args.counters, args.slots, args.rows, split, s, rt, v,
+                           gv);
+}
+
+// Several GEMVs sharing x (q4rdna_mul_mat_group): the row tiles of all of
+// them form one index space, GEMV i owning [tile_begin_i, tile_begin_i +
+// rows_i / 32); workgroup b covers one (row tile, K chunk) as gemv_kernel
+// does.  Every K chunk holds at most W*T groups (the short-range path).
+template <bool GATE, int T, int W>
+__global__ __launch_bounds__(64 * W) void gemv_group_kernel(GemvGroupArgs a) {
+    __shared__ Shared sh;
+    const uint32_t groups = a.cols / kGroup;
+    const uint32_t split = a.split;
+    const uint32_t logical = xcd_remap(blockIdx.x, gridDim.x);
+    const uint32_t gt = logical / split, s = logical % split;
+    // The workgroup's GEMV (constant indices only, so the entries stay in
+    // the kernel-argument segment).
+    GemvGroupEntry G = a.g[0];
+#pragma unroll
+    for (uint32_t i = 1; i < kMaxBurst; ++i)
+        if (i < a.count && gt >= a.g[i].tile_begin) G = a.g[i];
+    const uint32_t rt = gt - G.tile_begin;
+    const uint32_t g_begin = static_cast<uint32_t>((static_cast<uint64_t>(s) * groups) / split);
+    const uint32_t g_end = static_cast<uint32_t>((static_cast<uint64_t>(s + 1) * groups) / split);
+    float v = 0.f, gv = 0.f;
+    tile_row_partial_short<GATE, T, W>(sh, G.w, G.gate, a.x, a.cols, rt, g_begin, g_end, v, gv);
+    if (G.add != nullptr)
+        finish_rows<GATE, true>(sh, G.y, G.add, G.partial, G.counters, G.slots, G.rows, split, s, rt, v, gv);
+    else
+        finish_rows<GATE, false>(sh, G.y, nullptr, G.partial, G.counters, G.slots, G.rows, split, s, rt, v, gv);
 }
 
 // ---- several activation vectors against one weight (n = 2..8) -------------
@@ -901,6 +942,37 @@ hipError_t launch_gemv(const GemvArgs &args, hipStream_t stream) {
     }
     return args.add != nullptr ? launch_gemv_t<false, true>(args, stream)
                                : launch_gemv_t<false, false>(args, stream);
+}
+
+hipError_t launch_gemv_group(const GemvGroupArgs &args, hipStream_t stream) {
+    const uint32_t groups = args.cols / kGroup;
+    const uint32_t chunk = (groups + args.split - 1) / args.split;
+    const dim3 grid(args.tiles * args.split);
+    const bool glu = args.g[0].gate != nullptr;
+    auto go = [&](auto gate_tag, auto t_tag, auto w_tag) {
+        constexpr bool G = decltype(gate_tag)::value;
+        constexpr int T = decltype(t_tag)::value, W = decltype(w_tag)::value;
+        hipLaunchKernelGGL((gemv_group_kernel<G, T, W>), grid, dim3(64 * W), 0, stream, args);
+    };
+    using F = std::false_type;
+    using Tr = std::true_type;
+    auto by_t = [&](auto gate_tag, auto w_tag) {
+        constexpr int W = decltype(w_tag)::value;
+        const uint32_t per_wave = (chunk + W - 1) / W;
+        if (per_wave <= 1) go(gate_tag, std::integral_constant<int, 1>{}, w_tag);
+        else if (per_wave <= 2) go(gate_tag, std::integral_constant<int, 2>{}, w_tag);
+        else if (per_wave <= 4) go(gate_tag, std::integral_constant<int, 4>{}, w_tag);
+        else if (per_wave <= 8) go(gate_tag, std::integral_constant<int, 8>{}, w_tag);
+        else go(gate_tag, std::integral_constant<int, 64 / W>{}, w_tag);
+    };
+    if (args.short_waves == kShortWaves) {
+        if (glu) by_t(Tr{}, std::integral_constant<int, kShortWaves>{});
+        else by_t(F{}, std::integral_constant<int, kShortWaves>{});
+    } else {
+        if (glu) by_t(Tr{}, std::integral_constant<int, kWaves>{});
+        else by_t(F{}, std::integral_constant<int, kWaves>{});
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_gemv_multi(const GemvArgs &args, hipStream_t stream) {

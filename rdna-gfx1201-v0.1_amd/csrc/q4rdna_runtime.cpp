@@ -47,6 +47,7 @@ int set_error(int code, const char *fmt, ...) {
 namespace {
 
 using q4rdna::kGroup;
+using q4rdna::kGroupChunkGroups;
 using q4rdna::kTileBytes;
 using q4rdna::kTileRows;
 using q4rdna::set_error;
@@ -611,6 +612,73 @@ int q4rdna_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const f
     return launch_one(L, w, gate ? gate->tiles : nullptr, x, add, y, static_cast<hipStream_t>(stream));
 }
 
+namespace {
+
+// A validated group on the VALU kernel: one index space of row tiles over
+// all GEMVs, every K chunk at most kGroupChunkGroups groups.  The split is
+// the shape policy's for the group's total rows (or the caller's), raised
+// until the chunks fit.
+int launch_group_valu(const q4rdna_group_desc *descs, uint32_t count, const float *x, bool glu, uint32_t split_k,
+                      hipStream_t stream) {
+    const uint32_t cols = descs[0].weight.columns, groups = cols / kGroup;
+    const int device = descs[0].weight.device;
+    uint64_t total_rows = 0;
+    for (uint32_t i = 0; i < count; ++i) total_rows += descs[i].weight.rows;
+    if (total_rows > 0x7fffffffull) return set_error(Q4RDNA_ERR_ARGUMENT, "group too large");
+    uint32_t split = split_k != 0 ? split_k : policy_split(static_cast<uint32_t>(total_rows), cols, device);
+    split = std::max(split, (groups + kGroupChunkGroups - 1) / kGroupChunkGroups);
+    split = std::min(split, groups);
+    if (split > kMaxSplit)
+        return set_error(Q4RDNA_NOT_APPLICABLE, "K = %u needs more than %u chunks of %u groups", cols, kMaxSplit,
+                         kGroupChunkGroups);
+    const uint32_t tiles = static_cast<uint32_t>(total_rows / kTileRows);
+    const uint64_t workgroups = static_cast<uint64_t>(tiles) * split;
+    if (workgroups > 0x7fffffffull) return set_error(Q4RDNA_ERR_ARGUMENT, "group too large");
+    const uint32_t streams = glu ? 2u : 1u;
+    size_t partial_floats = 0, counters = 0, slots = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        const uint32_t rows = descs[i].weight.rows;
+        if (split == 2) {
+            slots += static_cast<size_t>(streams) * rows;
+        } else if (split > 2) {
+            partial_floats += static_cast<size_t>(split) * streams * rows;
+            counters += rows / kTileRows;
+        }
+    }
+    Workspace *ws = nullptr;
+    int rc;
+    if (split > 1 && (rc = get_workspace(device, stream, partial_floats, counters, slots, &ws)) != Q4RDNA_OK) return rc;
+    q4rdna::GemvGroupArgs args{};
+    args.x = x;
+    args.count = count;
+    args.cols = cols;
+    args.split = split;
+    args.tiles = tiles;
+    args.short_waves = workgroups <= 4ull * cu_count(device) ? 8u : 4u;
+    uint32_t tile_begin = 0;
+    size_t poff = 0, coff = 0, soff = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        const q4rdna_group_desc &d = descs[i];
+        const uint32_t rows = d.weight.rows;
+        args.g[i] = q4rdna::GemvGroupEntry{d.weight.tiles, d.gate_tiles, d.add, d.y,
+                                           split > 2 ? ws->partial + poff : nullptr,
+                                           split > 2 ? ws->counters + coff : nullptr,
+                                           split == 2 ? ws->slots + soff : nullptr, rows, tile_begin};
+        tile_begin += rows / kTileRows;
+        if (split == 2) {
+            soff += static_cast<size_t>(streams) * rows;
+        } else if (split > 2) {
+            poff += static_cast<size_t>(split) * streams * rows;
+            coff += rows / kTileRows;
+        }
+    }
+    hipError_t e = q4rdna::launch_gemv_group(args, stream);
+    if (e != hipSuccess) return hip_fail(e, "group GEMV launch");
+    return Q4RDNA_OK;
+}
+
+}  // namespace
+
 int q4rdna_mul_mat_group(const q4rdna_group_desc *descs, uint32_t count, const float *x, int64_t x_ne0,
                          const q4rdna_launch_options *options, void *stream) {
     if (descs == nullptr || count == 0 || count > Q4RDNA_MAX_GROUP)
@@ -638,6 +706,17 @@ int q4rdna_mul_mat_group(const q4rdna_group_desc *descs, uint32_t count, const f
     const uint32_t groups = descs[0].weight.columns / kGroup;
     uint32_t steps = options ? options->burst_steps : 0;
     if (steps > 2) return set_error(Q4RDNA_ERR_ARGUMENT, "burst_steps %u is outside 0..2", steps);
+    const uint32_t split_k = options ? options->split_k : 0;
+    if (split_k > kMaxSplit) return set_error(Q4RDNA_ERR_ARGUMENT, "split_k %u exceeds %u", split_k, kMaxSplit);
+    uint32_t kernel = options ? options->kernel : Q4RDNA_KERNEL_POLICY;
+    if (kernel > Q4RDNA_KERNEL_BURST) return set_error(Q4RDNA_ERR_ARGUMENT, "unknown kernel %u", kernel);
+    // The policy: the VALU kernel (faster on every projection shape measured,
+    // alone or grouped) unless K needs more chunks than it splits into;
+    // burst_steps names the burst kernel, split_k the VALU kernel.
+    if (kernel == Q4RDNA_KERNEL_POLICY)
+        kernel = steps != 0 || groups > kGroupChunkGroups * kMaxSplit ? Q4RDNA_KERNEL_BURST : Q4RDNA_KERNEL_VALU;
+    if (kernel == Q4RDNA_KERNEL_VALU)
+        return launch_group_valu(descs, count, x, glu, split_k, static_cast<hipStream_t>(stream));
     if (glu) steps = 1;
     if (steps == 0) steps = burst_steps_policy(blocks, groups, cu_count(descs[0].weight.device));
     const uint32_t chunks = burst_chunks(groups, steps);

@@ -171,10 +171,13 @@ def mul_mat_batch(w: QWeight, x: torch.Tensor, y: torch.Tensor, gate: QWeight | 
                                              ctypes.byref(opts), s))
 
 
-def mul_mat_group(items: Sequence[tuple], x: torch.Tensor, burst_steps: int = 0, stream: int | None = None) -> bool:
+def mul_mat_group(items: Sequence[tuple], x: torch.Tensor, burst_steps: int = 0, stream: int | None = None,
+                  kernel: int = _lib.KERNEL_POLICY, split_k: int = 0) -> bool:
     """GEMVs sharing one activation x in one launch.  items: (weight, y) or
     (weight, y, gate_weight_or_None, add_or_None); every weight has
-    x.numel() columns.  Returns False when not applicable."""
+    x.numel() columns.  kernel: KERNEL_VALU (split_k applies, 0 = the
+    policy) or KERNEL_BURST (burst_steps applies); 0 = the policy.  Returns
+    False when not applicable."""
     if not 1 <= len(items) <= _lib.MAX_GROUP:
         raise ValueError(f"a group holds 1..{_lib.MAX_GROUP} GEMVs")
     descs = (_lib.GroupDesc * len(items))()
@@ -194,6 +197,8 @@ def mul_mat_group(items: Sequence[tuple], x: torch.Tensor, burst_steps: int = 0,
         descs[i].y = y.data_ptr()
     opts = LaunchOptions()
     opts.burst_steps = burst_steps
+    opts.kernel = kernel
+    opts.split_k = split_k
     s = _stream(x.device) if stream is None else stream
     return check(load().q4rdna_mul_mat_group(descs, len(items), x.data_ptr(), x.numel(), ctypes.byref(opts), s))
 
