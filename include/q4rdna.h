@@ -186,10 +186,15 @@ int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, cons
  * 1..Q4RDNA_MAX_GROUP; every weight has K = x_ne0 columns (else
  * NOT_APPLICABLE) and lives on the current device; gate_tiles is given for
  * every descriptor or for none, each of its weight's shape; no y may overlap
- * x.  x is converted once per workgroup in the kernel (no separate prepare
- * launch).  The split-K scratch is the stream's, as for q4rdna_mul_mat.  No
- * reference counterpart: the reference launches one kernel per projection
- * and fuses only gate/up (source/q4rdna.cu:736-741,769-793). */
+ * x.  x is read once per workgroup in the kernel (no separate prepare
+ * launch).  options->kernel: Q4RDNA_KERNEL_VALU (the policy; split_k applies,
+ * 0 = the shape policy for the group's total rows; each output then equals
+ * q4rdna_mul_mat_ex of its weight at that split bit for bit) or
+ * Q4RDNA_KERNEL_BURST (burst_steps applies; a nonzero burst_steps with the
+ * policy kernel selects it).  The split-K scratch is the stream's, as for
+ * q4rdna_mul_mat.  No reference counterpart: the reference launches one
+ * kernel per projection and fuses only gate/up
+ * (source/q4rdna.cu:736-741,769-793). */
 #define Q4RDNA_MAX_GROUP 8
 typedef struct q4rdna_group_desc {
     q4rdna_weight weight;      /* W (the up projection for SwiGLU) */

@@ -32,7 +32,9 @@
  *
  * Build: gcc -O2 -std=c11 -ffp-contract=off -fopenmp -fPIC -shared (no FMA
  * contraction, matching an x86-64 build of the reference without FMA
- * instructions; OpenMP only spreads independent rows over threads).
+ * instructions; OpenMP only spreads independent rows over threads).  The
+ * bench's CPU baseline also compiles it with -O3 -march=native on the host it
+ * runs on; contraction stays off there too, so its results are the same bits.
  */
 #include <fenv.h>
 #ifdef _OPENMP
