@@ -126,3 +126,39 @@ def test_split2_noalloc_shares_the_protocol(cuda):
         torch.cuda.synchronize()
         assert torch.isnan(y_bad).all()
         assert torch.equal(y_na, y_ref)
+
+
+@pytest.mark.parametrize("rows,cols", [(32, 128), (96, 192), (64, 4096), (160, 28672)])
+@pytest.mark.parametrize("kind", ["plain", "add", "glu", "glu+add"])
+def test_split2_edge_shapes(cuda, rows, cols, kind):
+    """Split 2 at the smallest shapes (one row tile; one group per chunk; an
+    odd group count) and a long K, with every epilogue: both parity bars."""
+    t, w = weight(rows, cols, rows + cols)
+    gt, g = weight(rows, cols, rows + cols + 1) if "glu" in kind else (None, None)
+    add_np = O.gaussian_x(rows, rows + 2 * cols) if "add" in kind else None
+    x_np = O.gaussian_x(cols, rows + 3 * cols)
+    y = torch.full((rows,), 7.0, device="cuda")
+    assert api.mul_mat_ex(w, torch.from_numpy(x_np).cuda(), y, gate=g,
+                          add=None if add_np is None else torch.from_numpy(add_np).cuda(), split_k=2)
+    torch.cuda.synchronize()
+    assert_gemv_parity(y.cpu().numpy(), t, rows, cols, x_np, gate_tiles=gt, add=add_np, label=(rows, cols, kind))
+
+
+def test_group_of_eight_mixed_rows(cuda):
+    """The largest group (8 GEMVs of different row counts, some with a bias)
+    on the VALU kernel at split 2: every output within both bars."""
+    cols = 4096
+    rows_list = [32, 64, 96, 1024, 4096, 128, 2048, 160]
+    members = []
+    for i, rows in enumerate(rows_list):
+        t, w = weight(rows, cols, 600 + i)
+        add_np = O.gaussian_x(rows, 610 + i) if i % 3 == 0 else None
+        members.append((t, w, add_np, rows))
+    x_np = O.gaussian_x(cols, 620)
+    x = torch.from_numpy(x_np).cuda()
+    ys = [torch.full((rows,), 7.0, device="cuda") for *_, rows in members]
+    items = [(w, y, None, None if a is None else torch.from_numpy(a).cuda()) for (t, w, a, rows), y in zip(members, ys)]
+    assert api.mul_mat_group(items, x, split_k=2)
+    torch.cuda.synchronize()
+    for (t, w, a, rows), y in zip(members, ys):
+        assert_gemv_parity(y.cpu().numpy(), t, rows, cols, x_np, add=a, label=rows)
