@@ -617,7 +617,8 @@ def tensor_table(seed: int):
     return rows_out
 
 
-def layer_chain(tensors, replays: int, check_layers=(0, 17, 35)):
+def layer_chain(tensors, replays: int, check_layers=(0, 17, 35),
+                dispatches=("reference", "grouped", "burst")):
     """The stack as a decoder runs it: layer l+1's input depends on layer l,
     so every projection waits for the one before.  Per layer: q, k, v on
     x_l; o on q's output plus the residual x_l (o's real input is the
@@ -686,7 +687,7 @@ def layer_chain(tensors, replays: int, check_layers=(0, 17, 35)):
                                stream=stream)
 
     out = {}
-    for dispatch in ("reference", "grouped", "burst"):
+    for dispatch in dispatches:
         bufs = buffers()
         st = torch.cuda.Stream()
         with torch.cuda.stream(st):
@@ -762,6 +763,8 @@ def main() -> int:
     ap.add_argument("--cold-steps", type=int, default=25, help="steps timed one by one right after the stack is built")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-per-tensor", action="store_true")
+    ap.add_argument("--no-layer-chain", action="store_true",
+                    help="skip the dependent decoder-layer chain (reference and grouped dispatch) in the stack bench")
     ap.add_argument("--no-fused", action="store_true",
                     help="skip the SwiGLU-fused stack (216 GEMVs, gate/up as one SwiGLU GEMV per layer)")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -836,6 +839,13 @@ def main() -> int:
         log(f"[bench] SwiGLU-fused stack ({fused['gemvs']} GEMVs): {fused['us_per_stack']:.1f} us per step, "
             f"parity gate {fused['parity_gate_max']:.2e}")
 
+    chain = None
+    if not args.no_layer_chain:
+        # One decoder layer after another (each layer's input is the
+        # previous one's output): the reference's six launches per layer and
+        # the grouped four, from HIP graphs of all 36 layers.
+        chain = layer_chain(tensors, 50, check_layers=(0, len(tensors) // 7 - 1), dispatches=("reference", "grouped"))
+
     value = stack_bytes / (ms_per_step / 1000.0) / 1e9
     achieved = stack_bytes / (sweep_us / 1e6) / 1e9
     traffic = load_traffic()
@@ -861,6 +871,7 @@ def main() -> int:
         "sweep_us": round(sweep_us, 2),
         "per_tensor_launches": per_tensor,
         "swiglu_fused_stack": fused,
+        "decoder_layer_chain": chain,
         "parity_gate_max": parity,
         "settle": {"seconds": args.settle, "untimed_steps": settled},
         "cold_start": None if not cold_sweep else {
