@@ -133,12 +133,14 @@ __device__ __forceinline__ void kslot_digits(const float (&xs)[16], bool have, i
 // Group factor 2^(E-26) of the digits (NaN for a non-finite group).
 __device__ __forceinline__ float digit_factor(bool bad, int e) { return bad ? __builtin_nanf("") : ldexpf(1.0f, e - 26); }
 
-// The k-slot's record is written whole, row 3 as zeros (stores that cover
-// whole 64-byte runs measured 0.7 us faster over a 20,736-group stack than
-// leaving a 16-byte hole in every record), with nontemporal stores: the
-// digits then leave the L2 as they are written instead of at the end of the
-// launch, and the sweep launch after it started 2.2 us sooner.
-__device__ __forceinline__ void prep_kslot(const float *x, int kslot, bool have, gptr_u8 out, bool &bad, int &e_out) {
+// With `pad` the k-slot's record is written whole, row 3 as zeros (stores
+// that cover whole 64-byte runs measured 0.7 us faster over a 20,736-group
+// stack than leaving a 16-byte hole in every record).  The stores are
+// nontemporal: the digits then leave the L2 as they are written instead of
+// at the end of the launch, and the sweep launch after it started 2.2 us
+// sooner.
+__device__ __forceinline__ void prep_kslot(const float *x, int kslot, bool have, bool pad, gptr_u8 out, bool &bad,
+                                           int &e_out) {
     float xs[16];
     load_kslot(x, kslot, have, xs);
     i32x4 rows[3];
@@ -146,7 +148,7 @@ __device__ __forceinline__ void prep_kslot(const float *x, int kslot, bool have,
     if (!have) return;
 #pragma unroll
     for (int d = 0; d < 3; ++d) __builtin_nontemporal_store(rows[d], (gptr_wi32x4)(out + 16 * d));
-    __builtin_nontemporal_store(i32x4{0, 0, 0, 0}, (gptr_wi32x4)(out + 48));
+    if (pad) __builtin_nontemporal_store(i32x4{0, 0, 0, 0}, (gptr_wi32x4)(out + 48));
 }
 
 // Single-vector layout per group (kPrepBytes = 272): byte (kslot*4 + d)*16 + e
@@ -164,7 +166,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const float *const *__restric
     gptr_u8 out = (gptr_u8)(prep + static_cast<size_t>(valid ? gid : 0) * kPrepBytes);
     bool bad;
     int e;
-    prep_kslot(x, kslot, valid, out + 64 * kslot, bad, e);
+    prep_kslot(x, kslot, valid, true, out + 64 * kslot, bad, e);
     if (valid && kslot == 0)
         __builtin_nontemporal_store(i32x4{static_cast<int>(__float_as_uint(digit_factor(bad, e))), 0, 0, 0},
                                     (gptr_wi32x4)(out + 256));
@@ -687,6 +689,11 @@ constexpr uint32_t kBatchQuadBytes = 1040;
 // Lane 4p + kslot of a wave converts k-slot kslot of the wave's (group,
 // vector) pair p (16 pairs per wave, pair = g * n + vector).  Slots past n in
 // the last quad are never written and stay zero from the plan's creation.
+// PAD: whole records (n > 2).  Whole records measured faster at n = 4 and 8
+// (prepare 15 / 25 against 17 / 31 us) and slower at n = 2 (12.5 against
+// 10.4 us), where half of each quad's slots stay unwritten anyway.  As a
+// run-time flag the same choice measured slower at n = 4 and 8 (21 / 38 us).
+template <bool PAD>
 __global__ __launch_bounds__(256) void prep_batch_kernel(const PlanDesc *__restrict__ descs,
                                                          const uint32_t *__restrict__ owner, uint32_t total_groups,
                                                          uint32_t n) {
@@ -702,7 +709,7 @@ __global__ __launch_bounds__(256) void prep_batch_kernel(const PlanDesc *__restr
     gptr_u8 quad = (gptr_u8)(d.prep + (static_cast<size_t>(g) * quads + vec / 4) * kBatchQuadBytes);
     bool bad;
     int e;
-    prep_kslot(x, kslot, valid, quad + 256 * kslot + 64 * slot, bad, e);
+    prep_kslot(x, kslot, valid, PAD, quad + 256 * kslot + 64 * slot, bad, e);
     if (valid && kslot == 0) __builtin_nontemporal_store(digit_factor(bad, e), (gptr_f32)(quad + 1024 + 4 * slot));
 }
 
@@ -1137,7 +1144,12 @@ hipError_t launch_plan(const PlanDesc *descs, const uint32_t *deal, uint32_t wor
 hipError_t launch_prep_batch(const PlanDesc *descs, const uint32_t *owner, uint32_t groups, uint32_t n,
                              hipStream_t stream) {
     if (groups == 0) return hipSuccess;
-    hipLaunchKernelGGL(prep_batch_kernel, dim3((groups * n + 63) / 64), dim3(256), 0, stream, descs, owner, groups, n);
+    if (n > 2)
+        hipLaunchKernelGGL(prep_batch_kernel<true>, dim3((groups * n + 63) / 64), dim3(256), 0, stream, descs, owner,
+                           groups, n);
+    else
+        hipLaunchKernelGGL(prep_batch_kernel<false>, dim3((groups * n + 63) / 64), dim3(256), 0, stream, descs, owner,
+                           groups, n);
     return hipGetLastError();
 }
 
