@@ -46,7 +46,8 @@ constexpr int kWaves = 4;
 // split into three balanced int8 digits.  A lane's three digit rows are 48
 // contiguous bytes (row d at 16*d) of a 64-byte k-slot record: the
 // single-vector and batched layouts both keep a k-slot's rows together.  Row
-// 3 is written as zeros: the MFMA rows it feeds are discarded.  `have` false:
+// 3 feeds MFMA rows that are discarded; it is written as zeros where the
+// record is written whole (prep_kslot's `pad`).  `have` false:
 // the lane's group lies past the end: it loads a readable stand-in group,
 // discards the values and writes nothing; its three sibling lanes are in
 // the same state.
@@ -153,10 +154,10 @@ __device__ __forceinline__ void prep_kslot(const float *x, int kslot, bool have,
 
 // Single-vector layout per group (kPrepBytes = 272): byte (kslot*4 + d)*16 + e
 // for digit d (row d = 3 holds zeros), the float factor 2^(E-26) at 256 (NaN
-// for a non-finite group) followed by 12 zero bytes.  Lane 4p + kslot of a wave converts k-slot kslot of the
-// wave's group p (16 groups per wave); group_x[g] is the address of global
-// group g's 64 activations (built by the host); its digits go to
-// prep + g * kPrepBytes.
+// for a non-finite group) followed by 12 zero bytes.  Lane 4p + kslot of a
+// wave converts k-slot kslot of the wave's group p (16 groups per wave);
+// group_x[g] is the address of global group g's 64 activations (built by the
+// host); its digits go to prep + g * kPrepBytes.
 __global__ __launch_bounds__(256) void prep_kernel(const float *const *__restrict__ group_x,
                                                    uint8_t *__restrict__ prep, uint32_t total_groups) {
     const int lane = threadIdx.x & 63, kslot = lane & 3;
