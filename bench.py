@@ -861,6 +861,9 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
+        "arithmetic": ("fp32 activations, outputs and accumulation; the sweep multiplies the 4-bit codes on int8 MFMA "
+                       "against each 64-element activation group re-encoded as three int8 digits of a 22-bit block "
+                       "fixed-point value (rounding <= 2^-23 of the group maximum), then applies the fp16 scales in fp32"),
         "data": "synthetic",
         "config": {"workload": f"qwen3-8b {args.layers}-layer stack: {len(tensors)} Q4_RDNA group-64 GEMVs at batch 1, "
                                "descriptors in layer order, fresh x per tensor, one multi-tensor plan per step",
