@@ -249,7 +249,7 @@ def check_parity(tensors, picks):
         tiles = t["w"].tiles.cpu().numpy()
         x = t["x"].cpu().numpy()
         y64, a64 = O.gemv_f64(tiles, t["rows"], t["cols"], x)
-        worst = max(worst, O.gemv_errors(t["y"].cpu().numpy(), y64, a64)["gate"])
+        worst = worse(worst, O.gemv_errors(t["y"].cpu().numpy(), y64, a64)["gate"])
     return worst
 
 
@@ -409,6 +409,13 @@ def load_traffic():
         return None
 
 
+def worse(a: float, *more: float) -> float:
+    """The largest error figure; NaN (a non-finite output) counts as inf, so
+    it can never hide behind a finite one as it would in max()."""
+    vals = (a,) + more
+    return float("inf") if any(v != v for v in vals) else max(vals)
+
+
 def mean(v):
     return sum(v) / len(v)
 
@@ -513,7 +520,7 @@ def batch_table(tensors, batches, steps: int, warmup: int, seed: int):
             ys = items[i][2].cpu().numpy()
             for v in range(n):
                 y64, a64 = O.gemv_f64(tiles, t["rows"], t["cols"], xs[v])
-                worst = max(worst, O.gemv_errors(ys[v], y64, a64)["gate"])
+                worst = worse(worst, O.gemv_errors(ys[v], y64, a64)["gate"])
         layers = len(tensors) / 7
         row = dict(batch=n, us_per_stack=round(ms_per_step * 1000, 2), us_per_layer=round(ms_per_step * 1000 / layers, 2),
                    sweep_us=round(mean(sweep_ms) * 1000, 2), prepare_us=round(mean(prep_ms) * 1000, 2),
@@ -617,29 +624,54 @@ def tensor_table(seed: int):
     return rows_out
 
 
+def chain_parity(y, tiles, rows, cols, xin, add=None, gate_tiles=None):
+    """One launch of the chain against both bars, on the inputs it read: the
+    per-row gate against the fp64 oracle and the relative L2 against the
+    reference bench's sequential fp32 loop (epilogues applied in fp64).  A
+    non-finite output gives inf."""
+    import numpy as np
+    import oracle as O
+    y = np.asarray(y, dtype=np.float64)
+    if not np.isfinite(y).all():
+        return float("inf"), float("inf")
+    want, _ = O.gemv_f64(tiles, rows, cols, xin)
+    seq = O.gemv_seq_f32_mt(tiles, rows, cols, xin)[0].astype(np.float64)
+    if add is not None:
+        want, seq = want + add, seq + add
+    if gate_tiles is not None:
+        g64, _ = O.gemv_f64(gate_tiles, rows, cols, xin)
+        gseq = O.gemv_seq_f32_mt(gate_tiles, rows, cols, xin)[0].astype(np.float64)
+        want, seq = want * O.silu(g64), seq * O.silu(gseq)
+    rms = float(np.sqrt(np.mean(want ** 2)))
+    return float(np.max(np.abs(y - want) / np.maximum(np.abs(want), 0.01 * rms))), O.rel_l2(y, seq)
+
+
 def layer_chain(tensors, replays: int, check_layers=(0, 17, 35),
-                dispatches=("reference", "grouped", "burst")):
+                dispatches=("reference", "grouped")):
     """The stack as a decoder runs it: layer l+1's input depends on layer l,
-    so every projection waits for the one before.  Per layer: q, k, v on
-    x_l; o on q's output plus the residual x_l (o's real input is the
-    attention output, a step outside this path) giving h; gate/up SwiGLU on
-    h; down on that plus the residual h, giving x_{l+1}.  Two dispatches over
-    the same weights, each captured into one HIP graph of all 36 layers and
-    replayed:
+    so every projection waits for the one before.  Per layer: x_l RMS-
+    normalized feeds q, k and v; o on q's output plus the residual x_l (o's
+    real input is the attention output, a step outside this path) gives h;
+    h RMS-normalized feeds the gate/up SwiGLU site; down on that plus the
+    residual h gives x_{l+1}.  The two normalizations stand for the
+    decoder's own (without them the N(0, 0.02) weights grow the activations
+    quadratically through SwiGLU, to inf within five layers); each is one
+    torch kernel.  Two dispatches over the same weights, each captured into
+    one HIP graph of all 36 layers and replayed:
       reference  the reference's hooks: q, k, v, o(+add), gate/up SwiGLU,
                  down(+add) as six per-tensor launches (VALU kernel)
       grouped    q/k/v as one group launch sharing x (the group policy:
                  the VALU kernel), then o(+add), gate/up SwiGLU and
                  down(+add) through the per-tensor entry points: four
                  launches
-      burst      the same four launches all on the MFMA burst kernel
-                 (activation converted in the kernel)
-    Parity: every launch of layers `check_layers` against the fp64 oracle
-    on the inputs it actually read."""
+    us_per_layer is the whole chain's time per layer, normalizations
+    included; norm_us_per_layer is a graph of the normalizations alone over
+    the same buffers, and gemv_us_per_layer the difference, the GEMV
+    launches' share.  Parity: every launch of layers `check_layers` against
+    both bars on the inputs it actually read; replays equal the eager run."""
     import numpy as np
     import torch
-    import oracle as O
-    from q4rdna import _lib, api
+    from q4rdna import api
 
     by = {t["name"]: t for t in tensors}
     layers = len(tensors) // 7
@@ -655,73 +687,35 @@ def layer_chain(tensors, replays: int, check_layers=(0, 17, 35),
     def buffers():
         b = []
         for l in range(layers):
-            b.append(dict(q=torch.empty(4096, device=dev), k=torch.empty(1024, device=dev),
-                          v=torch.empty(1024, device=dev), h=torch.empty(4096, device=dev),
+            b.append(dict(xn=torch.empty(4096, device=dev), q=torch.empty(4096, device=dev),
+                          k=torch.empty(1024, device=dev), v=torch.empty(1024, device=dev),
+                          h=torch.empty(4096, device=dev), hn=torch.empty(4096, device=dev),
                           act=torch.empty(12288, device=dev), out=torch.empty(4096, device=dev)))
         return b
 
-    def run(dispatch, bufs, stream):
+    def norm(x, out):
+        out.copy_(torch.nn.functional.rms_norm(x, (x.numel(),), eps=1e-6))
+
+    def run(dispatch, bufs, stream, gemvs=True):
         for l in range(layers):
             b = bufs[l]
             x = x0 if l == 0 else bufs[l - 1]["out"]
-            if dispatch == "reference":
-                api.mul_mat(w(l, "attn_q"), x, b["q"], stream=stream)
-                api.mul_mat(w(l, "attn_k"), x, b["k"], stream=stream)
-                api.mul_mat(w(l, "attn_v"), x, b["v"], stream=stream)
+            norm(x, b["xn"])
+            if gemvs:
+                if dispatch == "reference":
+                    api.mul_mat(w(l, "attn_q"), b["xn"], b["q"], stream=stream)
+                    api.mul_mat(w(l, "attn_k"), b["xn"], b["k"], stream=stream)
+                    api.mul_mat(w(l, "attn_v"), b["xn"], b["v"], stream=stream)
+                else:
+                    api.mul_mat_group([(w(l, "attn_q"), b["q"]), (w(l, "attn_k"), b["k"]),
+                                       (w(l, "attn_v"), b["v"])], b["xn"], stream=stream)
                 api.mul_mat_add(w(l, "attn_output"), b["q"], x, b["h"], stream=stream)
-                api.mul_mat_glu(w(l, "ffn_up"), w(l, "ffn_gate"), b["h"], b["act"], stream=stream)
+            norm(b["h"], b["hn"])
+            if gemvs:
+                api.mul_mat_glu(w(l, "ffn_up"), w(l, "ffn_gate"), b["hn"], b["act"], stream=stream)
                 api.mul_mat_add(w(l, "ffn_down"), b["act"], b["h"], b["out"], stream=stream)
-            elif dispatch == "grouped":
-                api.mul_mat_group([(w(l, "attn_q"), b["q"]), (w(l, "attn_k"), b["k"]), (w(l, "attn_v"), b["v"])], x,
-                                  stream=stream)
-                api.mul_mat_add(w(l, "attn_output"), b["q"], x, b["h"], stream=stream)
-                api.mul_mat_glu(w(l, "ffn_up"), w(l, "ffn_gate"), b["h"], b["act"], stream=stream)
-                api.mul_mat_add(w(l, "ffn_down"), b["act"], b["h"], b["out"], stream=stream)
-            else:
-                api.mul_mat_group([(w(l, "attn_q"), b["q"]), (w(l, "attn_k"), b["k"]), (w(l, "attn_v"), b["v"])], x,
-                                  stream=stream, kernel=_lib.KERNEL_BURST)
-                api.mul_mat_ex(w(l, "attn_output"), b["q"], b["h"], add=x, kernel=_lib.KERNEL_BURST, stream=stream)
-                api.mul_mat_group([(w(l, "ffn_up"), b["act"], w(l, "ffn_gate"))], b["h"], stream=stream,
-                                  kernel=_lib.KERNEL_BURST)
-                api.mul_mat_ex(w(l, "ffn_down"), b["act"], b["out"], add=b["h"], kernel=_lib.KERNEL_BURST,
-                               stream=stream)
 
-    out = {}
-    for dispatch in dispatches:
-        bufs = buffers()
-        st = torch.cuda.Stream()
-        with torch.cuda.stream(st):
-            run(dispatch, bufs, st.cuda_stream)  # eager: allocates the stream's split-K workspace
-        torch.cuda.synchronize()
-        # Parity on the eager run: each launch against the oracle on its own inputs.
-        worst = 0.0
-        for l in check_layers:
-            if l >= layers:
-                continue
-            b = bufs[l]
-            x = (x0 if l == 0 else bufs[l - 1]["out"]).cpu().numpy()
-            q, h, act = b["q"].cpu().numpy(), b["h"].cpu().numpy(), b["act"].cpu().numpy()
-
-            def gate_of(y, part, xin, add=None, gate_part=None):
-                t = by[f"blk.{l}.{part}.weight"]
-                y64, a64 = O.gemv_f64(t["w"].tiles.cpu().numpy(), t["rows"], t["cols"], xin)
-                want, bound = y64, a64
-                if add is not None:
-                    want, bound = want + add.astype(np.float64), bound + np.abs(add)
-                if gate_part is not None:
-                    g = by[f"blk.{l}.{gate_part}.weight"]
-                    g64, ga = O.gemv_f64(g["w"].tiles.cpu().numpy(), g["rows"], g["cols"], xin)
-                    want = want * O.silu(g64)
-                rms = float(np.sqrt(np.mean(want ** 2)))
-                return float(np.max(np.abs(y.astype(np.float64) - want) / np.maximum(np.abs(want), 0.01 * rms)))
-
-            worst = max(worst, gate_of(q, "attn_q", x), gate_of(b["k"].cpu().numpy(), "attn_k", x),
-                        gate_of(b["v"].cpu().numpy(), "attn_v", x), gate_of(h, "attn_output", q, add=x),
-                        gate_of(act, "ffn_up", h, gate_part="ffn_gate"),
-                        gate_of(b["out"].cpu().numpy(), "ffn_down", act, add=h))
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=st):
-            run(dispatch, bufs, st.cuda_stream)
+    def time_graph(graph, st):
         # Untimed replays for about 0.2 s first: the GPU's clocks settle a
         # few ms into sustained work.
         t0 = time.perf_counter()
@@ -737,14 +731,56 @@ def layer_chain(tensors, replays: int, check_layers=(0, 17, 35),
                 graph.replay()
             e.record(st.cuda_stream)
         torch.cuda.synchronize()
-        us = a.elapsed_ms(e) * 1000.0 / (replays * layers)
+        return a.elapsed_ms(e) * 1000.0 / (replays * layers)
+
+    out = {}
+    for dispatch in dispatches:
+        bufs = buffers()
+        st = torch.cuda.Stream()
+        with torch.cuda.stream(st):
+            run(dispatch, bufs, st.cuda_stream)  # eager: allocates the stream's split-K workspace
+        torch.cuda.synchronize()
+        eager = [{k: v.clone() for k, v in b.items()} for b in bufs]
+        # Parity on the eager run: each launch against the oracle on its own inputs.
+        gate_max, l2_max = 0.0, 0.0
+        for l in check_layers:
+            if l >= layers:
+                continue
+            b = {k: v.cpu().numpy() for k, v in eager[l].items()}
+            x = (x0 if l == 0 else eager[l - 1]["out"]).cpu().numpy()
+
+            def tiles(part):
+                return by[f"blk.{l}.{part}.weight"]["w"].tiles.cpu().numpy()
+
+            for figures in (chain_parity(b["q"], tiles("attn_q"), 4096, 4096, b["xn"]),
+                            chain_parity(b["k"], tiles("attn_k"), 1024, 4096, b["xn"]),
+                            chain_parity(b["v"], tiles("attn_v"), 1024, 4096, b["xn"]),
+                            chain_parity(b["h"], tiles("attn_output"), 4096, 4096, b["q"], add=x),
+                            chain_parity(b["act"], tiles("ffn_up"), 12288, 4096, b["hn"], gate_tiles=tiles("ffn_gate")),
+                            chain_parity(b["out"], tiles("ffn_down"), 4096, 12288, b["act"], add=b["h"])):
+                gate_max, l2_max = worse(gate_max, figures[0]), worse(l2_max, figures[1])
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=st):
+            run(dispatch, bufs, st.cuda_stream)
+        us = time_graph(graph, st)
+        same = all(torch.equal(bufs[l][k], eager[l][k]) for l in range(layers) for k in bufs[l])
+        norms = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(norms, stream=st):
+            run(dispatch, bufs, st.cuda_stream, gemvs=False)
+        norm_us = time_graph(norms, st)
         layer_bytes = sum(algorithmic_bytes(by[f"blk.0.{p}.weight"]["rows"], by[f"blk.0.{p}.weight"]["cols"])
                           for p in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"))
+        gemv_us = us - norm_us
         out[dispatch] = dict(launches_per_layer=6 if dispatch == "reference" else 4, us_per_layer=round(us, 2),
-                             gb_per_s=round(layer_bytes / us / 1e3, 1), pct_of_peak=round(layer_bytes / us / 1e3 / 80, 2),
-                             parity_gate_max=worst)
-        log(f"[layer] {dispatch}: {us:.2f} us per layer ({out[dispatch]['gb_per_s']} GB/s), parity gate {worst:.2e}")
-        del graph, bufs
+                             norm_us_per_layer=round(norm_us, 2), gemv_us_per_layer=round(gemv_us, 2),
+                             gb_per_s=round(layer_bytes / gemv_us / 1e3, 1),
+                             pct_of_peak=round(layer_bytes / gemv_us / 1e3 / 80, 2),
+                             parity_gate_max=gate_max, parity_rel_l2_max=l2_max, replays_equal_eager=same,
+                             parity_layers=[l for l in check_layers if l < layers])
+        log(f"[layer] {dispatch}: {us:.2f} us per layer, normalizations {norm_us:.2f} us, GEMVs {gemv_us:.2f} us "
+            f"({out[dispatch]['gb_per_s']} GB/s), parity gate {gate_max:.2e}, rel-L2 {l2_max:.2e}, "
+            f"replays equal eager: {same}")
+        del graph, norms, bufs
     out["layers"] = layers
     out["target_us_per_layer_at_70pct"] = 18.36
     return out
@@ -775,7 +811,7 @@ def main() -> int:
                          "vectors per GEMV and print one JSON line with the table instead of the stack bench")
     ap.add_argument("--layer-chain", action="store_true",
                     help="the stack as dependent decoder layers (q/k/v -> o -> gate/up -> down, 36 layers, HIP graph): "
-                         "us per layer for the reference's per-tensor dispatch and for the burst dispatch; prints one "
+                         "us per layer for the reference's per-tensor dispatch and for the grouped dispatch; prints one "
                          "JSON line instead of the stack bench")
     ap.add_argument("--tensors", action="store_true",
                     help="per-tensor launch figures (projection shapes, lm_head, long-K split sweep with "
@@ -844,7 +880,9 @@ def main() -> int:
         # One decoder layer after another (each layer's input is the
         # previous one's output): the reference's six launches per layer and
         # the grouped four, from HIP graphs of all 36 layers.
-        chain = layer_chain(tensors, 50, check_layers=(0, len(tensors) // 7 - 1), dispatches=("reference", "grouped"))
+        layers = len(tensors) // 7
+        chain = layer_chain(tensors, 50, check_layers=sorted({0, layers // 2 - 1 if layers > 2 else 0, layers - 1}),
+                            dispatches=("reference", "grouped"))
 
     value = stack_bytes / (ms_per_step / 1000.0) / 1e9
     achieved = stack_bytes / (sweep_us / 1e6) / 1e9

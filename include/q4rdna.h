@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define Q4RDNA_ABI_VERSION 1
+#define Q4RDNA_ABI_VERSION 2
 
 /* status codes */
 #define Q4RDNA_OK 0
@@ -146,19 +146,17 @@ int q4rdna_mul_mat_glu(const q4rdna_weight *up, const q4rdna_weight *gate, const
                        int64_t x_ne0, int glu_op, float *y, int64_t y_ne0, void *stream);
 
 /* Launch options: split_k = number of K chunks reduced across workgroups of
- * the VALU kernel (0 = the shape policy, the reference's launch policy at
- * source/q4rdna.cu:578-680 and its LLAMA_Q4_RDNA_COOP override :579-584);
- * kernel = which per-tensor kernel runs (Q4RDNA_KERNEL_*; 0 = the shape
- * policy); burst_steps = K chunk of a burst unit in 16-group steps (1 or 2,
- * 0 = the shape policy).  Zero-initialised options mean "policy" throughout. */
+ * the per-tensor kernel (0 = the shape policy, the reference's launch policy
+ * at source/q4rdna.cu:578-680 and its LLAMA_Q4_RDNA_COOP override
+ * :579-584); kernel = Q4RDNA_KERNEL_POLICY or Q4RDNA_KERNEL_VALU (the same
+ * kernel; any other value is an argument error); reserved words must be
+ * zero.  Zero-initialised options mean "policy" throughout. */
 #define Q4RDNA_KERNEL_POLICY 0
-#define Q4RDNA_KERNEL_VALU 1  /* split-K VALU kernel (split_k applies) */
-#define Q4RDNA_KERNEL_BURST 2 /* int8-MFMA burst kernel (burst_steps applies) */
+#define Q4RDNA_KERNEL_VALU 1 /* the split-K VALU kernel (split_k applies) */
 typedef struct q4rdna_launch_options {
     uint32_t split_k;
     uint32_t kernel;
-    uint32_t burst_steps;
-    uint32_t reserved[5];
+    uint32_t reserved[6];
 } q4rdna_launch_options;
 
 /* q4rdna_mul_mat / _add / _glu with explicit options (add, gate may be NULL). */
@@ -186,14 +184,17 @@ int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, cons
  * 1..Q4RDNA_MAX_GROUP; every weight has K = x_ne0 columns (else
  * NOT_APPLICABLE) and lives on the current device; gate_tiles is given for
  * every descriptor or for none, each of its weight's shape; no y may overlap
- * x.  x is read once per workgroup in the kernel (no separate prepare
- * launch).  options->kernel: Q4RDNA_KERNEL_VALU (the policy; split_k applies,
- * 0 = the shape policy for the group's total rows; each output then equals
- * q4rdna_mul_mat_ex of its weight at that split bit for bit) or
- * Q4RDNA_KERNEL_BURST (burst_steps applies; a nonzero burst_steps with the
- * policy kernel selects it).  The split-K scratch is the stream's, as for
- * q4rdna_mul_mat.  No reference counterpart: the reference launches one
- * kernel per projection and fuses only gate/up
+ * x, another descriptor's y or another descriptor's add (argument error).
+ * x is read once per workgroup in the kernel (no separate prepare launch).
+ * options->split_k applies (0 = the shape policy for the group's total rows,
+ * raised until every K chunk holds at most 64 groups; K above 262,144
+ * columns, 64 chunks of 64 groups, is NOT_APPLICABLE).  Each output equals q4rdna_mul_mat_ex of its
+ * weight at the group's split bit for bit when both launches run the same
+ * workgroup width: eight waves, which each launch uses while it has at most
+ * four workgroups per CU (rows / 32 * split of the whole group, or of the one
+ * weight), and four waves above that.  The split-K scratch is the stream's,
+ * as for q4rdna_mul_mat.  No reference counterpart: the reference launches
+ * one kernel per projection and fuses only gate/up
  * (source/q4rdna.cu:736-741,769-793). */
 #define Q4RDNA_MAX_GROUP 8
 typedef struct q4rdna_group_desc {
@@ -222,7 +223,10 @@ uint32_t q4rdna_policy_split_k(uint32_t rows, uint32_t columns, int device);
  * q4rdna_mul_mat_ex (bit-identical at the same split).  Every call on a GPU
  * shares that GPU's array: calls that overlap on one GPU race, so issue them
  * on one stream or order them with events.  The first call on a GPU looks
- * the array up and sets its counters and slots with a kernel on `stream`. */
+ * the array's address up; its counters and slots are zero from the start
+ * (a zero-initialised device variable, left zero by every launch), so no
+ * set-up runs on any stream and the first call may be captured into a
+ * graph. */
 #define Q4RDNA_NOALLOC_PARTIAL_FLOATS (1u << 20)
 #define Q4RDNA_NOALLOC_COUNTERS 16384u
 #define Q4RDNA_NOALLOC_SLOTS (1u << 20)

@@ -340,3 +340,21 @@ def gaussian_weights(rows: int, cols: int, seed: int, std: float = 0.02) -> np.n
 
 def gaussian_x(cols: int, seed: int) -> np.ndarray:
     return np.random.default_rng(seed).standard_normal(cols, dtype=np.float32)
+
+
+def bench_activation(cols: int) -> np.ndarray:
+    """The reference bench's deterministic activation
+    (source/q4rdna_gemv_bench.hip:224-227): x_i = sinf(float(i) * 0.013f) *
+    0.25f + cosf(float(i) * 0.007f) * 0.125f, all in fp32.  The arguments are
+    fp32 products, sinf/cosf are the C library's (the reference's std::sin
+    and std::cos on float), and since the two scalings by powers of two are
+    exact, the sum rounds once whether or not the compiler fuses it."""
+    libm = ctypes.CDLL("libm.so.6")
+    libm.sinf.restype = libm.cosf.restype = ctypes.c_float
+    libm.sinf.argtypes = libm.cosf.argtypes = [ctypes.c_float]
+    i = np.arange(cols, dtype=np.float32)
+    a = i * np.float32(0.013)
+    b = i * np.float32(0.007)
+    s = np.array([libm.sinf(float(v)) for v in a], dtype=np.float32)
+    c = np.array([libm.cosf(float(v)) for v in b], dtype=np.float32)
+    return (s * np.float32(0.25) + c * np.float32(0.125)).astype(np.float32)

@@ -59,40 +59,40 @@ __device__ __forceinline__ uint32_t add_agent(uint32_t *p, uint32_t v) {
 // operations across it.
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// Two K chunks of a row meet in one exchange slot (kSlotEmpty between
-// launches): each chunk's workgroup swaps its partial sums into the slot with
-// one device-scope atomic.  The first to arrive reads kSlotEmpty back and is
+// Two K chunks of a row meet in one exchange slot (zero between launches):
+// each chunk's workgroup swaps its partial sums, XOR kSlotKey, into the slot
+// with one device-scope atomic.  The first to arrive reads zero back and is
 // done; the second reads the first's partials, adds its own -- fp32 addition
 // is commutative, so the sum is the same whichever chunk came first -- and
-// puts kSlotEmpty back.  One atomic round trip replaces the store,
+// puts zero back.  One atomic round trip replaces the store,
 // acknowledgement, arrival count and reload of the arrival chain.  A partial
-// whose bits equal the sentinel (a signaling NaN, which arithmetic never
-// produces) is sent as a quiet NaN.  GATE: the slot is the 64-bit pair (sum,
-// SwiGLU gate sum) at words 2*row, 2*row + 1; otherwise word row.  Both
-// layouts keep every word kSlotEmpty between launches, so one slot region
-// serves both.
+// whose bits equal kSlotKey (a signaling NaN, which arithmetic never
+// produces) would store as zero, so it is sent as a quiet NaN.  GATE: the
+// slot is the 64-bit pair (sum, SwiGLU gate sum) at words 2*row, 2*row + 1,
+// and only the sum's word tells an empty slot; otherwise word row.  Both
+// layouts keep every word zero between launches, so one slot region serves
+// both, and zero-filled memory is a valid empty region.
 typedef __attribute__((address_space(1))) uint64_t *gptr_au64;
-__device__ __forceinline__ uint32_t slot_bits(float v) {
+__device__ __forceinline__ uint32_t slot_word(float v) {
     const uint32_t b = __float_as_uint(v);
-    return b == kSlotEmpty ? kSlotQuietNan : b;
+    return (b == kSlotKey ? kSlotQuietNan : b) ^ kSlotKey;
 }
 template <bool GATE>
 __device__ __forceinline__ bool exchange_pair(uint32_t *slots, uint32_t row, float &v, float &gv) {
     if constexpr (GATE) {
         gptr_au64 p = (gptr_au64)slots + row;
-        const uint64_t mine = (static_cast<uint64_t>(__float_as_uint(gv)) << 32) | slot_bits(v);
+        const uint64_t mine = (static_cast<uint64_t>(__float_as_uint(gv) ^ kSlotKey) << 32) | slot_word(v);
         const uint64_t got = __hip_atomic_exchange(p, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (static_cast<uint32_t>(got) == kSlotEmpty) return false;
-        v = __uint_as_float(static_cast<uint32_t>(got)) + v;
-        gv = __uint_as_float(static_cast<uint32_t>(got >> 32)) + gv;
-        __hip_atomic_store(p, (static_cast<uint64_t>(kSlotEmpty) << 32) | kSlotEmpty, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+        if (static_cast<uint32_t>(got) == 0u) return false;
+        v = __uint_as_float(static_cast<uint32_t>(got) ^ kSlotKey) + v;
+        gv = __uint_as_float(static_cast<uint32_t>(got >> 32) ^ kSlotKey) + gv;
+        __hip_atomic_store(p, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else {
         gptr_au32 p = (gptr_au32)slots + row;
-        const uint32_t got = __hip_atomic_exchange(p, slot_bits(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (got == kSlotEmpty) return false;
-        v = __uint_as_float(got) + v;
-        __hip_atomic_store(p, kSlotEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t got = __hip_atomic_exchange(p, slot_word(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (got == 0u) return false;
+        v = __uint_as_float(got ^ kSlotKey) + v;
+        __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     return true;
 }

@@ -11,15 +11,18 @@ constexpr uint32_t kGroup = 64;
 constexpr uint32_t kTileRows = 32;
 constexpr uint32_t kTileBytes = 1088;
 
-// Exchange slots of two-chunk split-K launches: every word holds kSlotEmpty
-// (a signaling-NaN pattern) between launches; a partial with those bits is
-// sent as kSlotQuietNan.
-constexpr uint32_t kSlotEmpty = 0x7fa5a5a5u;
+// Exchange slots of two-chunk split-K launches: a partial sum p is stored as
+// bits(p) XOR kSlotKey, so every word is zero between launches and memory
+// that was zero-filled (a memset, a zero-initialised device array) is a valid
+// set of empty slots.  kSlotKey is a signaling-NaN pattern, which arithmetic
+// never produces; a partial with exactly those bits would store as zero, so
+// it is sent as kSlotQuietNan instead.
+constexpr uint32_t kSlotKey = 0x7fa5a5a5u;
 constexpr uint32_t kSlotQuietNan = 0x7fc00000u;
 
 // One GEMV launch.  gate != nullptr selects SwiGLU, add != nullptr the bias
 // epilogue.  split == 2 (gemv_kernel) reduces the two K chunks through
-// slots[rows (x2 with gate)], kSlotEmpty on entry and left so.  Other splits
+// slots[rows (x2 with gate)], zero on entry and left zero.  Other splits
 // > 1 reduce K chunks across workgroups through partial[split * rows (x2
 // with gate)] and counters[rows / 32], which must be zero on entry and are
 // left zero.
@@ -109,38 +112,9 @@ hipError_t launch_prep_batch(const PlanDesc *descs, const uint32_t *owner, uint3
                              hipStream_t stream);
 hipError_t launch_plan_batch(const PlanDesc *descs, uint32_t items, uint32_t n, uint32_t workgroups, uint32_t *sched,
                              hipStream_t stream);
-// A burst launch: up to kMaxBurst GEMVs that share one activation x of
-// `cols` floats, all of K = cols.  A unit is (GEMV, 64-row block, K chunk of
-// 16 * steps groups), one workgroup each, units numbered GEMV by GEMV from
-// unit_begin, block-major then chunk; `chunks` chunks per block.  With
-// gate != nullptr (every GEMV of a launch, or none) a unit streams the gate
-// tiles of its block too and the epilogue is SwiGLU.  With chunks == 2 the
-// two units of a row meet in slots[rows (x2 with gate)] (kSlotEmpty between
-// launches, left so); with more, the units of a block meet in
-// partial[stream][chunk][rows] through counters[block] (zero between
-// launches, left zero).
-constexpr uint32_t kMaxBurst = 8;
-constexpr uint32_t kBurstStepGroups = 16;  // groups of one 64-row workgroup step (four waves of four groups)
-struct BurstGemv {
-    const uint8_t *w;
-    const uint8_t *gate;
-    const float *add;
-    float *y;
-    float *partial;
-    uint32_t *counters;
-    uint32_t *slots;
-    uint32_t rows;
-    uint32_t unit_begin;
-};
-struct BurstArgs {
-    BurstGemv g[kMaxBurst];
-    const float *x;
-    uint32_t count, cols, chunks, units;
-};
-// steps = 1 or 2 (K chunk of 16 or 32 groups per unit).
-hipError_t launch_burst(const BurstArgs &args, uint32_t steps, hipStream_t stream);
+constexpr uint32_t kMaxGroup = 8;  // GEMVs of one group launch (Q4RDNA_MAX_GROUP)
 
-// A VALU group launch (gemv_kernel's arithmetic): up to kMaxBurst GEMVs
+// A VALU group launch (gemv_kernel's arithmetic): up to kMaxGroup GEMVs
 // sharing x of `cols` floats, the row tiles of all of them numbered GEMV by
 // GEMV from tile_begin (`tiles` in all), each split into `split` K chunks of
 // at most kGroupChunkGroups groups.  The chunks of a row tile meet as in
@@ -160,7 +134,7 @@ struct GemvGroupEntry {
     uint32_t tile_begin;
 };
 struct GemvGroupArgs {
-    GemvGroupEntry g[kMaxBurst];
+    GemvGroupEntry g[kMaxGroup];
     const float *x;
     uint32_t count, cols, split, tiles;
     uint32_t short_waves;  // 8 or 4, as GemvArgs::short_waves

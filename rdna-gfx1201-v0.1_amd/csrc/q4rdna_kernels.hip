@@ -393,7 +393,7 @@ __global__ __launch_bounds__(64 * W) void gemv_group_kernel(GemvGroupArgs a) {
     // the kernel-argument segment).
     GemvGroupEntry G = a.g[0];
 #pragma unroll
-    for (uint32_t i = 1; i < kMaxBurst; ++i)
+    for (uint32_t i = 1; i < kMaxGroup; ++i)
         if (i < a.count && gt >= a.g[i].tile_begin) G = a.g[i];
     const uint32_t rt = gt - G.tile_begin;
     const uint32_t g_begin = static_cast<uint32_t>((static_cast<uint64_t>(s) * groups) / split);

@@ -228,7 +228,6 @@ __device__ __forceinline__ uint32_t high_nibbles_x16(uint32_t t) { return t & 0x
 constexpr int kStepGroups = 4;                         // groups per wave step
 constexpr int kWgStepGroups = kWaves * kStepGroups;    // groups per workgroup step
 static_assert(kChunkGroups % kWgStepGroups == 0, "chunks are whole workgroup steps");
-static_assert(kBurstStepGroups == kWgStepGroups, "a burst step is one workgroup step");
 // LDS bytes per staged tile: 1024 + a 64-byte skew.  Over the 252-tensor
 // stack the 64-byte skew measures 10.2M SQ_LDS_BANK_CONFLICT cycles against
 // 23.7M for a 32- or 128-byte skew and 50.9M for none, at equal sweep time.
@@ -911,220 +910,6 @@ __global__ __launch_bounds__(64 * kBatchWaves) void plan_batch_kernel(const Plan
     }
 }
 
-// ---- burst kernel: one launch of a few GEMVs that share one x -------------
-//
-// For launches of a few MB (one projection, or q/k/v, gate/up of one layer),
-// where the sweep's separate prepare launch and per-item pipeline would cost
-// more than the bytes.  A unit is (GEMV, 64-row block, K chunk of 16*S
-// groups), one workgroup.  Each wave owns S steps of the sweep's geometry
-// (groups g0 + 4*wave .. +3 of the block's two row tiles, g0 = chunk start +
-// 16t) and issues every load of the unit at once, in straight-line code:
-// first its share of x, then the tiles of its S steps (and of the SwiGLU
-// gate) into registers, then the scales.  All are plain vector loads, which
-// complete in order, so waiting for x leaves the tiles in flight: the wave
-// converts its x groups into digits in its own LDS meanwhile, then restages
-// each step's tiles through LDS as it arrives and runs the sweep's MFMA
-// arithmetic on it.  (Loading the tiles straight into LDS instead makes the
-// compiler drain every load before the first use of x.)  The units of a
-// block meet in the split-K arrival chain when its rows span several chunks.
-template <int S, bool GLU>
-struct BurstShared {
-    static constexpr int kStreams = GLU ? 2 : 1;
-    // The stages, reused for the reduction once every wave has computed.
-    union {
-        uint8_t stage[kWaves][kStageBytes];
-        Red red;
-    };
-    uint8_t digits[kWaves][S * kStepGroups * kPrepBytes];
-    uint32_t last;
-};
-
-// A unit's end: the useful lanes publish their rows; thread t < 64 sums row
-// t's 16 (wave, group) partials in the fixed order.  One chunk: y = (sum +
-// add), times silu(gate sum) for SwiGLU.  Two: the row's sums meet in its
-// exchange slot and the second to arrive applies the epilogue.  More: the
-// sums (and gate sums) are published with device-scope stores, drained
-// before the block's arrival count, and the last unit of the block to
-// arrive sums the chunks in chunk order and applies the epilogue.
-template <bool GLU>
-__device__ __forceinline__ void burst_finish(Red &red, uint32_t &last, const BurstGemv &G, uint32_t block,
-                                             uint32_t chunk, uint32_t chunks, const float (&acc)[16],
-                                             const float (&gacc)[16], const LaneRole &ln, int wave) {
-    if (ln.useful) {
-        float *dst = &red[0][wave][ln.gB][32 * ln.T + 16 * ln.h];
-#pragma unroll
-        for (int n = 0; n < 16; ++n) dst[n] = acc[n];
-        if constexpr (GLU) {
-            float *gdst = &red[1][wave][ln.gB][32 * ln.T + 16 * ln.h];
-#pragma unroll
-            for (int n = 0; n < 16; ++n) gdst[n] = gacc[n];
-        }
-    }
-    __syncthreads();
-    const uint32_t row = block * kBlockRows + threadIdx.x;
-    const bool mine = threadIdx.x < kBlockRows && row < G.rows;
-    float v = 0.0f, gv = 0.0f;
-    if (threadIdx.x < kBlockRows) {
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w)
-#pragma unroll
-            for (int g = 0; g < kStepGroups; ++g) v += red[0][w][g][threadIdx.x];
-        if constexpr (GLU) {
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w)
-#pragma unroll
-                for (int g = 0; g < kStepGroups; ++g) gv += red[1][w][g][threadIdx.x];
-        }
-    }
-    if (chunks <= 2) {
-        if (mine && (chunks == 1 || exchange_pair<GLU>(G.slots, row, v, gv))) {
-            if (G.add != nullptr) v += ((gptr_cf32)G.add)[row];
-            if constexpr (GLU) v *= silu(gv);
-            *((gptr_f32)G.y + row) = v;
-        }
-        return;
-    }
-    if (mine) {
-        store_agent(&G.partial[static_cast<size_t>(chunk) * G.rows + row], v);
-        if constexpr (GLU) store_agent(&G.partial[static_cast<size_t>(chunks + chunk) * G.rows + row], gv);
-    }
-    wait_stores();
-    __syncthreads();
-    if (threadIdx.x == 0) last = (add_agent(&G.counters[block], 1u) == chunks - 1) ? 1u : 0u;
-    __syncthreads();
-    if (last == 0u) return;
-    if (mine) {
-        float u = load_agent(&G.partial[row]);
-        for (uint32_t k = 1; k < chunks; ++k) u += load_agent(&G.partial[static_cast<size_t>(k) * G.rows + row]);
-        if (G.add != nullptr) u += ((gptr_cf32)G.add)[row];
-        if constexpr (GLU) {
-            const float *gp = G.partial + static_cast<size_t>(chunks) * G.rows;
-            float g = load_agent(&gp[row]);
-            for (uint32_t k = 1; k < chunks; ++k) g += load_agent(&gp[static_cast<size_t>(k) * G.rows + row]);
-            u *= silu(g);
-        }
-        *((gptr_f32)G.y + row) = u;
-    }
-    if (threadIdx.x == 0) store_agent(&G.counters[block], 0u);
-}
-
-template <int S, bool GLU>
-__global__ __launch_bounds__(256) void burst_kernel(BurstArgs a) {
-    using Sh = BurstShared<S, GLU>;
-    constexpr int kStreams = Sh::kStreams;
-    __shared__ Sh sh;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const LaneRole ln = lane_role(lane);
-    const uint32_t u = xcd_remap(blockIdx.x, gridDim.x);
-    // The unit's GEMV (constant indices only, so the descriptors stay in
-    // the kernel-argument segment).
-    BurstGemv G = a.g[0];
-#pragma unroll
-    for (uint32_t i = 1; i < kMaxBurst; ++i)
-        if (i < a.count && u >= a.g[i].unit_begin) G = a.g[i];
-    const uint32_t local = u - G.unit_begin;
-    const uint32_t block = local / a.chunks, chunk = local - block * a.chunks;
-    const uint32_t groups = a.cols / kGroup;
-    const uint32_t g_begin = chunk * (kWgStepGroups * S);
-    const uint32_t g_end = min(groups, g_begin + kWgStepGroups * S);
-    const uint32_t tiles = G.rows / kTileRows;
-    const size_t row_tile_bytes = static_cast<size_t>(groups) * kTileBytes;
-    // The block's two row tiles; a second one past the last re-reads the
-    // last (its rows are never written).
-    const size_t second = 2 * block + 1 < tiles ? row_tile_bytes : 0;
-    const uint8_t *rt[kStreams][2];
-    rt[0][0] = G.w + static_cast<size_t>(2 * block) * row_tile_bytes;
-    rt[0][1] = rt[0][0] + second;
-    if constexpr (GLU) {
-        rt[kStreams - 1][0] = G.gate + static_cast<size_t>(2 * block) * row_tile_bytes;
-        rt[kStreams - 1][1] = rt[kStreams - 1][0] + second;
-    }
-    uint8_t *stage = sh.stage[wave];
-    uint8_t *digits = sh.digits[wave];
-
-    // 1. This wave's x: lane L < 16*S converts k-slot L%4 of group
-    // g0(t) + 4*wave + (L/4)%4 of step t = L/16.  Lanes without a group
-    // read the chunk's first group and discard it.
-    const int xt = lane >> 4, xp = (lane >> 2) & 3, xk = lane & 3;
-    const uint32_t xg = g_begin + kWgStepGroups * xt + kStepGroups * wave + xp;
-    const bool xhave = xt < S && xg < g_end;
-    float xs[16];
-    load_kslot_f32_always(a.x + static_cast<size_t>(xhave ? xg : g_begin) * kGroup, xk, xhave, xs);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // 2. Every tile of the wave's steps, then the scales, into registers:
-    // straight-line code, group indices past the chunk clamped to its last
-    // group (re-read, never used).
-    WaveRegs r[S][kStreams];
-#pragma unroll
-    for (int t = 0; t < S; ++t) {
-        const uint32_t g = g_begin + kWgStepGroups * t + kStepGroups * wave;
-#pragma unroll
-        for (int st = 0; st < kStreams; ++st)
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const uint32_t gc = min(g + (c >> 1), g_end - 1);
-                r[t][st].code[c] = __builtin_nontemporal_load(
-                    (gptr_i32x4)(rt[st][c & 1] + static_cast<size_t>(gc) * kTileBytes + 64 + 16 * lane));
-            }
-    }
-#pragma unroll
-    for (int t = 0; t < S; ++t) {
-        const uint32_t g = g_begin + kWgStepGroups * t + kStepGroups * wave;
-        const uint32_t gb = min(g + ln.gB, g_end - 1);
-#pragma unroll
-        for (int st = 0; st < kStreams; ++st) {
-            const uint8_t *own = rt[st][ln.T] + static_cast<size_t>(gb) * kTileBytes + 32 * ln.h;
-            r[t][st].sc[0] = __builtin_nontemporal_load((gptr_i32x4)own);
-            r[t][st].sc[1] = __builtin_nontemporal_load((gptr_i32x4)(own + 16));
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    // 3. Digits of the wave's groups into its own LDS (the layout of a prep
-    // record, kPrepBytes per group), while the tiles are in flight.
-    {
-        i32x4 rows[3];
-        bool bad;
-        int e;
-        kslot_digits(xs, xhave, rows, bad, e);
-        if (xhave) {
-            uint8_t *rec = digits + (xt * kStepGroups + xp) * kPrepBytes;
-#pragma unroll
-            for (int d = 0; d < 3; ++d) *reinterpret_cast<i32x4 *>(rec + 64 * xk + 16 * d) = rows[d];
-            if (xk == 0) *reinterpret_cast<float *>(rec + 256) = digit_factor(bad, e);
-        }
-    }
-    __builtin_amdgcn_wave_barrier();  // the digit writes of every lane precede the reads below (one wave's LDS ops run in order)
-
-    // 4. Each step as its tiles arrive: restaged through the wave's LDS
-    // stage, then the MFMA arithmetic.
-    float acc[16], gacc[16];
-#pragma unroll
-    for (int n = 0; n < 16; ++n) acc[n] = gacc[n] = 0.0f;
-#pragma unroll
-    for (int t = 0; t < S; ++t) {
-        const uint32_t g = g_begin + kWgStepGroups * t + kStepGroups * wave;
-        const bool valid = g + ln.kslot < g_end;
-        const uint8_t *rec = digits + t * kStepGroups * kPrepBytes;
-        const i32x4 av = *reinterpret_cast<const i32x4 *>(rec + ln.gB * kPrepBytes + ln.a_offset);
-        const float fv = *reinterpret_cast<const float *>(rec + ln.kslot * kPrepBytes + 256);
-#pragma unroll
-        for (int st = 0; st < kStreams; ++st) {
-            WaveRegs &q = r[t][st];
-            q.a = av;
-            q.f = fv;
-            restage(q, stage, ln, lane);
-            if (st == 0)
-                compute_wave_batched<true>(q, acc, valid);
-            else
-                compute_wave_batched<true>(q, gacc, valid);
-        }
-    }
-    __syncthreads();  // every stage read is done before the reduction reuses the stages
-    burst_finish<GLU>(sh.red, sh.last, G, block, chunk, a.chunks, acc, gacc, ln, wave);
-}
-
 }  // namespace
 
 hipError_t launch_prep(const float *const *group_x, uint8_t *prep, uint32_t groups, hipStream_t stream) {
@@ -1161,19 +946,6 @@ hipError_t launch_plan_batch(const PlanDesc *descs, uint32_t items, uint32_t n, 
         hipLaunchKernelGGL(plan_batch_kernel<1>, dim3(workgroups), block, 0, stream, descs, items, n, sched);
     else
         hipLaunchKernelGGL(plan_batch_kernel<2>, dim3(workgroups), block, 0, stream, descs, items, n, sched);
-    return hipGetLastError();
-}
-
-hipError_t launch_burst(const BurstArgs &args, uint32_t steps, hipStream_t stream) {
-    if (args.units == 0) return hipSuccess;
-    const bool glu = args.g[0].gate != nullptr;
-    const dim3 grid(args.units), block(256);
-    if (glu)
-        hipLaunchKernelGGL((burst_kernel<1, true>), grid, block, 0, stream, args);
-    else if (steps >= 2)
-        hipLaunchKernelGGL((burst_kernel<2, false>), grid, block, 0, stream, args);
-    else
-        hipLaunchKernelGGL((burst_kernel<1, false>), grid, block, 0, stream, args);
     return hipGetLastError();
 }
 

@@ -11,13 +11,15 @@
 // a GPU's copy comes from hipGetSymbolAddress with that GPU current, once per
 // GPU, and only that address is ever passed to a kernel.
 //
-// Counters must be zero and slots kSlotEmpty when a launch starts.  The first
-// call on a GPU sets both with a fill kernel on its stream, and every launch
-// leaves them so (the last workgroup to arrive at a row tile or 64-row block
-// resets its counter; the second chunk to reach a slot empties it).  Partial
-// sums need no clearing: every launch writes the ones it reads.  Every call
-// on a GPU shares that GPU's array, so calls that overlap on one GPU race:
-// issue them on one stream, or order them with events.
+// Counters and slots must be zero when a launch starts.  The array is a
+// zero-initialised device variable, so both hold from the moment the code
+// object is loaded, with no set-up launch (a first call captured into a graph
+// or made on any stream finds them ready), and every launch leaves them so
+// (the last workgroup to arrive at a row tile or 64-row block resets its
+// counter; the second chunk to reach a slot puts zero back).  Partial sums
+// need no clearing: every launch writes the ones it reads.  Every call on a
+// GPU shares that GPU's array, so calls that overlap on one GPU race: issue
+// them on one stream, or order them with events.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -37,22 +39,13 @@ static_assert(kPartialBytes % 256 == 0 && kCounterBytes % 256 == 0, "the counter
 
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
-// Counters to zero, slots to kSlotEmpty (a fill kernel, not a memset, so a
-// caller may capture the first call into a graph).
-__global__ __launch_bounds__(256) void init_scratch(uint32_t *__restrict__ counters, uint32_t *__restrict__ slots) {
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < Q4RDNA_NOALLOC_COUNTERS; i += gridDim.x * blockDim.x)
-        counters[i] = 0u;
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < Q4RDNA_NOALLOC_SLOTS; i += gridDim.x * blockDim.x)
-        slots[i] = q4rdna::kSlotEmpty;
-}
-
 // Device address of each GPU's copy of `scratch`, looked up on the first
 // call on that GPU (a fixed table: nothing is allocated).
 constexpr int kMaxDevices = 64;
 std::atomic<uint8_t *> g_scratch[kMaxDevices];
 std::mutex g_setup;
 
-int scratch_of(int device, hipStream_t stream, uint8_t **out) {
+int scratch_of(int device, uint8_t **out) {
     if (device < 0 || device >= kMaxDevices)
         return q4rdna::set_error(Q4RDNA_ERR_ARGUMENT, "device %d is outside the no-alloc table", device);
     uint8_t *p = g_scratch[device].load(std::memory_order_acquire);
@@ -65,11 +58,6 @@ int scratch_of(int device, hipStream_t stream, uint8_t **out) {
             hipError_t e = hipGetSymbolAddress(reinterpret_cast<void **>(&p), HIP_SYMBOL(scratch));
             if (e != hipSuccess || p == nullptr)
                 return q4rdna::set_error(Q4RDNA_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
-            hipLaunchKernelGGL(init_scratch, dim3(256), dim3(256), 0, stream,
-                               reinterpret_cast<uint32_t *>(p + kPartialBytes),
-                               reinterpret_cast<uint32_t *>(p + kPartialBytes + kCounterBytes));
-            e = hipGetLastError();
-            if (e != hipSuccess) return q4rdna::set_error(Q4RDNA_ERR_HIP, "scratch set-up: %s", hipGetErrorString(e));
             g_scratch[device].store(p, std::memory_order_release);
         }
     }
@@ -99,7 +87,7 @@ extern "C" int q4rdna_mul_mat_ex_noalloc(const q4rdna_weight *w, const q4rdna_we
                                  static_cast<unsigned>(Q4RDNA_NOALLOC_COUNTERS),
                                  static_cast<unsigned>(Q4RDNA_NOALLOC_SLOTS));
     uint8_t *base = nullptr;
-    if ((rc = scratch_of(w->device, s, &base)) != Q4RDNA_OK) return rc;
+    if ((rc = scratch_of(w->device, &base)) != Q4RDNA_OK) return rc;
     return q4rdna::launch_tensor_in(L, w, gt, x, add, y, reinterpret_cast<float *>(base),
                                     reinterpret_cast<uint32_t *>(base + kPartialBytes),
                                     reinterpret_cast<uint32_t *>(base + kPartialBytes + kCounterBytes), s);

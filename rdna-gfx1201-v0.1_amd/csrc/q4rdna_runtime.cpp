@@ -112,7 +112,7 @@ int parse_index(const uint8_t *image, uint64_t image_size, uint64_t file_size, F
 
 // Split-K scratch per (device, stream): partial sums, per-row-tile arrival
 // counters (kept zero between launches by the kernels) and two-chunk
-// exchange slots (kept kSlotEmpty between launches by the kernel).
+// exchange slots (kept zero between launches by the kernel).
 struct Workspace {
     float *partial = nullptr;
     uint32_t *counters = nullptr;
@@ -158,7 +158,7 @@ int get_workspace(int device, hipStream_t stream, size_t partial_floats, size_t 
         // Set once, complete before any launch uses them (launches on
         // non-blocking streams are not ordered after the null stream).
         if (cc > 0) e = hipMemset(c, 0, cc * sizeof(uint32_t));
-        if (e == hipSuccess && sc > 0) e = hipMemsetD32(reinterpret_cast<hipDeviceptr_t>(sl), static_cast<int>(q4rdna::kSlotEmpty), sc);
+        if (e == hipSuccess && sc > 0) e = hipMemset(sl, 0, sc * sizeof(uint32_t));
         if (e == hipSuccess) e = hipDeviceSynchronize();
         if (e != hipSuccess) {
             (void)hipFree(p);
@@ -223,35 +223,14 @@ int check_io(const float *x, const float *y) {
     return Q4RDNA_OK;
 }
 
-}  // namespace
-
-namespace {
-
-// Burst units of 16 * steps groups.  Two steps (half the units, half the
-// split-K arrivals) when one-step units would oversubscribe the CUs
-// moderately; one step when they fit one per CU, or when there are so many
-// that every CU runs several waves of them anyway.  Measured on MI355X
-// (graph replays): q/k/v of a layer in one group 7.9 against 8.4 us,
-// 4096x12288 12.0 against 13.0; 4096x4096 alone 6.9 against 7.4,
-// 1024x4096 6.3 against 7.1, 151936x4096 69 against 74.
-uint32_t burst_steps_policy(uint64_t blocks, uint32_t groups, uint32_t cus) {
-    const uint64_t units1 = blocks * ((groups + q4rdna::kBurstStepGroups - 1) / q4rdna::kBurstStepGroups);
-    return units1 > cus && units1 <= 8ull * cus && groups > q4rdna::kBurstStepGroups ? 2u : 1u;
-}
-
-uint32_t burst_chunks(uint32_t groups, uint32_t steps) {
-    const uint32_t chunk = q4rdna::kBurstStepGroups * steps;
-    return (groups + chunk - 1) / chunk;
-}
-
-uint32_t blocks_of(uint32_t rows) { return (rows + q4rdna::kBlockRows - 1) / q4rdna::kBlockRows; }
-
-// Which kernel serves a per-tensor launch when the caller leaves it to the
-// policy.
-uint32_t tensor_kernel_policy(const q4rdna_weight *w, bool gate) {
-    (void)w;
-    (void)gate;
-    return Q4RDNA_KERNEL_VALU;
+// Launch options beyond split_k: the kernel is the VALU kernel (0 = the
+// policy, which is that kernel) and the reserved words are zero.
+int check_options(const q4rdna_launch_options *options) {
+    if (options == nullptr) return Q4RDNA_OK;
+    if (options->kernel > Q4RDNA_KERNEL_VALU) return set_error(Q4RDNA_ERR_ARGUMENT, "unknown kernel %u", options->kernel);
+    for (uint32_t r : options->reserved)
+        if (r != 0) return set_error(Q4RDNA_ERR_ARGUMENT, "reserved launch options must be zero");
+    return Q4RDNA_OK;
 }
 
 }  // namespace
@@ -271,32 +250,14 @@ int check_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const fl
     if (add != nullptr && !aligned(add, 4)) return set_error(Q4RDNA_ERR_ARGUMENT, "misaligned add");
     const uint32_t s = options ? options->split_k : 0;
     if (s > kMaxSplit) return set_error(Q4RDNA_ERR_ARGUMENT, "split_k %u exceeds %u", s, kMaxSplit);
-    uint32_t kernel = options ? options->kernel : Q4RDNA_KERNEL_POLICY;
-    const uint32_t steps = options ? options->burst_steps : 0;
-    if (kernel > Q4RDNA_KERNEL_BURST) return set_error(Q4RDNA_ERR_ARGUMENT, "unknown kernel %u", kernel);
-    if (steps > 2) return set_error(Q4RDNA_ERR_ARGUMENT, "burst_steps %u is outside 0..2", steps);
-    // An explicit split names the VALU kernel's factor.
-    if (kernel == Q4RDNA_KERNEL_POLICY) kernel = s != 0 ? Q4RDNA_KERNEL_VALU : tensor_kernel_policy(w, gate != nullptr);
+    if ((rc = check_options(options)) != Q4RDNA_OK) return rc;
     TensorLaunch L{};
-    L.kernel = kernel;
-    const uint32_t groups = w->columns / kGroup;
-    if (kernel == Q4RDNA_KERNEL_VALU) {
-        L.split = resolve_split(w, s);
-        if (L.split == 2) {
-            L.slots = static_cast<size_t>(w->rows) * (gate ? 2 : 1);
-        } else if (L.split > 2) {
-            L.partial_floats = static_cast<size_t>(L.split) * w->rows * (gate ? 2 : 1);
-            L.counters = w->rows / kTileRows;
-        }
-    } else {
-        L.steps = gate != nullptr ? 1u : (steps != 0 ? steps : burst_steps_policy(blocks_of(w->rows), groups, cu_count(w->device)));
-        L.chunks = burst_chunks(groups, L.steps);
-        if (L.chunks == 2) {
-            L.slots = static_cast<size_t>(w->rows) * (gate ? 2 : 1);
-        } else if (L.chunks > 2) {
-            L.partial_floats = static_cast<size_t>(L.chunks) * w->rows * (gate ? 2 : 1);
-            L.counters = blocks_of(w->rows);
-        }
+    L.split = resolve_split(w, s);
+    if (L.split == 2) {
+        L.slots = static_cast<size_t>(w->rows) * (gate ? 2 : 1);
+    } else if (L.split > 2) {
+        L.partial_floats = static_cast<size_t>(L.split) * w->rows * (gate ? 2 : 1);
+        L.counters = w->rows / kTileRows;
     }
     *launch = L;
     return Q4RDNA_OK;
@@ -305,40 +266,28 @@ int check_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const fl
 int launch_tensor_in(const TensorLaunch &launch, const q4rdna_weight *w, const uint8_t *gate, const float *x,
                      const float *add, float *y, float *partial, uint32_t *counters, uint32_t *slots,
                      hipStream_t stream) {
-    hipError_t e;
-    if (launch.kernel == Q4RDNA_KERNEL_BURST) {
-        BurstArgs args{};
-        args.g[0] = BurstGemv{w->tiles, gate, add, y, partial, counters, slots, w->rows, 0};
-        args.x = x;
-        args.count = 1;
-        args.cols = w->columns;
-        args.chunks = launch.chunks;
-        args.units = blocks_of(w->rows) * launch.chunks;
-        e = launch_burst(args, launch.steps, stream);
-    } else {
-        GemvArgs args{};
-        args.w = w->tiles;
-        args.gate = gate;
-        args.x = x;
-        args.add = add;
-        args.y = y;
-        args.rows = w->rows;
-        args.cols = w->columns;
-        args.split = launch.split;
-        // Eight waves per workgroup while the launch is latency-bound (at
-        // most four workgroups per CU); with more, four waves of up to 16
-        // tiles keep more bytes in flight per CU (151936x4096: 60 us
-        // against 68).
-        const uint64_t workgroups = static_cast<uint64_t>(w->rows / kTileRows) * launch.split;
-        args.short_waves = workgroups <= 4ull * cu_count(w->device) ? 8u : 4u;
-        if (launch.split == 2) {
-            args.slots = slots;
-        } else if (launch.split > 2) {
-            args.partial = partial;
-            args.counters = counters;
-        }
-        e = launch_gemv(args, stream);
+    GemvArgs args{};
+    args.w = w->tiles;
+    args.gate = gate;
+    args.x = x;
+    args.add = add;
+    args.y = y;
+    args.rows = w->rows;
+    args.cols = w->columns;
+    args.split = launch.split;
+    // Eight waves per workgroup while the launch is latency-bound (at
+    // most four workgroups per CU); with more, four waves of up to 16
+    // tiles keep more bytes in flight per CU (151936x4096: 60 us
+    // against 68).
+    const uint64_t workgroups = static_cast<uint64_t>(w->rows / kTileRows) * launch.split;
+    args.short_waves = workgroups <= 4ull * cu_count(w->device) ? 8u : 4u;
+    if (launch.split == 2) {
+        args.slots = slots;
+    } else if (launch.split > 2) {
+        args.partial = partial;
+        args.counters = counters;
     }
+    const hipError_t e = launch_gemv(args, stream);
     if (e != hipSuccess) return hip_fail(e, "GEMV launch");
     return Q4RDNA_OK;
 }
@@ -686,7 +635,6 @@ int q4rdna_mul_mat_group(const q4rdna_group_desc *descs, uint32_t count, const f
     if (x == nullptr || !aligned(x, 4)) return set_error(Q4RDNA_ERR_ARGUMENT, "NULL or misaligned activation");
     const bool glu = descs[0].gate_tiles != nullptr;
     int rc;
-    uint64_t blocks = 0;
     for (uint32_t i = 0; i < count; ++i) {
         const q4rdna_group_desc &d = descs[i];
         if ((rc = check_weight(&d.weight)) != Q4RDNA_OK) return rc;
@@ -701,68 +649,26 @@ int q4rdna_mul_mat_group(const q4rdna_group_desc *descs, uint32_t count, const f
         const uintptr_t y0 = reinterpret_cast<uintptr_t>(d.y), y1 = y0 + 4ull * d.weight.rows;
         const uintptr_t x0 = reinterpret_cast<uintptr_t>(x), x1 = x0 + 4ull * d.weight.columns;
         if (y0 < x1 && x0 < y1) return set_error(Q4RDNA_ERR_ARGUMENT, "descriptor %u: y overlaps x", i);
-        blocks += blocks_of(d.weight.rows);
     }
-    const uint32_t groups = descs[0].weight.columns / kGroup;
-    uint32_t steps = options ? options->burst_steps : 0;
-    if (steps > 2) return set_error(Q4RDNA_ERR_ARGUMENT, "burst_steps %u is outside 0..2", steps);
+    // Workgroups of different GEMVs run unordered: an output may not overlap
+    // another GEMV's output or bias.
+    for (uint32_t i = 0; i < count; ++i) {
+        const uintptr_t a0 = reinterpret_cast<uintptr_t>(descs[i].y), a1 = a0 + 4ull * descs[i].weight.rows;
+        for (uint32_t j = 0; j < count; ++j) {
+            if (j == i) continue;
+            const uintptr_t b0 = reinterpret_cast<uintptr_t>(descs[j].y), b1 = b0 + 4ull * descs[j].weight.rows;
+            if (a0 < b1 && b0 < a1) return set_error(Q4RDNA_ERR_ARGUMENT, "descriptors %u and %u: outputs overlap", i, j);
+            if (descs[j].add != nullptr) {
+                const uintptr_t c0 = reinterpret_cast<uintptr_t>(descs[j].add), c1 = c0 + 4ull * descs[j].weight.rows;
+                if (a0 < c1 && c0 < a1)
+                    return set_error(Q4RDNA_ERR_ARGUMENT, "descriptor %u: y overlaps descriptor %u's add", i, j);
+            }
+        }
+    }
     const uint32_t split_k = options ? options->split_k : 0;
     if (split_k > kMaxSplit) return set_error(Q4RDNA_ERR_ARGUMENT, "split_k %u exceeds %u", split_k, kMaxSplit);
-    uint32_t kernel = options ? options->kernel : Q4RDNA_KERNEL_POLICY;
-    if (kernel > Q4RDNA_KERNEL_BURST) return set_error(Q4RDNA_ERR_ARGUMENT, "unknown kernel %u", kernel);
-    // The policy: the VALU kernel (faster on every projection shape measured,
-    // alone or grouped) unless K needs more chunks than it splits into;
-    // burst_steps names the burst kernel, split_k the VALU kernel.
-    if (kernel == Q4RDNA_KERNEL_POLICY)
-        kernel = steps != 0 || groups > kGroupChunkGroups * kMaxSplit ? Q4RDNA_KERNEL_BURST : Q4RDNA_KERNEL_VALU;
-    if (kernel == Q4RDNA_KERNEL_VALU)
-        return launch_group_valu(descs, count, x, glu, split_k, static_cast<hipStream_t>(stream));
-    if (glu) steps = 1;
-    if (steps == 0) steps = burst_steps_policy(blocks, groups, cu_count(descs[0].weight.device));
-    const uint32_t chunks = burst_chunks(groups, steps);
-    if (blocks * chunks > 0x7fffffffull) return set_error(Q4RDNA_ERR_ARGUMENT, "group too large");
-    const uint32_t streams = glu ? 2u : 1u;
-    // Two chunks meet in exchange slots (rows x streams words per GEMV),
-    // more in partials and arrival counters.
-    size_t partial_floats = 0, counters = 0, slots = 0;
-    for (uint32_t i = 0; i < count; ++i) {
-        if (chunks == 2) {
-            slots += static_cast<size_t>(streams) * descs[i].weight.rows;
-        } else if (chunks > 2) {
-            partial_floats += static_cast<size_t>(chunks) * streams * descs[i].weight.rows;
-            counters += blocks_of(descs[i].weight.rows);
-        }
-    }
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    Workspace *ws = nullptr;
-    if (chunks > 1 &&
-        (rc = get_workspace(descs[0].weight.device, s, partial_floats, counters, slots, &ws)) != Q4RDNA_OK)
-        return rc;
-    q4rdna::BurstArgs args{};
-    args.x = x;
-    args.count = count;
-    args.cols = descs[0].weight.columns;
-    args.chunks = chunks;
-    uint32_t units = 0;
-    size_t poff = 0, coff = 0, soff = 0;
-    for (uint32_t i = 0; i < count; ++i) {
-        const q4rdna_group_desc &d = descs[i];
-        args.g[i] = q4rdna::BurstGemv{d.weight.tiles, d.gate_tiles, d.add, d.y,
-                                      chunks > 2 ? ws->partial + poff : nullptr,
-                                      chunks > 2 ? ws->counters + coff : nullptr,
-                                      chunks == 2 ? ws->slots + soff : nullptr, d.weight.rows, units};
-        units += blocks_of(d.weight.rows) * chunks;
-        if (chunks == 2) {
-            soff += static_cast<size_t>(streams) * d.weight.rows;
-        } else if (chunks > 2) {
-            poff += static_cast<size_t>(chunks) * streams * d.weight.rows;
-            coff += blocks_of(d.weight.rows);
-        }
-    }
-    args.units = units;
-    hipError_t e = q4rdna::launch_burst(args, steps, s);
-    if (e != hipSuccess) return hip_fail(e, "group GEMV launch");
-    return Q4RDNA_OK;
+    if ((rc = check_options(options)) != Q4RDNA_OK) return rc;
+    return launch_group_valu(descs, count, x, glu, split_k, static_cast<hipStream_t>(stream));
 }
 
 int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x, uint32_t n,

@@ -13,17 +13,12 @@ namespace q4rdna {
 // Record `fmt` as the calling thread's last error; returns `code`.
 int set_error(int code, const char *fmt, ...);
 
-// How a per-tensor GEMV launches: the kernel (Q4RDNA_KERNEL_VALU or
-// Q4RDNA_KERNEL_BURST), the VALU kernel's split-K factor or the burst
-// kernel's steps per unit and chunks per block, and the workspace it needs:
-// exchange slots (words, kSlotEmpty between launches) for the VALU kernel at
-// split 2, else fp32 partials and arrival counters; none when the K
-// dimension is not split.
+// How a per-tensor GEMV launches: the VALU kernel's split-K factor and the
+// workspace it needs: exchange slots (words, zero between launches) at split
+// 2, else fp32 partials and arrival counters; none when the K dimension is
+// not split.
 struct TensorLaunch {
-    uint32_t kernel;
     uint32_t split;
-    uint32_t steps;
-    uint32_t chunks;
     size_t partial_floats;
     size_t counters;
     size_t slots;
@@ -37,7 +32,7 @@ int check_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const fl
 // Launch a validated per-tensor GEMV with a caller-provided workspace of at
 // least launch.partial_floats floats, launch.counters counters and
 // launch.slots slot words (each ignored when its count is zero); counters
-// zero on entry and slots kSlotEmpty, both left so.
+// and slots zero on entry, both left zero.
 int launch_tensor_in(const TensorLaunch &launch, const q4rdna_weight *w, const uint8_t *gate, const float *x,
                      const float *add, float *y, float *partial, uint32_t *counters, uint32_t *slots,
                      hipStream_t stream);

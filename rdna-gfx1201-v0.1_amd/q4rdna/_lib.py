@@ -63,13 +63,11 @@ class Weight(ctypes.Structure):
 
 KERNEL_POLICY = 0
 KERNEL_VALU = 1
-KERNEL_BURST = 2
 MAX_GROUP = 8
 
 
 class LaunchOptions(ctypes.Structure):
-    _fields_ = [("split_k", ctypes.c_uint32), ("kernel", ctypes.c_uint32), ("burst_steps", ctypes.c_uint32),
-                ("reserved", ctypes.c_uint32 * 5)]
+    _fields_ = [("split_k", ctypes.c_uint32), ("kernel", ctypes.c_uint32), ("reserved", ctypes.c_uint32 * 6)]
 
 
 class GroupDesc(ctypes.Structure):

@@ -129,10 +129,9 @@ def mul_mat_glu(up: QWeight, gate: QWeight, x: torch.Tensor, y: torch.Tensor | N
 
 def mul_mat_ex(w: QWeight, x: torch.Tensor, y: torch.Tensor, gate: QWeight | None = None,
                add: torch.Tensor | None = None, split_k: int = 0, stream: int | None = None,
-               kernel: int = _lib.KERNEL_POLICY, burst_steps: int = 0) -> bool:
-    """GEMV with explicit launch options: split_k for the VALU kernel (0 =
-    the shape policy), kernel (KERNEL_VALU / KERNEL_BURST, 0 = the policy),
-    burst_steps (1 or 2, 0 = the policy)."""
+               kernel: int = _lib.KERNEL_POLICY) -> bool:
+    """GEMV with explicit launch options: split_k (0 = the shape policy),
+    kernel (KERNEL_VALU, or 0 = the policy, which is that kernel)."""
     _f32_buf(x, "x", w.cols, w.device)
     _f32_buf(y, "y", w.rows, w.device)
     if add is not None:
@@ -142,7 +141,6 @@ def mul_mat_ex(w: QWeight, x: torch.Tensor, y: torch.Tensor, gate: QWeight | Non
     opts = LaunchOptions()
     opts.split_k = split_k
     opts.kernel = kernel
-    opts.burst_steps = burst_steps
     s = _stream(x.device) if stream is None else stream
     return check(load().q4rdna_mul_mat_ex(ctypes.byref(w.raw), ctypes.byref(gate.raw) if gate else None,
                                           x.data_ptr(), _ptr(add), y.data_ptr(), ctypes.byref(opts), s))
@@ -171,13 +169,12 @@ def mul_mat_batch(w: QWeight, x: torch.Tensor, y: torch.Tensor, gate: QWeight | 
                                              ctypes.byref(opts), s))
 
 
-def mul_mat_group(items: Sequence[tuple], x: torch.Tensor, burst_steps: int = 0, stream: int | None = None,
+def mul_mat_group(items: Sequence[tuple], x: torch.Tensor, stream: int | None = None,
                   kernel: int = _lib.KERNEL_POLICY, split_k: int = 0) -> bool:
     """GEMVs sharing one activation x in one launch.  items: (weight, y) or
     (weight, y, gate_weight_or_None, add_or_None); every weight has
-    x.numel() columns.  kernel: KERNEL_VALU (split_k applies, 0 = the
-    policy) or KERNEL_BURST (burst_steps applies); 0 = the policy.  Returns
-    False when not applicable."""
+    x.numel() columns.  split_k: 0 = the shape policy for the group's total
+    rows.  Returns False when not applicable."""
     if not 1 <= len(items) <= _lib.MAX_GROUP:
         raise ValueError(f"a group holds 1..{_lib.MAX_GROUP} GEMVs")
     descs = (_lib.GroupDesc * len(items))()
@@ -196,7 +193,6 @@ def mul_mat_group(items: Sequence[tuple], x: torch.Tensor, burst_steps: int = 0,
         descs[i].add = _ptr(add)
         descs[i].y = y.data_ptr()
     opts = LaunchOptions()
-    opts.burst_steps = burst_steps
     opts.kernel = kernel
     opts.split_k = split_k
     s = _stream(x.device) if stream is None else stream
@@ -215,6 +211,14 @@ def pack(w: torch.Tensor, algorithm: int = ALGO_SIDECAR, out: torch.Tensor | Non
     rows, cols = w.shape
     if out is None:
         out = torch.empty(packed_size(rows, cols), dtype=torch.uint8, device=w.device)
+    # The library sees only out's address: a short, mistyped or misplaced
+    # buffer would be written past its end on the GPU.
+    if out.dtype != torch.uint8 or not out.is_cuda or not out.is_contiguous():
+        raise ValueError("out must be a contiguous uint8 CUDA tensor")
+    if out.numel() != packed_size(rows, cols):
+        raise ValueError(f"out holds {out.numel()} bytes, {rows}x{cols} packs into {packed_size(rows, cols)}")
+    if out.device != w.device:
+        raise ValueError(f"out lives on {out.device}, w on {w.device}")
     s = _stream(w.device) if stream is None else stream
     check(load().q4rdna_pack(w.data_ptr(), rows, cols, algorithm, out.data_ptr(), s))
     return out

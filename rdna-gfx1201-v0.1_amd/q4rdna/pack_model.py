@@ -6,9 +6,15 @@ each decoder layer, in layer-major order, named by their ggml names, read
 from the shards that model.safetensors.index.json lists.  Quantization runs
 on the GPU through q4rdna_pack with the sidecar scale search, which is
 bit-identical to the reference's native packer
-(source/q4rdna_sidecar_pack.cpp:126-179); the reference's Python packer runs
-the same search with torch float32 reductions, so the two agree except for
-rare summation-order ties.
+(source/q4rdna_sidecar_pack.cpp:126-179).  The reference's Python packer
+runs the same search with torch float32 reductions and an exact fp16 decode,
+so the two write different bytes for a few groups: where a scale and its
+negation tie exactly (a group with symmetric extremes), where two adjacent
+fp16 scales tie to float32 rounding (the summation orders rank them
+differently), where a scale is an fp16 subnormal (the native search decodes
+it at half its value), where the Python search overflows to an infinite
+scale, and in the sign of a zero scale.  On N(0, 0.02) bf16 weights the
+first two kinds are 24 of 262,144 groups.
 
     python -m q4rdna.pack_model --model DIR --output FILE [--layers N] [--max-tensors K]
 """

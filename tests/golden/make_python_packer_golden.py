@@ -78,6 +78,9 @@ def differing_groups(a: np.ndarray, b: np.ndarray, rows: int, cols: int) -> np.n
 
 
 def main() -> int:
+    # The reference tree is read-only to this script: no bytecode cache is
+    # written next to the module it imports.
+    sys.dont_write_bytecode = True
     sys.path.insert(0, REFERENCE_SOURCE)
     from pack_q4rdna_sidecar import pack_tensor  # the reference's canonical packer
 

@@ -1,9 +1,10 @@
 """Two-chunk split-K in the per-tensor VALU kernel: at split 2 the two K
-chunks of a row meet in an exchange slot that every launch must leave empty.
+chunks of a row meet in an exchange slot that every launch must leave empty
+(all-zero memory; a partial is stored XOR a signaling-NaN key).
 Launches of both slot layouts (one word per row; a (sum, SwiGLU gate sum)
 pair per row) alternate on one stream over the same slots: every result is
 bit-identical from round to round and within both parity bars.  NaN partials,
-including the slots' own signaling-NaN pattern fed in as an activation, still
+including the slots' own signaling-NaN key fed in as an activation, still
 finish every row, and the launches after them are unaffected."""
 import numpy as np
 import pytest
@@ -15,7 +16,7 @@ from conftest import assert_gemv_parity
 
 pytestmark = pytest.mark.gpu
 
-SLOT_EMPTY = 0x7FA5A5A5  # the kernel's empty-slot pattern (a signaling NaN)
+SLOT_KEY = 0x7FA5A5A5  # the kernel's slot key (a signaling NaN); a partial with these bits would store as zero
 
 
 def random_tiles(rows: int, cols: int, seed: int) -> np.ndarray:
@@ -76,7 +77,7 @@ def test_split2_slot_layouts_alternate_on_one_stream(cuda):
 @pytest.mark.parametrize("gated", [False, True])
 @pytest.mark.parametrize("chunk", [0, 1])
 def test_split2_nan_partials_finish_every_row(cuda, gated, chunk):
-    """An activation in chunk `chunk` set to the empty-slot bit pattern makes
+    """An activation in chunk `chunk` set to the slot key's bit pattern makes
     that chunk's partial of every row NaN: every row still gets written (NaN),
     and a clean launch right after on the same stream is exact again."""
     rows, cols = 4096, 4096
@@ -84,7 +85,7 @@ def test_split2_nan_partials_finish_every_row(cuda, gated, chunk):
     gt, g = weight(rows, cols, 401) if gated else (None, None)
     x_np = O.gaussian_x(cols, 402)
     bad = x_np.copy()
-    bad.view(np.uint32)[chunk * (cols // 2) + 5] = SLOT_EMPTY
+    bad.view(np.uint32)[chunk * (cols // 2) + 5] = SLOT_KEY
     st = torch.cuda.Stream()
     y_bad = torch.full((rows,), 7.0, device="cuda")
     y = torch.full((rows,), 7.0, device="cuda")

@@ -147,27 +147,85 @@ def test_valu_group_replays_from_a_hip_graph(cuda):
 
 
 def test_valu_group_options(cuda):
-    """An explicit kernel choice is honoured; unknown kernels and oversize
+    """An explicit VALU kernel equals the policy; unknown kernels (2, the
+    withdrawn burst kernel, and 3), nonzero reserved words and oversize
     splits are argument errors that launch nothing."""
     L = q4rdna.load()
     cols = 4096
     _, w = weight(1024, cols, 760)
     x = torch.from_numpy(O.gaussian_x(cols, 761)).cuda()
     y_valu = torch.empty(1024, device="cuda")
-    y_burst = torch.empty(1024, device="cuda")
+    y_policy = torch.empty(1024, device="cuda")
     assert api.mul_mat_group([(w, y_valu)], x, kernel=_lib.KERNEL_VALU)
-    assert api.mul_mat_group([(w, y_burst)], x, kernel=_lib.KERNEL_BURST)
+    assert api.mul_mat_group([(w, y_policy)], x)
     torch.cuda.synchronize()
-    assert not torch.equal(y_valu, y_burst)  # different arithmetic, both within parity (checked above)
+    assert torch.equal(y_valu, y_policy)
     arr = (_lib.GroupDesc * 1)()
     arr[0].weight = w.raw
     arr[0].y = y_valu.data_ptr()
-    for kernel, split in ((3, 0), (_lib.KERNEL_VALU, 65)):
+    for kernel, split, reserved in ((2, 0, 0), (3, 0, 0), (_lib.KERNEL_VALU, 65, 0), (0, 0, 1)):
         o = _lib.LaunchOptions()
         o.kernel = kernel
         o.split_k = split
+        o.reserved[0] = reserved
         y_valu.fill_(7.0)
         rc = L.q4rdna_mul_mat_group(arr, 1, x.data_ptr(), cols, ctypes.byref(o), torch.cuda.current_stream().cuda_stream)
-        assert rc == q4rdna.ERR_ARGUMENT, (kernel, split)
+        assert rc == q4rdna.ERR_ARGUMENT, (kernel, split, reserved)
         torch.cuda.synchronize()
         assert (y_valu == 7.0).all()
+        y1 = torch.full((1024,), 7.0, device="cuda")
+        rc = L.q4rdna_mul_mat_ex(ctypes.byref(w.raw), None, x.data_ptr(), None, y1.data_ptr(), ctypes.byref(o),
+                                 torch.cuda.current_stream().cuda_stream)
+        assert rc == q4rdna.ERR_ARGUMENT, (kernel, split, reserved)
+        torch.cuda.synchronize()
+        assert (y1 == 7.0).all()
+
+
+def test_valu_group_rejects_overlapping_outputs(cuda):
+    """Members run unordered, so an output overlapping another member's
+    output or bias is an argument error, and nothing is launched; the same
+    buffers without overlap run."""
+    L = q4rdna.load()
+    cols = 4096
+    _, w = weight(256, cols, 770)
+    x = torch.from_numpy(O.gaussian_x(cols, 771)).cuda()
+    buf = torch.full((1024,), 7.0, device="cuda")
+    add = torch.zeros(256, device="cuda")
+
+    def run(y0, y1, add1):
+        arr = (_lib.GroupDesc * 2)()
+        for i, (y, a) in enumerate(((y0, None), (y1, add1))):
+            arr[i].weight = w.raw
+            arr[i].y = y.data_ptr()
+            arr[i].add = None if a is None else a.data_ptr()
+        return L.q4rdna_mul_mat_group(arr, 2, x.data_ptr(), cols, None, torch.cuda.current_stream().cuda_stream)
+
+    assert run(buf[0:256], buf[128:384], None) == q4rdna.ERR_ARGUMENT          # outputs overlap
+    assert "overlap" in q4rdna.last_error()
+    assert run(buf[0:256], buf[512:768], buf[200:456]) == q4rdna.ERR_ARGUMENT  # y0 overlaps member 1's add
+    torch.cuda.synchronize()
+    assert (buf == 7.0).all()
+    assert run(buf[0:256], buf[256:512], add) == q4rdna.OK
+    torch.cuda.synchronize()
+    assert torch.equal(buf[0:256], buf[256:512])
+
+
+def test_valu_group_past_the_eight_wave_threshold(cuda):
+    """Two gate-projection-shaped members at split 2 make 1,536 workgroups,
+    more than four per CU, so the group runs four-wave workgroups while a
+    single 12288 x 4096 launch at split 2 (768) runs eight: the outputs may
+    differ from q4rdna_mul_mat_ex in the last bits, and both meet the bars."""
+    rows, cols = 12288, 4096
+    assert 2 * (2 * rows // 32) > 4 * torch.cuda.get_device_properties(0).multi_processor_count
+    t1, w1 = weight(rows, cols, 780)
+    t2, w2 = weight(rows, cols, 781)
+    x_np = O.gaussian_x(cols, 782)
+    x = torch.from_numpy(x_np).cuda()
+    ys = [torch.full((rows,), float("nan"), device="cuda") for _ in range(2)]
+    assert api.mul_mat_group([(w1, ys[0]), (w2, ys[1])], x, split_k=2)
+    r = torch.full((rows,), float("nan"), device="cuda")
+    assert api.mul_mat_ex(w1, x, r, split_k=2)
+    torch.cuda.synchronize()
+    for t, y in ((t1, ys[0]), (t2, ys[1])):
+        assert_gemv_parity(y.cpu().numpy(), t, rows, cols, x_np, label="group of two")
+    assert_gemv_parity(r.cpu().numpy(), t1, rows, cols, x_np, label="single")

@@ -177,6 +177,93 @@ def test_full_stack_216_swiglu_plan(cuda, stack):
     plan.close()
 
 
+def rms_norm(x: torch.Tensor, out: torch.Tensor) -> None:
+    """A decoder's RMS normalization without a weight (eps 1e-6), written
+    into a fixed buffer; it keeps the chain's activations O(1)."""
+    out.copy_(torch.nn.functional.rms_norm(x, (x.numel(),), eps=1e-6))
+
+
+@pytest.mark.parametrize("dispatch", ["reference", "grouped"])
+def test_decoder_layer_chain(cuda, stack, dispatch):
+    """The stack as a decoder runs it, every layer's input the previous
+    layer's output: x_l normalized (RMS) feeds q, k and v; o on q's output
+    plus the residual x_l gives h; h normalized feeds the gate/up SwiGLU
+    site; down on that plus the residual h gives x_{l+1}.  (Without the
+    normalizations the N(0, 0.02) weights grow the activations
+    quadratically through SwiGLU and they overflow within five layers.)
+    "reference" is the reference's per-tensor dispatch (six launches per
+    layer, source/q4rdna.cu:713-793 from the hooks of
+    llama-cpp-q4rdna-integration.patch); "grouped" runs q/k/v as one
+    shared-x group (four launches).  All 36 layers run eagerly on one
+    stream, then are captured into one HIP graph and replayed: every output
+    of the replays equals the eager run bit for bit, and every launch of
+    layers 0, 17 and 35 meets both bars on the inputs it read."""
+    by = {t["name"]: t for t in stack}
+    layers = len(stack) // 7
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x51EEC000)
+    x0 = torch.randn(4096, generator=gen, device="cuda")
+    bufs = [dict(xn=torch.empty(4096, device="cuda"), q=torch.empty(4096, device="cuda"),
+                 k=torch.empty(1024, device="cuda"), v=torch.empty(1024, device="cuda"),
+                 h=torch.empty(4096, device="cuda"), hn=torch.empty(4096, device="cuda"),
+                 act=torch.empty(12288, device="cuda"), out=torch.empty(4096, device="cuda")) for _ in range(layers)]
+
+    def w(l, part):
+        return by[f"blk.{l}.{part}.weight"]["w"]
+
+    def run(stream):
+        for l in range(layers):
+            b = bufs[l]
+            x = x0 if l == 0 else bufs[l - 1]["out"]
+            rms_norm(x, b["xn"])
+            if dispatch == "reference":
+                assert api.mul_mat(w(l, "attn_q"), b["xn"], b["q"], stream=stream) is not None
+                assert api.mul_mat(w(l, "attn_k"), b["xn"], b["k"], stream=stream) is not None
+                assert api.mul_mat(w(l, "attn_v"), b["xn"], b["v"], stream=stream) is not None
+            else:
+                assert api.mul_mat_group([(w(l, "attn_q"), b["q"]), (w(l, "attn_k"), b["k"]),
+                                          (w(l, "attn_v"), b["v"])], b["xn"], stream=stream)
+            assert api.mul_mat_add(w(l, "attn_output"), b["q"], x, b["h"], stream=stream) is not None
+            rms_norm(b["h"], b["hn"])
+            assert api.mul_mat_glu(w(l, "ffn_up"), w(l, "ffn_gate"), b["hn"], b["act"], stream=stream) is not None
+            assert api.mul_mat_add(w(l, "ffn_down"), b["act"], b["h"], b["out"], stream=stream) is not None
+
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        run(st.cuda_stream)
+    torch.cuda.synchronize()
+    eager = [{k: v.clone() for k, v in b.items()} for b in bufs]
+    assert all(torch.isfinite(v).all() for b in eager for v in b.values())
+    for l in CHECK_LAYERS:
+        b = {k: v.cpu().numpy() for k, v in eager[l].items()}
+        x = (x0 if l == 0 else eager[l - 1]["out"]).cpu().numpy()
+
+        def tiles(part):
+            return by[f"blk.{l}.{part}.weight"]["w"].tiles.cpu().numpy()
+
+        for part, rows in (("attn_q", 4096), ("attn_k", 1024), ("attn_v", 1024)):
+            assert_gemv_parity(b[part[-1]], tiles(part), rows, 4096, b["xn"], label=(dispatch, l, part))
+        assert_gemv_parity(b["h"], tiles("attn_output"), 4096, 4096, b["q"], add=x, label=(dispatch, l, "o + add"))
+        assert_gemv_parity(b["act"], tiles("ffn_up"), 12288, 4096, b["hn"], gate_tiles=tiles("ffn_gate"),
+                           label=(dispatch, l, "swiglu"))
+        assert_gemv_parity(b["out"], tiles("ffn_down"), 4096, 12288, b["act"], add=b["h"],
+                           label=(dispatch, l, "down + add"))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        run(st.cuda_stream)
+    for rep in range(2):
+        for b in bufs:
+            for v in b.values():
+                v.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(st):
+            graph.replay()
+        st.synchronize()
+        for l in range(layers):
+            for k in bufs[l]:
+                assert torch.equal(bufs[l][k], eager[l][k]), (dispatch, rep, l, k)
+
+
 # ----------------------------------------------------------------- many items per workgroup
 
 KINDS = {

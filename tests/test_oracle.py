@@ -7,6 +7,7 @@ closed forms.  Tests that plant a mistake plant it in a copy of the oracle's
 computation here on the CPU and show the checks catch it.
 """
 import hashlib
+import os
 
 import numpy as np
 import pytest
@@ -303,6 +304,30 @@ def test_silu_textbook():
     assert np.allclose(O.silu(g), g / (1 + np.exp(-g)), rtol=1e-15, atol=1e-300)
 
 
+def silu_identities_hold(f) -> bool:
+    """Facts of silu(g) = g * sigmoid(g) that do not restate the formula:
+    silu(g) - silu(-g) = g (sigmoid(g) + sigmoid(-g) = 1), silu(0) = 0,
+    silu'(0) = 1/2 (silu(h) / h = 1/2 + h/4 + O(h^3)), silu(g) -> g for large
+    g and -> g e^g for very negative g."""
+    g = np.array([0.1, 0.7, 1.5, 3.0, 9.0, 20.0])
+    ok = np.allclose(f(g) - f(-g), g, rtol=1e-13, atol=0)
+    ok &= f(np.array([0.0]))[0] == 0.0
+    for h in (1e-3, 1e-4):
+        ok &= abs(f(np.array([h]))[0] / h - (0.5 + h / 4)) < h ** 3
+    ok &= abs(f(np.array([40.0]))[0] - 40.0) < 1e-13
+    ok &= abs(f(np.array([-40.0]))[0] / (-40.0 * np.exp(-40.0)) - 1.0) < 1e-12
+    return bool(ok)
+
+
+def test_silu_identities():
+    assert silu_identities_hold(O.silu)
+    # planted mistakes: the sign of the exponent, a dropped g, the sigmoid
+    # of -g: each breaks at least one identity
+    assert not silu_identities_hold(lambda g: g / (1 + np.exp(g)))
+    assert not silu_identities_hold(lambda g: 1 / (1 + np.exp(-g)))
+    assert not silu_identities_hold(lambda g: -g / (1 + np.exp(g)))
+
+
 # ----------------------------------------------------------------- sidecar
 
 def test_stack_known_answers():
@@ -334,3 +359,31 @@ def test_sidecar_validation_rules(golden):
     assert mutate(48 + 80, (5).to_bytes(8, "little")) == -3       # size
     assert mutate(48 + 72, (0).to_bytes(8, "little")) == -3       # offset < data_offset
     assert O.validate_sidecar(img[: len(img) - 300]) == -4        # truncated data
+
+
+# ----------------------------------------------------------------- the reference bench's own case
+
+BENCH_CASE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "q4rdna_bench_case.json")
+
+
+def test_bench_case_fixture_pins_the_oracle():
+    """The reference bench's correctness case (source/q4rdna_gemv_bench.hip:
+    215-262): the oracle's absmax packer (source/q4rdna_cpu_experiment.cpp's
+    default search) writes the tile stream whose sha256 the reference's own
+    experiment produced for these weights, and the bench activation has the
+    recorded bytes."""
+    import json
+    case = json.load(open(BENCH_CASE))
+    _, w = O.bf16_round(O.gaussian_weights(case["rows"], case["cols"], case["seed"]))
+    tiles, _ = O.pack_mt(w, O.ALGO_ABSMAX)
+    assert hashlib.sha256(tiles.tobytes()).hexdigest() == case["tiles_sha256"]
+    x = O.bench_activation(case["cols"])
+    assert hashlib.sha256(x.tobytes()).hexdigest() == case["x_sha256"]
+    # the formula itself, at points where it is known in closed form
+    assert x[0] == np.float32(0.125)
+    assert abs(float(x[1]) - (np.sin(0.013) * 0.25 + np.cos(0.007) * 0.125)) < 1e-7
+    # every scale is a normal fp16 number, so the bench's fp16 decode
+    # (which halves subnormals, :163-187) reads them as IEEE does
+    assert case["scales_normal"]
+    assert np.array_equal(O.gemv_seq_f32(tiles[:1088 * 64 * 2], 64, case["cols"], x),
+                          O.gemv_seq_f32(tiles[:1088 * 64 * 2], 64, case["cols"], x, ref_cpu_decode=True))

@@ -143,3 +143,83 @@ def test_noalloc_calls_replay_from_a_hip_graph(cuda):
         st.synchronize()
         assert torch.equal(y1, want[0]) and torch.equal(y2, want[1]), rep
     assert_gemv_parity(y2.cpu().numpy(), t2, 1024, 12288, x2.cpu().numpy(), label="graph replay")
+
+
+FIRST_CALL_CAPTURED = r"""
+import ctypes, sys
+sys.path[:0] = [{root!r}, {pkg!r}]
+import numpy as np
+import torch
+import q4rdna
+from q4rdna import _lib, api
+L = q4rdna.load()
+
+
+def weight(rows, cols, seed):
+    rng = np.random.default_rng(seed)
+    t = rng.integers(0, 256, (rows // 32, cols // 64, 1088), dtype=np.uint8)
+    s = (rng.uniform(1e-3, 3e-2, (rows // 32, cols // 64, 32)) * rng.choice([-1.0, 1.0], (rows // 32, cols // 64, 32)))
+    t[:, :, :64] = s.astype(np.float16).view(np.uint8).reshape(rows // 32, cols // 64, 64)
+    return api.QWeight.from_tiles(torch.from_numpy(t.reshape(-1)).cuda(), rows, cols)
+
+
+def call(fn, w, gate, x, y, split, stream):
+    o = _lib.LaunchOptions()
+    o.split_k = split
+    return fn(ctypes.byref(w.raw), None if gate is None else ctypes.byref(gate.raw), x.data_ptr(), None,
+              y.data_ptr(), ctypes.byref(o), stream)
+
+
+big, small = (weight(4096, 4096, 1), weight(4096, 4096, 2)), (weight(1024, 4096, 3), weight(1024, 4096, 4))
+st = torch.cuda.Stream()
+xg = torch.randn(4096, device="cuda")
+yg = [torch.full((4096,), float("nan"), device="cuda") for _ in range(2)]
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+# The process's first no-alloc calls, split 2 (exchange slots), plain and
+# SwiGLU, are captured: nothing runs until the graph is replayed.
+with torch.cuda.graph(g, stream=st):
+    assert call(L.q4rdna_mul_mat_ex_noalloc, big[0], None, xg, yg[0], 2, st.cuda_stream) == 0, q4rdna.last_error()
+    assert call(L.q4rdna_mul_mat_ex_noalloc, big[0], big[1], xg, yg[1], 2, st.cuda_stream) == 0, q4rdna.last_error()
+cur = torch.cuda.current_stream().cuda_stream
+# Eager split-2 calls before the first replay, larger then smaller, each
+# equal bit for bit to q4rdna_mul_mat_ex at the same split.
+for up, gate in (big, small, big):
+    for gt in (None, gate):
+        x = torch.randn(up.cols, device="cuda")
+        y_na = torch.full((up.rows,), float("nan"), device="cuda")
+        y_ex = torch.full((up.rows,), float("nan"), device="cuda")
+        assert call(L.q4rdna_mul_mat_ex_noalloc, up, gt, x, y_na, 2, cur) == 0, q4rdna.last_error()
+        assert call(L.q4rdna_mul_mat_ex, up, gt, x, y_ex, 2, cur) == 0, q4rdna.last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(y_na, y_ex), (up.rows, gt is not None)
+want = [torch.empty(4096, device="cuda") for _ in range(2)]
+assert call(L.q4rdna_mul_mat_ex, big[0], None, xg, want[0], 2, cur) == 0
+assert call(L.q4rdna_mul_mat_ex, big[0], big[1], xg, want[1], 2, cur) == 0
+torch.cuda.synchronize()
+for rep in range(3):
+    for y in yg:
+        y.fill_(float("nan"))
+    torch.cuda.synchronize()
+    with torch.cuda.stream(st):
+        g.replay()
+    st.synchronize()
+    assert torch.equal(yg[0], want[0]) and torch.equal(yg[1], want[1]), rep
+print("ok")
+"""
+
+
+def test_noalloc_first_call_captured_then_eager_calls(cuda):
+    """In a fresh process, the first allocation-free calls (split 2, plain
+    and SwiGLU) are captured into a graph, so they do not run; eager split-2
+    calls made before the first replay must still equal q4rdna_mul_mat_ex
+    bit for bit (the empty exchange slot is all-zero memory, which the device
+    array holds from the start), and the replays must too."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = FIRST_CALL_CAPTURED.format(root=root, pkg=os.path.join(root, "rdna-gfx1201-v0.1_amd"))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert r.stdout.strip().endswith("ok"), r.stdout
