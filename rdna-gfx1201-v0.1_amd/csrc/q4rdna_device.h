@@ -35,6 +35,53 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
+// Cross-lane sums, v + v of lane ^ m, without LDS: m = 8 is a DPP row rotate
+// by 8 (lane i of a 16-lane row reads lane (i + 8) mod 16 = i ^ 8), fused
+// into the add; m = 16 and m = 32 swap rows (v_permlane16_swap) or halves
+// (v_permlane32_swap) between two copies of v, after which the two copies
+// hold, lane by lane, v and its partner.  fp32 addition is commutative, so
+// each lane's sum equals v + partner bit for bit.
+__device__ __forceinline__ float add_xor8(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float add_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// Sum over the lanes that share lane & 7 (xor 8, 16, 32, in that order).
+__device__ __forceinline__ float add_over_a(float v) { return add_xor32(add_xor16(add_xor8(v))); }
+
+// add_over_a of four values at once, the result transposed: lane l returns
+// the sum of v[l >> 4] (over the lanes sharing l & 7).  The row swaps pair
+// v[0] with v[1] and v[2] with v[3], so each permlane swap and add reduces
+// two of the values; every lane-row's sum has add_over_a's operands in
+// add_over_a's order, so the sums are the same bits.
+__device__ __forceinline__ float add_over_a4(const float (&v)[4]) {
+    const float v0 = add_xor8(v[0]), v1 = add_xor8(v[1]), v2 = add_xor8(v[2]), v3 = add_xor8(v[3]);
+    // Lane-rows 0..3 of s01: v0 (rows 0+1), v1 (rows 0+1), v0 (rows 2+3), v1 (rows 2+3).
+    const auto p01 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v0), __float_as_uint(v1), false, false);
+    const float s01 = __uint_as_float(p01[0]) + __uint_as_float(p01[1]);
+    const auto p23 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v2), __float_as_uint(v3), false, false);
+    const float s23 = __uint_as_float(p23[0]) + __uint_as_float(p23[1]);
+    // Lanes 0..31 take s01's halves, lanes 32..63 s23's.
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(s01), __float_as_uint(s23), false, false);
+    return __uint_as_float(h[0]) + __uint_as_float(h[1]);
+}
+
+// n / d for d = split, n * d < 2^32: magic = ceil(2^32 / d) for d > 1
+// (split_magic on the host), 0 for d = 1.
+__device__ __forceinline__ uint32_t div_split(uint32_t n, uint32_t d, uint32_t magic) {
+    return d == 1 ? n : __umulhi(n, magic);
+}
+
+// The wave's index in its workgroup, as a wave-uniform (scalar) value, so
+// that addresses built from it stay in scalar registers.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)); }
+
 // Device-scope (agent) relaxed atomics: on gfx950 these are single sc1
 // loads/stores and a plain atomic add, coherent across the XCDs' L2s without
 // the whole-L2 write-back/invalidate that release/acquire fences emit.  Every

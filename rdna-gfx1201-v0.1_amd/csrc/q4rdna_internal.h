@@ -38,8 +38,10 @@ struct GemvArgs {
     float *partial;
     uint32_t *counters;
     uint32_t *slots;
-    uint32_t short_waves;  // 8 or 4: waves per workgroup for K chunks of at most 64 groups
+    uint32_t short_waves;  // waves per workgroup: 8 or 4 for K chunks of at most 64 groups,
+                           // 16 for chunks of 65..128 groups (gemv_waves)
     uint32_t vectors;      // launch_gemv_multi: activation vectors (x [vectors][cols], y/add [vectors][rows])
+    uint32_t split_magic;  // split_magic(split)
 };
 
 // Device-side descriptor of one GEMV in a multi-tensor plan.  Work items are
@@ -78,7 +80,20 @@ constexpr uint32_t kPrepBytes = 272;
 constexpr uint32_t kChunkGroups = 192;
 constexpr uint32_t kBlockRows = 64;
 
+// The kernels divide by the split with a multiply: magic = ceil(2^32 /
+// split) (0 for split 1) gives n / split exactly for n * split < 2^32, which
+// gemv_shape_fits guarantees for every n they divide (the workgroup index
+// and s * groups).
+inline uint32_t split_magic(uint32_t split) {
+    return split <= 1 ? 0u : static_cast<uint32_t>(((uint64_t{1} << 32) + split - 1) / split);
+}
+inline bool gemv_shape_fits(uint64_t row_tiles, uint64_t groups, uint64_t split) {
+    return row_tiles * split * split < (uint64_t{1} << 32) && groups * split * split < (uint64_t{1} << 32);
+}
 hipError_t launch_gemv(const GemvArgs &args, hipStream_t stream);
+// GemvArgs::short_waves for rows of `groups` groups split into `split` K
+// chunks, `workgroups` in all on `cus` CUs.
+uint32_t gemv_waves(uint32_t groups, uint32_t split, uint64_t workgroups, uint32_t cus);
 // args.vectors = 2..8 activation vectors; every K chunk (args.split of them)
 // must hold at most gemv_multi_stage_groups(args.vectors) groups.
 hipError_t launch_gemv_multi(const GemvArgs &args, hipStream_t stream);
@@ -138,6 +153,7 @@ struct GemvGroupArgs {
     const float *x;
     uint32_t count, cols, split, tiles;
     uint32_t short_waves;  // 8 or 4, as GemvArgs::short_waves
+    uint32_t split_magic;  // split_magic(split)
 };
 hipError_t launch_gemv_group(const GemvGroupArgs &args, hipStream_t stream);
 

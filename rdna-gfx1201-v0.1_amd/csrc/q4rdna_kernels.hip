@@ -12,13 +12,19 @@
 // 1024 code bytes arrive in four fully coalesced loads, plus one 8-byte load
 // of the lane's four scales.
 //
-// Decode.  XOR 0x88888888 turns every nibble into offset binary u = q + 8;
-// the low nibbles (mask 0x0F0F0F0F) and the high nibbles kept in place (mask
-// 0xF0F0F0F0, i.e. 16*u) convert with one v_cvt_f32_ubyteN each.  The 1/16
-// of the high nibbles is folded into the staged activation, and the -8 offset
-// into a per-(group, lane) constant c = -8 * sum of the lane's eight x values,
-// so per weight the inner loop is one conversion and one fma.  The fp16
-// scale multiplies the lane's per-(row, group) partial once per group.
+// Decode.  XOR 0x88888888 turns every nibble into offset binary u = q + 8.
+// Masked in place, a nibble in bits 0-3 (4-7) of a 16-bit half is the fp16
+// subnormal u * 2^-24 (16u * 2^-24), exact; rows 4q and 4q+2 sit in the
+// halves of the dword itself, rows 4q+1 and 4q+3 in the halves of the dword
+// shifted right by 8.  So a dword of 8 codes becomes four f16x2 registers
+// with one shift and four masks, and each weight takes one v_fma_mix_f32
+// (fp16 operand, fp32 product and sum).  The 2^24 and the 1/16 of the high
+// nibbles are folded into the staged activation (x * 2^24 for even k,
+// x * 2^20 for odd k): every product is exactly u * x, so every partial sum
+// is the one of a float(u) * x loop.  The -8 offset is folded into a
+// per-(group, lane) constant c = -8 * sum of the lane's eight x values, and
+// the fp16 scale multiplies the lane's per-(row, group) partial once per
+// group.  The staged activation is finite for |x| < 2^104.
 //
 // Activations.  The workgroup stages x for up to 64 groups at a time in LDS,
 // rearranged so lane a reads its 4 even-k values, its 4 odd-k values (/16)
@@ -30,8 +36,9 @@
 // the first wait; longer chunks by four waves that keep two tile batches in
 // flight.
 //
-// Reduction.  Lane partials are summed over a with xor-8/16/32 shuffles, the
-// waves' results in LDS in wave order, and K chunks split across
+// Reduction.  Lane partials are summed over a with xor-8/16/32 cross-lane
+// adds (a DPP row rotate and two permlane swaps), the waves' results in LDS
+// in wave order, and K chunks split across
 // workgroups through a partial buffer summed in chunk order by the last
 // workgroup to arrive, so every result is bit-reproducible run to run.
 #include <type_traits>
@@ -43,13 +50,17 @@ namespace {
 
 constexpr int kWaves = 4;       // waves of the pipelined loop's workgroup
 constexpr int kShortWaves = 8;  // waves of the short-range kernel's workgroup
+constexpr int kWideWaves = 16;  // waves of the wide short-range workgroup (one per CU, chunks up to 128 groups)
 constexpr int kStageGroups = 64;  // groups of x staged in LDS at once
+constexpr int kWideStageGroups = 128;
 constexpr int kBatch = 2;         // default tiles per wave per loop trip (x2 in flight)
 
-struct XStage {
-    float4 v[kStageGroups][16];  // [g][a] even-k x, [g][8 + a] odd-k x / 16
-    float c[kStageGroups][8];    // -8 * sum of the lane's 8 x values
+template <int SG>
+struct XStageT {
+    float4 v[SG][16];  // [g][a] even-k x * 2^24, [g][8 + a] odd-k x * 2^20
+    float c[SG][8];    // -8 * sum of the lane's 8 x values
 };
+using XStage = XStageT<kStageGroups>;
 
 struct TileRegs {
     uint32_t d[4];
@@ -60,44 +71,72 @@ struct TileRegs {
 // the caches instead of evicting the activations and partial sums.
 __device__ __forceinline__ TileRegs load_tile(const uint8_t *__restrict__ tile, int q, int a) {
     TileRegs r;
-    const uint8_t *codes = tile + 64 + 4 * q + 32 * a;
+    // One 32-bit lane offset on the (wave-uniform) tile address.
+    const uint32_t lane_off = 64u + 4u * static_cast<uint32_t>(q) + 32u * static_cast<uint32_t>(a);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) r.d[j] = __builtin_nontemporal_load((gptr_u32)(codes + 256 * j));
-    const u32x2 s = __builtin_nontemporal_load((gptr_u32x2)(tile + 8 * q));
+    for (int j = 0; j < 4; ++j) r.d[j] = __builtin_nontemporal_load((gptr_u32)(tile + (lane_off + 256u * j)));
+    const u32x2 s = __builtin_nontemporal_load((gptr_u32x2)(tile + 8u * static_cast<uint32_t>(q)));
     r.s01 = s.x;
     r.s23 = s.y;
     return r;
 }
 
-// acc[r] += scale(row 4q+r) * sum over the lane's 8 k of code * x.
-__device__ __forceinline__ void tile_fma(const TileRegs &r, const float4 xl, const float4 xh,
-                                         const float c, float acc[4]) {
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// The 32 codes of a lane's tile slice as fp16 subnormals: for k-pair
+// a + 8j, l02[j] = (u of row 4q, u of row 4q+2) at even k, h02[j] = 16u of
+// the same rows at odd k, l13/h13 the same for rows 4q+1 and 4q+3.
+struct TileCodes {
+    f16x2 l02[4], h02[4], l13[4], h13[4];
+};
+
+__device__ __forceinline__ TileCodes split_codes(const TileRegs &r) {
+    TileCodes w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        // (d & mask) ^ offset is one v_bitop3_b32 each.
+        const uint32_t d = r.d[j], o = d >> 8;
+        w.l02[j] = __builtin_bit_cast(f16x2, (d & 0x000f000fu) ^ 0x00080008u);
+        w.h02[j] = __builtin_bit_cast(f16x2, (d & 0x00f000f0u) ^ 0x00800080u);
+        w.l13[j] = __builtin_bit_cast(f16x2, (o & 0x000f000fu) ^ 0x00080008u);
+        w.h13[j] = __builtin_bit_cast(f16x2, (o & 0x00f000f0u) ^ 0x00800080u);
+    }
+    return w;
+}
+
+// acc[r] += scale(row 4q + r) * (c + sum over the lane's 8 k of u * x), the
+// row's products in k order: for each k-pair the even k, then the odd k.
+// xl = even-k x * 2^24, xh = odd-k x * 2^20.
+__device__ __forceinline__ void apply_codes(const TileCodes &w, uint32_t s01, uint32_t s23, const float4 xl,
+                                            const float4 xh, const float c, float (&acc)[4]) {
     const float xlv[4] = {xl.x, xl.y, xl.z, xl.w};
     const float xhv[4] = {xh.x, xh.y, xh.z, xh.w};
     float p0 = c, p1 = c, p2 = c, p3 = c;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const uint32_t e = r.d[j] ^ 0x88888888u;
-        uint32_t lo = e & 0x0f0f0f0fu;
-        uint32_t hi = e & 0xf0f0f0f0u;
-        // Hide the masks' known bits so each byte converts with
-        // v_cvt_f32_ubyte{0,1,2,3} instead of an extract plus ubyte0.
-        asm("" : "+v"(lo));
-        asm("" : "+v"(hi));
-        p0 = fmaf(static_cast<float>(lo & 0xffu), xlv[j], p0);
-        p1 = fmaf(static_cast<float>((lo >> 8) & 0xffu), xlv[j], p1);
-        p2 = fmaf(static_cast<float>((lo >> 16) & 0xffu), xlv[j], p2);
-        p3 = fmaf(static_cast<float>(lo >> 24), xlv[j], p3);
-        p0 = fmaf(static_cast<float>(hi & 0xffu), xhv[j], p0);
-        p1 = fmaf(static_cast<float>((hi >> 8) & 0xffu), xhv[j], p1);
-        p2 = fmaf(static_cast<float>((hi >> 16) & 0xffu), xhv[j], p2);
-        p3 = fmaf(static_cast<float>(hi >> 24), xhv[j], p3);
+        p0 = fmaf(static_cast<float>(w.l02[j].x), xlv[j], p0);
+        p1 = fmaf(static_cast<float>(w.l13[j].x), xlv[j], p1);
+        p2 = fmaf(static_cast<float>(w.l02[j].y), xlv[j], p2);
+        p3 = fmaf(static_cast<float>(w.l13[j].y), xlv[j], p3);
+        p0 = fmaf(static_cast<float>(w.h02[j].x), xhv[j], p0);
+        p1 = fmaf(static_cast<float>(w.h13[j].x), xhv[j], p1);
+        p2 = fmaf(static_cast<float>(w.h02[j].y), xhv[j], p2);
+        p3 = fmaf(static_cast<float>(w.h13[j].y), xhv[j], p3);
     }
-    acc[0] = fmaf(half_bits_to_float(r.s01), p0, acc[0]);
-    acc[1] = fmaf(half_bits_to_float(r.s01 >> 16), p1, acc[1]);
-    acc[2] = fmaf(half_bits_to_float(r.s23), p2, acc[2]);
-    acc[3] = fmaf(half_bits_to_float(r.s23 >> 16), p3, acc[3]);
+    acc[0] = fmaf(half_bits_to_float(s01), p0, acc[0]);
+    acc[1] = fmaf(half_bits_to_float(s01 >> 16), p1, acc[1]);
+    acc[2] = fmaf(half_bits_to_float(s23), p2, acc[2]);
+    acc[3] = fmaf(half_bits_to_float(s23 >> 16), p3, acc[3]);
 }
+
+__device__ __forceinline__ void tile_fma(const TileRegs &r, const float4 xl, const float4 xh, const float c,
+                                         float (&acc)[4]) {
+    apply_codes(split_codes(r), r.s01, r.s23, xl, xh, c, acc);
+}
+
+// Staged activation factors (see the decode note above).
+constexpr float kEvenScale = 16777216.0f;  // 2^24
+constexpr float kOddScale = 1048576.0f;    // 2^20 = 2^24 / 16
 
 // Stage x for groups [g0, g0 + ng) into LDS.
 __device__ __forceinline__ void stage_x(XStage &st, const float *__restrict__ x, uint32_t g0, int ng) {
@@ -106,17 +145,22 @@ __device__ __forceinline__ void stage_x(XStage &st, const float *__restrict__ x,
         const gptr_cf32 b = (gptr_cf32)x + (static_cast<size_t>(g0) + g) * kGroup + 2 * a;
         const float l0 = b[0], h0 = b[1], l1 = b[16], h1 = b[17];
         const float l2 = b[32], h2 = b[33], l3 = b[48], h3 = b[49];
-        st.v[g][a] = make_float4(l0, l1, l2, l3);
-        st.v[g][8 + a] = make_float4(h0 * 0.0625f, h1 * 0.0625f, h2 * 0.0625f, h3 * 0.0625f);
+        st.v[g][a] = make_float4(l0 * kEvenScale, l1 * kEvenScale, l2 * kEvenScale, l3 * kEvenScale);
+        st.v[g][8 + a] = make_float4(h0 * kOddScale, h1 * kOddScale, h2 * kOddScale, h3 * kOddScale);
         st.c[g][a] = -8.0f * (((((((l0 + h0) + l1) + h1) + l2) + h2) + l3) + h3);
     }
 }
 
-struct Shared {
-    XStage st;
-    float red[2][kShortWaves][32];
+template <int SG, int WR>
+struct SharedT {
+    XStageT<SG> st;
+    float red[2][WR][32];
     uint32_t last;
 };
+using Shared = SharedT<kStageGroups, kShortWaves>;
+// The workgroup's shared memory for W waves.
+template <int W>
+using SharedFor = std::conditional_t<(W > kShortWaves), SharedT<kWideStageGroups, kWideWaves>, Shared>;
 
 template <bool GATE, int BATCH>
 __device__ __forceinline__ void load_batch(TileRegs (&t)[BATCH], TileRegs (&u)[BATCH],
@@ -150,29 +194,19 @@ __device__ __forceinline__ void compute_batch(const TileRegs (&t)[BATCH], const 
 }
 
 // Sum the lanes' row partials of a row tile over the workgroup: xor-8/16/32
-// shuffles within each wave, then the W waves in wave order through LDS.
+// cross-lane adds within each wave, then the W waves in wave order through LDS.
 // Threads 0..31 return the row sums (out, gout).
-template <bool GATE, int W>
-__device__ __forceinline__ void reduce_rows(Shared &sh, float (&acc)[4], float (&gacc)[4], float &out, float &gout) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int q = lane & 7, a = lane >> 3;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        acc[r] += __shfl_xor(acc[r], 8);
-        acc[r] += __shfl_xor(acc[r], 16);
-        acc[r] += __shfl_xor(acc[r], 32);
-        if constexpr (GATE) {
-            gacc[r] += __shfl_xor(gacc[r], 8);
-            gacc[r] += __shfl_xor(gacc[r], 16);
-            gacc[r] += __shfl_xor(gacc[r], 32);
-        }
-    }
-    if (a == 0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            sh.red[0][wave][4 * q + r] = acc[r];
-            if constexpr (GATE) sh.red[1][wave][4 * q + r] = gacc[r];
-        }
+template <bool GATE, int W, class Sh>
+__device__ __forceinline__ void reduce_rows(Sh &sh, float (&acc)[4], float (&gacc)[4], float &out, float &gout) {
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    // Lane l ends with row 4 (l & 7) + (l >> 4); lanes l and l ^ 8 agree.
+    const float tot = add_over_a4(acc);
+    float gtot = 0.f;
+    if constexpr (GATE) gtot = add_over_a4(gacc);
+    if ((lane & 8) == 0) {
+        const int row = 4 * (lane & 7) + (lane >> 4);
+        sh.red[0][wave][row] = tot;
+        if constexpr (GATE) sh.red[1][wave][row] = gtot;
     }
     __syncthreads();
     if (threadIdx.x < 32) {
@@ -203,7 +237,7 @@ __device__ __forceinline__ void tile_row_partial(Shared &sh, const uint8_t *__re
                                                  uint32_t rt, uint32_t g_begin, uint32_t g_end,
                                                  float &out, float &gout) {
     const uint32_t groups = cols / kGroup;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int q = lane & 7, a = lane >> 3;
     const size_t row_tile_offset = static_cast<size_t>(rt) * groups * kTileBytes;
     const uint8_t *wt = w + row_tile_offset;
@@ -241,14 +275,16 @@ __device__ __forceinline__ void tile_row_partial(Shared &sh, const uint8_t *__re
 // clamped to the range; a clamped duplicate is loaded but never used).  The
 // tiles then arrive in one overlapped window instead of one batch after
 // another.
-template <bool GATE, int T, int W>
-__device__ __forceinline__ void tile_row_partial_short(Shared &sh, const uint8_t *__restrict__ w,
+template <bool GATE, int T, int W, class Sh>
+__device__ __forceinline__ void tile_row_partial_short(Sh &sh, const uint8_t *__restrict__ w,
                                                        const uint8_t *__restrict__ gw,
                                                        const float *__restrict__ x, uint32_t cols, uint32_t rt,
                                                        uint32_t g_begin, uint32_t g_end, float &out, float &gout) {
-    static_assert(W * T <= kStageGroups && W <= kShortWaves, "the range fits one stage");
+    static_assert(W * T <= static_cast<int>(sizeof(sh.st.c) / sizeof(sh.st.c[0])) &&
+                      W <= static_cast<int>(sizeof(sh.red[0]) / sizeof(sh.red[0][0])),
+                  "the range fits one stage");
     const uint32_t groups = cols / kGroup;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int q = lane & 7, a = lane >> 3;
     const int ng = static_cast<int>(g_end - g_begin);
     const size_t first = (static_cast<size_t>(rt) * groups + g_begin) * kTileBytes;
@@ -287,8 +323,8 @@ __device__ __forceinline__ void tile_row_partial_short(Shared &sh, const uint8_t
         const int xg = (threadIdx.x >> 3) + 8 * W * m;
         if (xg < ng) {
             const float *lm = l[m], *hm = h[m];
-            sh.st.v[xg][xa] = make_float4(lm[0], lm[1], lm[2], lm[3]);
-            sh.st.v[xg][8 + xa] = make_float4(hm[0] * 0.0625f, hm[1] * 0.0625f, hm[2] * 0.0625f, hm[3] * 0.0625f);
+            sh.st.v[xg][xa] = make_float4(lm[0] * kEvenScale, lm[1] * kEvenScale, lm[2] * kEvenScale, lm[3] * kEvenScale);
+            sh.st.v[xg][8 + xa] = make_float4(hm[0] * kOddScale, hm[1] * kOddScale, hm[2] * kOddScale, hm[3] * kOddScale);
             sh.st.c[xg][xa] = -8.0f * (((((((lm[0] + hm[0]) + lm[1]) + hm[1]) + lm[2]) + hm[2]) + lm[3]) + hm[3]);
         }
     }
@@ -323,8 +359,8 @@ __device__ __forceinline__ float epilogue(float v, float gv, const float *__rest
 // for them to complete, then count arrivals, and the last workgroup of the
 // row tile sums the chunks in chunk order and resets the counter.  `add` may
 // be null (ADD false makes it so at compile time).
-template <bool GATE, bool ADD>
-__device__ __forceinline__ void finish_rows(Shared &sh, float *__restrict__ y, const float *__restrict__ add,
+template <bool GATE, bool ADD, class Sh>
+__device__ __forceinline__ void finish_rows(Sh &sh, float *__restrict__ y, const float *__restrict__ add,
                                             float *__restrict__ partial, uint32_t *__restrict__ counters,
                                             uint32_t *__restrict__ slots, uint32_t rows, uint32_t split, uint32_t s,
                                             uint32_t rt, float v, float gv) {
@@ -362,13 +398,13 @@ __device__ __forceinline__ void finish_rows(Shared &sh, float *__restrict__ y, c
 // chunks of one row tile run on one XCD.
 template <bool GATE, bool ADD, int T, int W>
 __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs args) {
-    __shared__ Shared sh;
+    __shared__ SharedFor<W> sh;
     const uint32_t groups = args.cols / kGroup;
     const uint32_t split = args.split;
     const uint32_t logical = xcd_remap(blockIdx.x, gridDim.x);
-    const uint32_t rt = logical / split, s = logical % split;
-    const uint32_t g_begin = static_cast<uint32_t>((static_cast<uint64_t>(s) * groups) / split);
-    const uint32_t g_end = static_cast<uint32_t>((static_cast<uint64_t>(s + 1) * groups) / split);
+    const uint32_t rt = div_split(logical, split, args.split_magic), s = logical - rt * split;
+    const uint32_t g_begin = div_split(s * groups, split, args.split_magic);
+    const uint32_t g_end = div_split((s + 1) * groups, split, args.split_magic);
     float v = 0.f, gv = 0.f;
     if constexpr (T == 0)
         tile_row_partial<GATE>(sh, args.w, args.gate, args.x, args.cols, rt, g_begin, g_end, v, gv);
@@ -388,7 +424,7 @@ __global__ __launch_bounds__(64 * W) void gemv_group_kernel(GemvGroupArgs a) {
     const uint32_t groups = a.cols / kGroup;
     const uint32_t split = a.split;
     const uint32_t logical = xcd_remap(blockIdx.x, gridDim.x);
-    const uint32_t gt = logical / split, s = logical % split;
+    const uint32_t gt = div_split(logical, split, a.split_magic), s = logical - gt * split;
     // The workgroup's GEMV (constant indices only, so the entries stay in
     // the kernel-argument segment).
     GemvGroupEntry G = a.g[0];
@@ -396,8 +432,8 @@ __global__ __launch_bounds__(64 * W) void gemv_group_kernel(GemvGroupArgs a) {
     for (uint32_t i = 1; i < kMaxGroup; ++i)
         if (i < a.count && gt >= a.g[i].tile_begin) G = a.g[i];
     const uint32_t rt = gt - G.tile_begin;
-    const uint32_t g_begin = static_cast<uint32_t>((static_cast<uint64_t>(s) * groups) / split);
-    const uint32_t g_end = static_cast<uint32_t>((static_cast<uint64_t>(s + 1) * groups) / split);
+    const uint32_t g_begin = div_split(s * groups, split, a.split_magic);
+    const uint32_t g_end = div_split((s + 1) * groups, split, a.split_magic);
     float v = 0.f, gv = 0.f;
     tile_row_partial_short<GATE, T, W>(sh, G.w, G.gate, a.x, a.cols, rt, g_begin, g_end, v, gv);
     if (G.add != nullptr)
@@ -429,48 +465,6 @@ struct MvShared {
     uint32_t last;
 };
 
-// The 32 weights of a lane's tile slice as offset-binary floats: wl[j][r] =
-// low nibble + 8 of row 4q + r at k-pair a + 8j, wh[j][r] = 16 * (high + 8).
-__device__ __forceinline__ void decode_tile(const TileRegs &r, float (&wl)[4][4], float (&wh)[4][4]) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t e = r.d[j] ^ 0x88888888u;
-        uint32_t lo = e & 0x0f0f0f0fu;
-        uint32_t hi = e & 0xf0f0f0f0u;
-        asm("" : "+v"(lo));
-        asm("" : "+v"(hi));
-        wl[j][0] = static_cast<float>(lo & 0xffu);
-        wl[j][1] = static_cast<float>((lo >> 8) & 0xffu);
-        wl[j][2] = static_cast<float>((lo >> 16) & 0xffu);
-        wl[j][3] = static_cast<float>(lo >> 24);
-        wh[j][0] = static_cast<float>(hi & 0xffu);
-        wh[j][1] = static_cast<float>((hi >> 8) & 0xffu);
-        wh[j][2] = static_cast<float>((hi >> 16) & 0xffu);
-        wh[j][3] = static_cast<float>(hi >> 24);
-    }
-}
-
-// acc[r] += scale(row 4q + r) * (c + sum_j wl[j][r] xl[j] + wh[j][r] xh[j]),
-// in tile_fma's order.
-__device__ __forceinline__ void apply_tile(const float (&wl)[4][4], const float (&wh)[4][4], uint32_t s01,
-                                           uint32_t s23, const float4 xl, const float4 xh, const float c,
-                                           float (&acc)[4]) {
-    const float xlv[4] = {xl.x, xl.y, xl.z, xl.w};
-    const float xhv[4] = {xh.x, xh.y, xh.z, xh.w};
-    float p[4] = {c, c, c, c};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) p[r] = fmaf(wl[j][r], xlv[j], p[r]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) p[r] = fmaf(wh[j][r], xhv[j], p[r]);
-    }
-    acc[0] = fmaf(half_bits_to_float(s01), p[0], acc[0]);
-    acc[1] = fmaf(half_bits_to_float(s01 >> 16), p[1], acc[1]);
-    acc[2] = fmaf(half_bits_to_float(s23), p[2], acc[2]);
-    acc[3] = fmaf(half_bits_to_float(s23 >> 16), p[3], acc[3]);
-}
-
 template <bool GATE, bool ADD, int NV, int T>
 __global__ __launch_bounds__(64 * kMvWaves) void gemv_multi_kernel(GemvArgs args) {
     constexpr int W = kMvWaves;
@@ -481,11 +475,11 @@ __global__ __launch_bounds__(64 * kMvWaves) void gemv_multi_kernel(GemvArgs args
     const uint32_t split = args.split;
     const uint32_t nv = args.vectors;
     const uint32_t logical = xcd_remap(blockIdx.x, gridDim.x);
-    const uint32_t rt = logical / split, s = logical % split;
-    const uint32_t g_begin = static_cast<uint32_t>((static_cast<uint64_t>(s) * groups) / split);
-    const uint32_t g_end = static_cast<uint32_t>((static_cast<uint64_t>(s + 1) * groups) / split);
+    const uint32_t rt = div_split(logical, split, args.split_magic), s = logical - rt * split;
+    const uint32_t g_begin = div_split(s * groups, split, args.split_magic);
+    const uint32_t g_end = div_split((s + 1) * groups, split, args.split_magic);
     const int ng = static_cast<int>(g_end - g_begin);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int q = lane & 7, a = lane >> 3;
     const size_t first = (static_cast<size_t>(rt) * groups + g_begin) * kTileBytes;
     const uint8_t *wt = args.w + first;
@@ -526,8 +520,8 @@ __global__ __launch_bounds__(64 * kMvWaves) void gemv_multi_kernel(GemvArgs args
         const int v = item / (SG * 8), xg = (item >> 3) % SG, xa = item & 7;
         if (v < static_cast<int>(nv) && xg < ng) {
             const float *lm = l[m], *hm = h[m];
-            sh.v[v][xg][xa] = make_float4(lm[0], lm[1], lm[2], lm[3]);
-            sh.v[v][xg][8 + xa] = make_float4(hm[0] * 0.0625f, hm[1] * 0.0625f, hm[2] * 0.0625f, hm[3] * 0.0625f);
+            sh.v[v][xg][xa] = make_float4(lm[0] * kEvenScale, lm[1] * kEvenScale, lm[2] * kEvenScale, lm[3] * kEvenScale);
+            sh.v[v][xg][8 + xa] = make_float4(hm[0] * kOddScale, hm[1] * kOddScale, hm[2] * kOddScale, hm[3] * kOddScale);
             sh.c[v][xg][xa] = -8.0f * (((((((lm[0] + hm[0]) + lm[1]) + hm[1]) + lm[2]) + hm[2]) + lm[3]) + hm[3]);
         }
     }
@@ -542,17 +536,17 @@ __global__ __launch_bounds__(64 * kMvWaves) void gemv_multi_kernel(GemvArgs args
     for (int i = 0; i < T; ++i) {
         const int gg = wave + W * i;
         if (gg < ng) {
-            float wl[4][4], wh[4][4], gl[4][4], gh[4][4];
-            decode_tile(t[i], wl, wh);
-            if constexpr (GATE) decode_tile(u[i], gl, gh);
+            const TileCodes w = split_codes(t[i]);
+            TileCodes gw;
+            if constexpr (GATE) gw = split_codes(u[i]);
 #pragma unroll
             for (int v = 0; v < NV; ++v) {
                 if (v < static_cast<int>(nv)) {
                     const float4 xl = sh.v[v][gg][a];
                     const float4 xh = sh.v[v][gg][8 + a];
                     const float c = sh.c[v][gg][a];
-                    apply_tile(wl, wh, t[i].s01, t[i].s23, xl, xh, c, acc[v]);
-                    if constexpr (GATE) apply_tile(gl, gh, u[i].s01, u[i].s23, xl, xh, c, gacc[v]);
+                    apply_codes(w, t[i].s01, t[i].s23, xl, xh, c, acc[v]);
+                    if constexpr (GATE) apply_codes(gw, u[i].s01, u[i].s23, xl, xh, c, gacc[v]);
                 }
             }
         }
@@ -560,26 +554,15 @@ __global__ __launch_bounds__(64 * kMvWaves) void gemv_multi_kernel(GemvArgs args
 
     // Lanes, then waves in wave order (reduce_rows, per vector).
 #pragma unroll
-    for (int v = 0; v < NV; ++v)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            acc[v][r] += __shfl_xor(acc[v][r], 8);
-            acc[v][r] += __shfl_xor(acc[v][r], 16);
-            acc[v][r] += __shfl_xor(acc[v][r], 32);
-            if constexpr (GATE) {
-                gacc[v][r] += __shfl_xor(gacc[v][r], 8);
-                gacc[v][r] += __shfl_xor(gacc[v][r], 16);
-                gacc[v][r] += __shfl_xor(gacc[v][r], 32);
-            }
+    for (int v = 0; v < NV; ++v) {
+        const float tot = add_over_a4(acc[v]);
+        float gtot = 0.f;
+        if constexpr (GATE) gtot = add_over_a4(gacc[v]);
+        if ((lane & 8) == 0) {
+            const int row = 4 * (lane & 7) + (lane >> 4);
+            sh.red[0][v][wave][row] = tot;
+            if constexpr (GATE) sh.red[1][v][wave][row] = gtot;
         }
-    if (a == 0) {
-#pragma unroll
-        for (int v = 0; v < NV; ++v)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                sh.red[0][v][wave][4 * q + r] = acc[v][r];
-                if constexpr (GATE) sh.red[1][v][wave][4 * q + r] = gacc[v][r];
-            }
     }
     __syncthreads();
     // Thread t < 32*nv finishes row t % 32 of vector t / 32.
@@ -874,7 +857,8 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(const float *__restrict_
 #pragma clang fp contract(on)
 
 // K chunks of at most 64 groups run the short-range kernel with W = 8 or 4
-// waves (args.short_waves) and T <= 64 / W tiles per wave; longer chunks the
+// waves (args.short_waves) and T <= 64 / W tiles per wave; chunks of up to
+// 128 groups the wide workgroup of 16 waves and T <= 8; longer chunks the
 // pipelined loop (T = 0) with kWaves waves.  The host keeps split <= groups,
 // so every chunk holds at least one group.
 template <bool GATE, bool ADD, int W>
@@ -883,7 +867,17 @@ hipError_t launch_gemv_w(const GemvArgs &args, hipStream_t stream) {
     const uint32_t groups = args.cols / kGroup;
     const uint32_t per_wave = ((groups + args.split - 1) / args.split + W - 1) / W;
     const dim3 grid(blocks), block(64 * W);
-    if (per_wave <= 1)
+    if constexpr (W == kWideWaves) {
+        if (per_wave <= 4)
+            hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 4, W>), grid, block, 0, stream, args);
+        else if (per_wave <= 6)
+            hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 6, W>), grid, block, 0, stream, args);
+        else if (per_wave <= 8)
+            hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 8, W>), grid, block, 0, stream, args);
+        else
+            return hipErrorInvalidValue;
+        return hipGetLastError();
+    } else if (per_wave <= 1)
         hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 1, W>), grid, block, 0, stream, args);
     else if (per_wave <= 2)
         hipLaunchKernelGGL((gemv_kernel<GATE, ADD, 2, W>), grid, block, 0, stream, args);
@@ -900,6 +894,7 @@ hipError_t launch_gemv_w(const GemvArgs &args, hipStream_t stream) {
 
 template <bool GATE, bool ADD>
 hipError_t launch_gemv_t(const GemvArgs &args, hipStream_t stream) {
+    if (args.short_waves == kWideWaves) return launch_gemv_w<GATE, ADD, kWideWaves>(args, stream);
     return args.short_waves == kShortWaves ? launch_gemv_w<GATE, ADD, kShortWaves>(args, stream)
                                            : launch_gemv_w<GATE, ADD, kWaves>(args, stream);
 }
@@ -985,6 +980,19 @@ hipError_t launch_gemv_multi(const GemvArgs &args, hipStream_t stream) {
 }
 
 uint32_t gemv_multi_stage_groups(uint32_t vectors) { return vectors > 4 ? 16u : 32u; }
+
+uint32_t gemv_waves(uint32_t groups, uint32_t split, uint64_t workgroups, uint32_t cus) {
+    const uint32_t chunk = (groups + split - 1) / split;
+    // A chunk longer than one eight-wave stage runs on 16 waves (one
+    // workgroup per CU, every tile in flight) while it fits their registers.
+    if (chunk > static_cast<uint32_t>(kStageGroups) && chunk <= static_cast<uint32_t>(kWideStageGroups) &&
+        workgroups <= cus)
+        return kWideWaves;
+    // Eight waves per workgroup while the launch is latency-bound (at most
+    // four workgroups per CU); with more, four waves of up to 16 tiles keep
+    // more bytes in flight per CU (151936x4096: 60 us against 68).
+    return workgroups <= 4ull * cus ? kShortWaves : kWaves;
+}
 
 hipError_t launch_dequant(const uint8_t *w, uint32_t rows, uint32_t cols, float *out, hipStream_t stream) {
     const uint64_t work = static_cast<uint64_t>(rows) * cols / 2;

@@ -253,6 +253,9 @@ int check_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const fl
     if ((rc = check_options(options)) != Q4RDNA_OK) return rc;
     TensorLaunch L{};
     L.split = resolve_split(w, s);
+    if (!gemv_shape_fits(w->rows / kTileRows, w->columns / kGroup, L.split))
+        return set_error(Q4RDNA_ERR_ARGUMENT, "shape %ux%u at split %u is beyond the kernels' index range", w->rows,
+                         w->columns, L.split);
     if (L.split == 2) {
         L.slots = static_cast<size_t>(w->rows) * (gate ? 2 : 1);
     } else if (L.split > 2) {
@@ -275,12 +278,10 @@ int launch_tensor_in(const TensorLaunch &launch, const q4rdna_weight *w, const u
     args.rows = w->rows;
     args.cols = w->columns;
     args.split = launch.split;
-    // Eight waves per workgroup while the launch is latency-bound (at
-    // most four workgroups per CU); with more, four waves of up to 16
-    // tiles keep more bytes in flight per CU (151936x4096: 60 us
-    // against 68).
+    args.split_magic = split_magic(launch.split);
     const uint64_t workgroups = static_cast<uint64_t>(w->rows / kTileRows) * launch.split;
-    args.short_waves = workgroups <= 4ull * cu_count(w->device) ? 8u : 4u;
+    args.short_waves =
+        gemv_waves(w->columns / kGroup, launch.split, workgroups, static_cast<uint32_t>(cu_count(w->device)));
     if (launch.split == 2) {
         args.slots = slots;
     } else if (launch.split > 2) {
@@ -582,7 +583,8 @@ int launch_group_valu(const q4rdna_group_desc *descs, uint32_t count, const floa
                          kGroupChunkGroups);
     const uint32_t tiles = static_cast<uint32_t>(total_rows / kTileRows);
     const uint64_t workgroups = static_cast<uint64_t>(tiles) * split;
-    if (workgroups > 0x7fffffffull) return set_error(Q4RDNA_ERR_ARGUMENT, "group too large");
+    if (workgroups > 0x7fffffffull || !q4rdna::gemv_shape_fits(tiles, groups, split))
+        return set_error(Q4RDNA_ERR_ARGUMENT, "group too large");
     const uint32_t streams = glu ? 2u : 1u;
     size_t partial_floats = 0, counters = 0, slots = 0;
     for (uint32_t i = 0; i < count; ++i) {
@@ -602,6 +604,7 @@ int launch_group_valu(const q4rdna_group_desc *descs, uint32_t count, const floa
     args.count = count;
     args.cols = cols;
     args.split = split;
+    args.split_magic = q4rdna::split_magic(split);
     args.tiles = tiles;
     args.short_waves = workgroups <= 4ull * cu_count(device) ? 8u : 4u;
     uint32_t tile_begin = 0;
@@ -712,7 +715,11 @@ int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, cons
     args.y = y;
     args.rows = w->rows;
     args.cols = w->columns;
+    if (!q4rdna::gemv_shape_fits(w->rows / kTileRows, groups, split))
+        return set_error(Q4RDNA_ERR_ARGUMENT, "shape %ux%u at split %u is beyond the kernels' index range", w->rows,
+                         w->columns, split);
     args.split = split;
+    args.split_magic = q4rdna::split_magic(split);
     args.vectors = n;
     if (split > 1) {
         Workspace *ws = nullptr;

@@ -188,12 +188,15 @@ def test_mul_mat_glu_swiglu(cuda, rows, cols):
 @pytest.mark.parametrize("kind", ["plain", "add", "glu", "glu+add"])
 def test_every_kernel_path_matches_oracle(cuda, kind):
     """Each per-tensor kernel path: K chunks of at most 64 groups (4, 8, 16,
-    32, 64 and 43 groups: 1, 2, 4 and 8 tiles per wave of eight, every load
-    issued before the first wait) and longer chunks (the pipelined loop),
-    each with the plain, add, SwiGLU and SwiGLU-after-add epilogues, against
-    both parity bars."""
+    32, 64, 43 and 48 groups: 1, 2, 4 and 8 tiles per wave of eight, every
+    load issued before the first wait), chunks of 65 to 128 groups on the
+    16-wave workgroup (65 and 80 groups: 6 tiles per wave, some waves' last
+    tile a clamped duplicate; 96 at splits 1 and 2; 128: 8 tiles per wave)
+    and longer chunks (192 groups: the pipelined loop), each with the plain,
+    add, SwiGLU and SwiGLU-after-add epilogues, against both parity bars."""
     rows = 96
-    for cols, splits in [(4096, (16, 8, 4, 2, 1)), (8192, (1, 3))]:
+    for cols, splits in [(4096, (16, 8, 4, 2, 1)), (8192, (1, 3)), (6144, (1, 2)), (4160, (1,)), (5120, (1,)),
+                         (12288, (2, 1))]:
         up_t = random_tiles(rows, cols, 31 + cols)
         x = O.gaussian_x(cols, 32 + cols)
         up = api.QWeight.from_tiles(dev_u8(up_t), rows, cols)
