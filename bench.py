@@ -128,6 +128,33 @@ class KernelEvent:
             self._hip.hipEventDestroy(self.ev)
 
 
+_BENCH_LIB = None
+
+
+def bench_lib():
+    """libq4rdna_bench_gfx950.so: the measurement kernels (a plain stream
+    read, an empty launch) and the decoder-layer bench's RMS normalization;
+    built beside the GEMV library, not part of its ABI."""
+    global _BENCH_LIB
+    if _BENCH_LIB is None:
+        import ctypes
+        path = os.path.join(ROOT, "rdna-gfx1201-v0.1_amd", "q4rdna", "libq4rdna_bench_gfx950.so")
+        lib = ctypes.CDLL(path)
+        lib.q4bench_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
+        lib.q4bench_empty.argtypes = [ctypes.c_uint32, ctypes.c_void_p]
+        lib.q4bench_rms_norm.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_float,
+                                         ctypes.c_void_p]
+        for f in (lib.q4bench_stream_read, lib.q4bench_empty, lib.q4bench_rms_norm):
+            f.restype = ctypes.c_int
+        _BENCH_LIB = lib
+    return _BENCH_LIB
+
+
+def bench_call(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed: hip error {rc}")
+
+
 def time_plan(plan, steps: int, warmup: int, sample_every: int = 8):
     """Run warmup + timed steps; returns (wall ms per step, sweep ms list,
     prepare ms list).  Every `sample_every`-th timed step carries HIP events
@@ -656,7 +683,7 @@ def layer_chain(tensors, replays: int, check_layers=(0, 17, 35),
     residual h gives x_{l+1}.  The two normalizations stand for the
     decoder's own (without them the N(0, 0.02) weights grow the activations
     quadratically through SwiGLU, to inf within five layers); each is one
-    torch kernel.  Two dispatches over the same weights, each captured into
+    launch of the bench library's RMS-norm kernel.  Two dispatches over the same weights, each captured into
     one HIP graph of all 36 layers and replayed:
       reference  the reference's hooks: q, k, v, o(+add), gate/up SwiGLU,
                  down(+add) as six per-tensor launches (VALU kernel)
@@ -693,8 +720,12 @@ def layer_chain(tensors, replays: int, check_layers=(0, 17, 35),
                           act=torch.empty(12288, device=dev), out=torch.empty(4096, device=dev)))
         return b
 
+    lib = bench_lib()
+
     def norm(x, out):
-        out.copy_(torch.nn.functional.rms_norm(x, (x.numel(),), eps=1e-6))
+        # One launch: out = x * rsqrt(mean(x^2) + 1e-6).
+        bench_call(lib.q4bench_rms_norm(x.data_ptr(), out.data_ptr(), x.numel(), 1e-6,
+                                        torch.cuda.current_stream().cuda_stream), "rms norm")
 
     def run(dispatch, bufs, stream, gemvs=True):
         for l in range(layers):
@@ -786,6 +817,83 @@ def layer_chain(tensors, replays: int, check_layers=(0, 17, 35),
     return out
 
 
+def floors(tensors, data, replays: int = 20):
+    """What the GEMV launches are measured against, from plain reads of the
+    same bytes (bench library kernels; graph replays, each read a different
+    layer's weights, so nothing is served from the 256 MB Infinity Cache):
+      stack_read      one read of the whole 3.69 GB stack buffer: the
+                      streaming ceiling of the plan sweep
+      empty_launch    one empty kernel, replayed from a graph of 100
+      stage_read      per decoder-layer stage (q+k+v, o, gate+up, down): one
+                      plain read of its weight bytes, µs per launch
+      layer_reads     the four stage reads of a layer one after another,
+                      36 layers per graph: the floor of four dependent
+                      launches that each stream their weights once."""
+    import torch
+    lib = bench_lib()
+    sink = torch.zeros(512, dtype=torch.int32, device="cuda")
+    st = torch.cuda.Stream()
+    by = {t["name"]: t for t in tensors}
+    layers = len(tensors) // 7
+
+    def span(l, first, last):
+        a = by[f"blk.{l}.{first}.weight"]["w"].tiles
+        b = by[f"blk.{l}.{last}.weight"]["w"].tiles
+        return a.data_ptr(), b.data_ptr() + b.numel() - a.data_ptr()
+
+    stages = (("q+k+v", "attn_q", "attn_v"), ("o", "attn_output", "attn_output"),
+              ("gate+up", "ffn_gate", "ffn_up"), ("down", "ffn_down", "ffn_down"))
+
+    def read(ptr, nbytes):
+        bench_call(lib.q4bench_stream_read(ptr, nbytes, sink.data_ptr(), st.cuda_stream), "stream read")
+
+    def time_graph(fn, launches):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(st):
+            fn()  # eager once
+            st.synchronize()
+            with torch.cuda.graph(g, stream=st):
+                fn()
+            for _ in range(3):
+                g.replay()
+            a, e = KernelEvent(), KernelEvent()
+            a.record(st.cuda_stream)
+            for _ in range(replays):
+                g.replay()
+            e.record(st.cuda_stream)
+        torch.cuda.synchronize()
+        return a.elapsed_ms(e) * 1000.0 / (replays * launches)
+
+    out = {}
+    nbytes = data.numel()
+    with torch.cuda.stream(st):
+        read(data.data_ptr(), nbytes)
+        st.synchronize()
+        a, e = KernelEvent(), KernelEvent()
+        a.record(st.cuda_stream)
+        for _ in range(5):
+            read(data.data_ptr(), nbytes)
+        e.record(st.cuda_stream)
+    torch.cuda.synchronize()
+    us = a.elapsed_ms(e) * 1000.0 / 5
+    out["stack_read"] = dict(bytes=nbytes, us=round(us, 2), gb_per_s=round(nbytes / us / 1e3, 1))
+    out["empty_launch_us"] = round(time_graph(lambda: bench_call(lib.q4bench_empty(100, st.cuda_stream), "empty"),
+                                              100), 3)
+    stage_out = {}
+    for name, first, last in stages:
+        nb = span(0, first, last)[1]
+        us = time_graph(lambda f=first, la=last: [read(*span(l, f, la)) for l in range(layers)], layers)
+        stage_out[name] = dict(bytes=nb, us=round(us, 2), gb_per_s=round(nb / us / 1e3, 1))
+    out["stage_read"] = stage_out
+    us = time_graph(lambda: [read(*span(l, f, la)) for l in range(layers) for _, f, la in stages], layers)
+    out["layer_reads_us_per_layer"] = round(us, 2)
+    log(f"[floors] stack read {out['stack_read']['us']} us ({out['stack_read']['gb_per_s']} GB/s), "
+        f"empty launch {out['empty_launch_us']} us, four dependent stage reads {us:.2f} us per layer")
+    for name, v in stage_out.items():
+        log(f"[floors] {name}: {v['bytes']} bytes in {v['us']} us ({v['gb_per_s']} GB/s)")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -813,6 +921,9 @@ def main() -> int:
                     help="the stack as dependent decoder layers (q/k/v -> o -> gate/up -> down, 36 layers, HIP graph): "
                          "us per layer for the reference's per-tensor dispatch and for the grouped dispatch; prints one "
                          "JSON line instead of the stack bench")
+    ap.add_argument("--floors", action="store_true",
+                    help="plain-read and launch floors (stack read, empty launch, per-stage reads and four "
+                         "dependent stage reads per layer); prints one JSON line instead of the stack bench")
     ap.add_argument("--tensors", action="store_true",
                     help="per-tensor launch figures (projection shapes, lm_head, long-K split sweep with "
                          "outlier groups); prints one JSON line with the table instead of the stack bench")
@@ -833,6 +944,9 @@ def main() -> int:
     stack_bytes = sum(algorithmic_bytes(t["rows"], t["cols"]) for t in tensors)
     if args.layer_chain:
         print(json.dumps({"layer_chain": layer_chain(tensors, max(args.steps, 20))}), flush=True)
+        return 0
+    if args.floors:
+        print(json.dumps({"floors": floors(tensors, _data)}), flush=True)
         return 0
     if args.batches:
         sizes = [int(v) for v in args.batches.split(",") if v]

@@ -1,0 +1,89 @@
+// Measurement kernels for bench.py (libq4rdna_bench_gfx950.so).  They are not
+// part of the GEMV library or its C ABI: they give the figures the GEMV
+// kernels are compared with (a plain read of the same bytes, an empty
+// launch) and the RMS normalization the decoder-layer bench puts between
+// layers.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "q4rdna_device.h"
+
+namespace {
+
+constexpr int kReadThreads = 512;
+constexpr int kReadLoads = 16;  // dword loads per thread, all in flight: 32 KB per workgroup
+constexpr uint64_t kReadChunk = static_cast<uint64_t>(kReadThreads) * kReadLoads * 4;
+
+// Workgroup b (remapped so consecutive chunks share an XCD) reads bytes
+// [b * 32 KB, (b + 1) * 32 KB) with nontemporal dword loads, each load of a
+// wave one contiguous 256-byte run; past the end the index is clamped, so
+// every load is issued unconditionally.  The XOR of the data is stored only
+// when `flag` is set and it equals a constant the caller never passes, so
+// the loads cannot be dropped and nothing is written.
+__global__ __launch_bounds__(kReadThreads) void stream_read_kernel(const uint32_t *__restrict__ p, uint64_t words,
+                                                                   uint32_t *sink, uint32_t flag) {
+    const uint64_t b = q4rdna::xcd_remap(blockIdx.x, gridDim.x);
+    const uint64_t base = b * (kReadChunk / 4) + threadIdx.x;
+    uint32_t v[kReadLoads];
+#pragma unroll
+    for (int i = 0; i < kReadLoads; ++i) {
+        const uint64_t w = base + static_cast<uint64_t>(i) * kReadThreads;
+        v[i] = __builtin_nontemporal_load((q4rdna::gptr_u32)(p + (w < words ? w : words - 1)));
+    }
+    uint32_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < kReadLoads; ++i) acc ^= v[i];
+    if (flag != 0 && acc == flag) sink[threadIdx.x] = acc;
+}
+
+__global__ void empty_kernel() {}
+
+// y = x * rsqrt(mean(x^2) + eps) by one workgroup of 1024 threads.
+constexpr int kNormThreads = 1024;
+__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                                                uint32_t n, float eps) {
+    __shared__ float part[kNormThreads / 64];
+    float s = 0.f;
+    for (uint32_t i = threadIdx.x; i < n; i += kNormThreads) s = fmaf(x[i], x[i], s);
+    s = q4rdna::add_over_a(s);  // lanes sharing lane & 7
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < kNormThreads / 64; ++w) t += part[w];
+    const float r = rsqrtf(t / static_cast<float>(n) + eps);
+    for (uint32_t i = threadIdx.x; i < n; i += kNormThreads) y[i] = x[i] * r;
+}
+
+}  // namespace
+
+extern "C" {
+
+// Reads `bytes` (a multiple of 4, at least 4) at p once; sink is 512 words
+// that are never written in practice.
+int q4bench_stream_read(const void *p, uint64_t bytes, uint32_t *sink, hipStream_t stream) {
+    if (p == nullptr || sink == nullptr || bytes < 4 || bytes % 4 != 0) return static_cast<int>(hipErrorInvalidValue);
+    const uint64_t blocks = (bytes + kReadChunk - 1) / kReadChunk;
+    if (blocks > 0x7fffffffull) return static_cast<int>(hipErrorInvalidValue);
+    hipLaunchKernelGGL(stream_read_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kReadThreads), 0, stream,
+                       static_cast<const uint32_t *>(p), bytes / 4, sink, 0u);
+    return static_cast<int>(hipGetLastError());
+}
+
+// `launches` launches of an empty one-wave kernel.
+int q4bench_empty(uint32_t launches, hipStream_t stream) {
+    for (uint32_t i = 0; i < launches; ++i) hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, stream);
+    return static_cast<int>(hipGetLastError());
+}
+
+// y[n] = x * rsqrt(mean(x^2) + eps), fp32, one launch.
+int q4bench_rms_norm(const float *x, float *y, uint32_t n, float eps, hipStream_t stream) {
+    if (x == nullptr || y == nullptr || n == 0) return static_cast<int>(hipErrorInvalidValue);
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(1), dim3(kNormThreads), 0, stream, x, y, n, eps);
+    return static_cast<int>(hipGetLastError());
+}
+
+}  // extern "C"
