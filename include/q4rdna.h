@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define Q4RDNA_ABI_VERSION 2
+#define Q4RDNA_ABI_VERSION 3
 
 /* status codes */
 #define Q4RDNA_OK 0
@@ -149,10 +149,20 @@ int q4rdna_mul_mat_glu(const q4rdna_weight *up, const q4rdna_weight *gate, const
  * the per-tensor kernel (0 = the shape policy, the reference's launch policy
  * at source/q4rdna.cu:578-680 and its LLAMA_Q4_RDNA_COOP override
  * :579-584); kernel = Q4RDNA_KERNEL_POLICY or Q4RDNA_KERNEL_VALU (the same
- * kernel; any other value is an argument error); reserved words must be
+ * kernel) or Q4RDNA_KERNEL_SEQUENTIAL (any other value, 2 included, which
+ * ABI 1 used for a kernel since withdrawn, is an argument error); reserved
+ * words must be
  * zero.  Zero-initialised options mean "policy" throughout. */
 #define Q4RDNA_KERNEL_POLICY 0
 #define Q4RDNA_KERNEL_VALU 1 /* the split-K VALU kernel (split_k applies) */
+/* The reference's old mapping (LLAMA_Q4_RDNA_MAPPING=old, source/q4rdna.cu:
+ * 190-234,626-634): one thread per row, its weights in k order, one fp32 fma
+ * each, so y is bit for bit the reference bench's CPU loop
+ * (source/q4rdna_gemv_bench.hip:189-210) before the epilogue.  split_k must be 0
+ * or 1; q4rdna_mul_mat_batch runs it once per vector, q4rdna_mul_mat_group
+ * refuses it (argument error).  Slow: an ablation and a bit-exact
+ * reference, not a decode path. */
+#define Q4RDNA_KERNEL_SEQUENTIAL 3
 typedef struct q4rdna_launch_options {
     uint32_t split_k;
     uint32_t kernel;
@@ -278,6 +288,22 @@ int q4rdna_plan_sweep(q4rdna_plan *plan, void *stream);
 void q4rdna_plan_destroy(q4rdna_plan *plan);
 /* Workgroups the plan launches (persistent grid). */
 uint32_t q4rdna_plan_workgroups(const q4rdna_plan *plan);
+
+/* Launch statistics, the reference's q4rdna_launches and per-entry hits
+ * (source/q4rdna.cu:57,73,706-709,742,764,789-791).  Every GEMV kernel
+ * launch the entry points above make counts once (q4rdna_mul_mat_batch's
+ * per-vector launches one each, a plan's sweep once), and every weight it
+ * streams that starts an entry of an open sidecar counts a hit for that
+ * entry (a SwiGLU launch hits both weights). */
+uint64_t q4rdna_launch_count(void);
+/* Hits of entry `index` of `sidecar` (0 for an invalid pair). */
+uint64_t q4rdna_sidecar_hits(const q4rdna_sidecar *sidecar, uint32_t index);
+/* The reference's report on stderr (source/q4rdna.cu:75-112, same lines):
+ * "Q4_RDNA: launched N decode GEMV kernels", with LLAMA_Q4_RDNA_TRACE set
+ * one "Q4_RDNA: hit <name> <hits>" line per entry that was hit, and the
+ * unique / hits-by-shape summary, over every open sidecar.  Printed at
+ * process exit once q4rdna_default_sidecar has loaded (source/q4rdna.cu:176). */
+void q4rdna_report_stats(void);
 
 /* ---- packing and dequantisation ------------------------------------------
  * Quantize fp32 W[rows][columns] (device, row-major) into tiles (device) with

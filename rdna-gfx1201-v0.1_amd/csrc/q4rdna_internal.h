@@ -91,6 +91,9 @@ inline bool gemv_shape_fits(uint64_t row_tiles, uint64_t groups, uint64_t split)
     return row_tiles * split * split < (uint64_t{1} << 32) && groups * split * split < (uint64_t{1} << 32);
 }
 hipError_t launch_gemv(const GemvArgs &args, hipStream_t stream);
+// The reference's old mapping, one thread per row in k order (split 1; the
+// split-K fields are unused).
+hipError_t launch_gemv_sequential(const GemvArgs &args, hipStream_t stream);
 // GemvArgs::short_waves for rows of `groups` groups split into `split` K
 // chunks, `workgroups` in all on `cus` CUs.
 uint32_t gemv_waves(uint32_t groups, uint32_t split, uint64_t workgroups, uint32_t cus);

@@ -309,6 +309,12 @@ __device__ __forceinline__ void tile_row_partial_short(Sh &sh, const uint8_t *__
             }
         }
     }
+    // Every wave's x loads are issued before any wave's tile loads (a bare
+    // barrier, no wait for the loads): loads return in issue order, so
+    // otherwise the last wave's x, which staging waits for, queues behind
+    // the other waves' tiles.
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     TileRegs t[T], u[T];
 #pragma unroll
@@ -505,6 +511,12 @@ __global__ __launch_bounds__(64 * kMvWaves) void gemv_multi_kernel(GemvArgs args
             }
         }
     }
+    // Every wave's x loads are issued before any wave's tile loads (a bare
+    // barrier, no wait for the loads): loads return in issue order, so
+    // otherwise the last wave's x, which staging waits for, queues behind
+    // the other waves' tiles.
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     TileRegs t[T], u[T];
 #pragma unroll
@@ -606,6 +618,51 @@ __global__ __launch_bounds__(64 * kMvWaves) void gemv_multi_kernel(GemvArgs args
         args.y[v * M + row] = epilogue<GATE, ADD>(sum, gsum, args.add ? args.add + v * M : nullptr, row);
     }
     if (threadIdx.x == 0) store_agent(&args.counters[rt], 0u);
+}
+
+// The reference's old mapping (source/q4rdna.cu:190-234, selected there by
+// LLAMA_Q4_RDNA_MAPPING=old): one thread per row, its weights in k order,
+// one fp32 fma each, sum = fma(scale * q, x_k, sum) -- the CPU loop's
+// arithmetic step for step, so the result is its bits.  x is staged one
+// group at a time in LDS; rows past the end compute a stand-in row and
+// store nothing (every thread reaches the barriers).
+constexpr int kSeqThreads = 256;
+template <bool GATE, bool ADD>
+__global__ __launch_bounds__(kSeqThreads) void gemv_sequential_kernel(GemvArgs args) {
+    __shared__ float xs[kGroup];
+    const uint32_t groups = args.cols / kGroup;
+    const uint32_t row = blockIdx.x * kSeqThreads + threadIdx.x;
+    const uint32_t r = min(row, args.rows - 1);
+    const uint32_t rt = r / kTileRows, lane = r % kTileRows;
+    const uint8_t *wt = args.w + static_cast<size_t>(rt) * groups * kTileBytes;
+    const uint8_t *gt = GATE ? args.gate + static_cast<size_t>(rt) * groups * kTileBytes : nullptr;
+    float sum = 0.f, gsum = 0.f;
+    for (uint32_t g = 0; g < groups; ++g) {
+        __syncthreads();
+        if (threadIdx.x < kGroup) xs[threadIdx.x] = args.x[static_cast<size_t>(g) * kGroup + threadIdx.x];
+        __syncthreads();
+        const uint8_t *tile = wt + static_cast<size_t>(g) * kTileBytes;
+        const float scale = half_bits_to_float(tile[2 * lane] | (static_cast<uint32_t>(tile[2 * lane + 1]) << 8));
+        float gscale = 0.f;
+        if constexpr (GATE)
+            gscale = half_bits_to_float(gt[static_cast<size_t>(g) * kTileBytes + 2 * lane] |
+                                        (static_cast<uint32_t>(gt[static_cast<size_t>(g) * kTileBytes + 2 * lane + 1]) << 8));
+        for (int i = 0; i < static_cast<int>(kGroup / 2); ++i) {
+            const uint8_t b = tile[64 + kTileRows * i + lane];
+            const int lo = static_cast<int>(static_cast<int8_t>(static_cast<uint8_t>(b << 4))) >> 4;
+            const int hi = static_cast<int>(static_cast<int8_t>(b)) >> 4;
+            sum = fmaf(scale * static_cast<float>(lo), xs[2 * i], sum);
+            sum = fmaf(scale * static_cast<float>(hi), xs[2 * i + 1], sum);
+            if constexpr (GATE) {
+                const uint8_t gb = gt[static_cast<size_t>(g) * kTileBytes + 64 + kTileRows * i + lane];
+                const int glo = static_cast<int>(static_cast<int8_t>(static_cast<uint8_t>(gb << 4))) >> 4;
+                const int ghi = static_cast<int>(static_cast<int8_t>(gb)) >> 4;
+                gsum = fmaf(gscale * static_cast<float>(glo), xs[2 * i], gsum);
+                gsum = fmaf(gscale * static_cast<float>(ghi), xs[2 * i + 1], gsum);
+            }
+        }
+    }
+    if (row < args.rows) args.y[row] = epilogue<GATE, ADD>(sum, gsum, args.add, row);
 }
 
 // out[row][k] = fp32(scale) * code, one thread per code byte.
@@ -977,6 +1034,18 @@ hipError_t launch_gemv_multi(const GemvArgs &args, hipStream_t stream) {
     }
     return args.add != nullptr ? launch_multi_t<false, true>(args, stream)
                                : launch_multi_t<false, false>(args, stream);
+}
+
+hipError_t launch_gemv_sequential(const GemvArgs &args, hipStream_t stream) {
+    const dim3 grid((args.rows + kSeqThreads - 1) / kSeqThreads), block(kSeqThreads);
+    if (args.gate != nullptr) {
+        if (args.add != nullptr) hipLaunchKernelGGL((gemv_sequential_kernel<true, true>), grid, block, 0, stream, args);
+        else hipLaunchKernelGGL((gemv_sequential_kernel<true, false>), grid, block, 0, stream, args);
+    } else {
+        if (args.add != nullptr) hipLaunchKernelGGL((gemv_sequential_kernel<false, true>), grid, block, 0, stream, args);
+        else hipLaunchKernelGGL((gemv_sequential_kernel<false, false>), grid, block, 0, stream, args);
+    }
+    return hipGetLastError();
 }
 
 uint32_t gemv_multi_stage_groups(uint32_t vectors) { return vectors > 4 ? 16u : 32u; }

@@ -75,8 +75,11 @@ extern "C" int q4rdna_mul_mat_ex_noalloc(const q4rdna_weight *w, const q4rdna_we
     if (rc != Q4RDNA_OK) return rc;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const uint8_t *gt = gate ? gate->tiles : nullptr;
-    if (L.partial_floats == 0 && L.counters == 0 && L.slots == 0)
-        return q4rdna::launch_tensor_in(L, w, gt, x, add, y, nullptr, nullptr, nullptr, s);
+    if (L.partial_floats == 0 && L.counters == 0 && L.slots == 0) {
+        if ((rc = q4rdna::launch_tensor_in(L, w, gt, x, add, y, nullptr, nullptr, nullptr, s)) == Q4RDNA_OK)
+            q4rdna::count_gemv_launch(w->tiles, gt);
+        return rc;
+    }
     if (L.partial_floats > Q4RDNA_NOALLOC_PARTIAL_FLOATS || L.counters > Q4RDNA_NOALLOC_COUNTERS ||
         L.slots > Q4RDNA_NOALLOC_SLOTS)
         return q4rdna::set_error(Q4RDNA_ERR_ARGUMENT,
@@ -88,7 +91,9 @@ extern "C" int q4rdna_mul_mat_ex_noalloc(const q4rdna_weight *w, const q4rdna_we
                                  static_cast<unsigned>(Q4RDNA_NOALLOC_SLOTS));
     uint8_t *base = nullptr;
     if ((rc = scratch_of(w->device, &base)) != Q4RDNA_OK) return rc;
-    return q4rdna::launch_tensor_in(L, w, gt, x, add, y, reinterpret_cast<float *>(base),
-                                    reinterpret_cast<uint32_t *>(base + kPartialBytes),
-                                    reinterpret_cast<uint32_t *>(base + kPartialBytes + kCounterBytes), s);
+    rc = q4rdna::launch_tensor_in(L, w, gt, x, add, y, reinterpret_cast<float *>(base),
+                                  reinterpret_cast<uint32_t *>(base + kPartialBytes),
+                                  reinterpret_cast<uint32_t *>(base + kPartialBytes + kCounterBytes), s);
+    if (rc == Q4RDNA_OK) q4rdna::count_gemv_launch(w->tiles, gt);
+    return rc;
 }

@@ -227,7 +227,9 @@ int check_io(const float *x, const float *y) {
 // policy, which is that kernel) and the reserved words are zero.
 int check_options(const q4rdna_launch_options *options) {
     if (options == nullptr) return Q4RDNA_OK;
-    if (options->kernel > Q4RDNA_KERNEL_VALU) return set_error(Q4RDNA_ERR_ARGUMENT, "unknown kernel %u", options->kernel);
+    if (options->kernel != Q4RDNA_KERNEL_POLICY && options->kernel != Q4RDNA_KERNEL_VALU &&
+        options->kernel != Q4RDNA_KERNEL_SEQUENTIAL)
+        return set_error(Q4RDNA_ERR_ARGUMENT, "unknown kernel %u", options->kernel);
     for (uint32_t r : options->reserved)
         if (r != 0) return set_error(Q4RDNA_ERR_ARGUMENT, "reserved launch options must be zero");
     return Q4RDNA_OK;
@@ -252,6 +254,14 @@ int check_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const fl
     if (s > kMaxSplit) return set_error(Q4RDNA_ERR_ARGUMENT, "split_k %u exceeds %u", s, kMaxSplit);
     if ((rc = check_options(options)) != Q4RDNA_OK) return rc;
     TensorLaunch L{};
+    if (options != nullptr && options->kernel == Q4RDNA_KERNEL_SEQUENTIAL) {
+        // The old mapping sums each row in one thread: no K chunks.
+        if (s > 1) return set_error(Q4RDNA_ERR_ARGUMENT, "the sequential kernel takes split_k 0 or 1, not %u", s);
+        L.split = 1;
+        L.sequential = true;
+        *launch = L;
+        return Q4RDNA_OK;
+    }
     L.split = resolve_split(w, s);
     if (!gemv_shape_fits(w->rows / kTileRows, w->columns / kGroup, L.split))
         return set_error(Q4RDNA_ERR_ARGUMENT, "shape %ux%u at split %u is beyond the kernels' index range", w->rows,
@@ -288,7 +298,7 @@ int launch_tensor_in(const TensorLaunch &launch, const q4rdna_weight *w, const u
         args.partial = partial;
         args.counters = counters;
     }
-    const hipError_t e = launch_gemv(args, stream);
+    const hipError_t e = launch.sequential ? launch_gemv_sequential(args, stream) : launch_gemv(args, stream);
     if (e != hipSuccess) return hip_fail(e, "GEMV launch");
     return Q4RDNA_OK;
 }
@@ -302,10 +312,13 @@ struct q4rdna_sidecar {
     uint64_t data_bytes = 0;
     std::vector<Entry> entries;
     std::unordered_map<std::string, uint32_t> by_name;
+    std::vector<uint32_t> by_offset;                  // entry indices in data order
+    std::unique_ptr<std::atomic<uint64_t>[]> hits;    // GEMV launches per entry
 };
 
 struct q4rdna_plan {
     int device = 0;
+    std::vector<const uint8_t *> weights;  // every GEMV's tiles (and gate tiles): the launch's hits
     q4rdna::PlanDesc *descs = nullptr;  // count + 1 (sentinel)
     uint8_t *scratch = nullptr;         // activation digits, split-K partials and counters
     uint32_t *sched = nullptr;          // batched sweeps' [next item, finished workgroups], zero between launches
@@ -319,6 +332,59 @@ struct q4rdna_plan {
     bool both_streams = false;  // some SwiGLU GEMV runs both weight streams in one item
 };
 
+
+namespace {
+
+// Launch statistics, the reference's q4rdna_launches and per-entry hits
+// (source/q4rdna.cu:57,73,706-709,742,764,789-791): every GEMV launch an
+// entry point makes counts once, and each weight it streams that starts a
+// sidecar entry counts a hit for that entry (a SwiGLU launch hits both).
+std::atomic<uint64_t> g_launches{0};
+std::mutex g_stats_mutex;
+std::vector<q4rdna_sidecar *> g_open;  // sidecars whose entries count hits
+
+void register_sidecar(q4rdna_sidecar *sc) {
+    std::lock_guard<std::mutex> lock(g_stats_mutex);
+    g_open.push_back(sc);
+}
+
+void unregister_sidecar(q4rdna_sidecar *sc) {
+    std::lock_guard<std::mutex> lock(g_stats_mutex);
+    g_open.erase(std::remove(g_open.begin(), g_open.end(), sc), g_open.end());
+}
+
+// One launch over `n` weights (null entries skipped).  No allocation, so
+// the allocation-free entry point may count too.
+void count_launch(const uint8_t *const *tiles, size_t n, uint64_t launches = 1) {
+    g_launches.fetch_add(launches, std::memory_order_relaxed);
+    std::lock_guard<std::mutex> lock(g_stats_mutex);
+    for (size_t i = 0; i < n; ++i) {
+        const uint8_t *t = tiles[i];
+        if (t == nullptr) continue;
+        for (q4rdna_sidecar *sc : g_open) {
+            if (sc->data == nullptr || t < sc->data || t >= sc->data + sc->data_bytes) continue;
+            const uint64_t rel = static_cast<uint64_t>(t - sc->data) + sc->data_offset;
+            const auto it = std::lower_bound(sc->by_offset.begin(), sc->by_offset.end(), rel,
+                                             [&](uint32_t idx, uint64_t v) { return sc->entries[idx].offset < v; });
+            if (it != sc->by_offset.end() && sc->entries[*it].offset == rel)
+                sc->hits[*it].fetch_add(launches, std::memory_order_relaxed);
+            break;
+        }
+    }
+}
+
+void count_launch(const uint8_t *a, const uint8_t *b = nullptr, uint64_t launches = 1) {
+    const uint8_t *t[2] = {a, b};
+    count_launch(t, 2, launches);
+}
+
+void report_at_exit() { q4rdna_report_stats(); }
+
+}  // namespace
+
+namespace q4rdna {
+void count_gemv_launch(const uint8_t *w, const uint8_t *gate) { count_launch(w, gate); }
+}  // namespace q4rdna
 
 namespace {
 
@@ -356,6 +422,12 @@ int finish_open(const FileHeader &h, std::vector<Entry> &&entries, int device, R
     }
     sc->entries = std::move(entries);
     for (uint32_t i = 0; i < sc->entries.size(); ++i) sc->by_name.emplace(sc->entries[i].name, i);
+    sc->by_offset.resize(sc->entries.size());
+    for (uint32_t i = 0; i < sc->entries.size(); ++i) sc->by_offset[i] = i;
+    std::sort(sc->by_offset.begin(), sc->by_offset.end(),
+              [&](uint32_t a, uint32_t b) { return sc->entries[a].offset < sc->entries[b].offset; });
+    sc->hits.reset(new std::atomic<uint64_t>[sc->entries.size()]());
+    register_sidecar(sc.get());
     *out = sc.release();
     return Q4RDNA_OK;
 }
@@ -420,6 +492,7 @@ int q4rdna_sidecar_open_memory(const void *image, uint64_t size, int device, q4r
 
 void q4rdna_sidecar_close(q4rdna_sidecar *sidecar) {
     if (sidecar == nullptr) return;
+    unregister_sidecar(sidecar);
     if (sidecar->data != nullptr) {
         DeviceGuard guard(sidecar->device);
         (void)hipFree(sidecar->data);
@@ -490,6 +563,9 @@ q4rdna_sidecar *q4rdna_default_sidecar(int device) {
                      static_cast<unsigned>(sc->entries.size()),
                      static_cast<double>(sc->data_bytes) / (1024.0 * 1024.0 * 1024.0), device, path);
         value = sc;
+        // The reference reports its launches when the process exits
+        // (source/q4rdna.cu:176).
+        std::atexit(report_at_exit);
     });
     if (value == nullptr || value->device != device) return nullptr;
     return value;
@@ -523,7 +599,9 @@ int q4rdna_mul_mat(const q4rdna_weight *w, const float *x, int64_t x_ne0, float 
                     static_cast<long long>(x_ne0), w->columns, static_cast<long long>(y_ne0), w->rows);
     q4rdna::TensorLaunch L{};
     if ((rc = q4rdna::check_mul_mat_ex(w, nullptr, x, nullptr, y, nullptr, &L)) != Q4RDNA_OK) return rc;
-    return launch_one(L, w, nullptr, x, nullptr, y, static_cast<hipStream_t>(stream));
+    if ((rc = launch_one(L, w, nullptr, x, nullptr, y, static_cast<hipStream_t>(stream))) == Q4RDNA_OK)
+        count_launch(w->tiles);
+    return rc;
 }
 
 int q4rdna_mul_mat_add(const q4rdna_weight *w, const float *x, int64_t x_ne0, const float *add, int64_t add_ne,
@@ -536,7 +614,9 @@ int q4rdna_mul_mat_add(const q4rdna_weight *w, const float *x, int64_t x_ne0, co
     if (add == nullptr) return set_error(Q4RDNA_ERR_ARGUMENT, "NULL add");
     q4rdna::TensorLaunch L{};
     if ((rc = q4rdna::check_mul_mat_ex(w, nullptr, x, add, y, nullptr, &L)) != Q4RDNA_OK) return rc;
-    return launch_one(L, w, nullptr, x, add, y, static_cast<hipStream_t>(stream));
+    if ((rc = launch_one(L, w, nullptr, x, add, y, static_cast<hipStream_t>(stream))) == Q4RDNA_OK)
+        count_launch(w->tiles);
+    return rc;
 }
 
 int q4rdna_mul_mat_glu(const q4rdna_weight *up, const q4rdna_weight *gate, const float *x, int64_t x_ne0, int glu_op,
@@ -551,7 +631,9 @@ int q4rdna_mul_mat_glu(const q4rdna_weight *up, const q4rdna_weight *gate, const
         return set_error(Q4RDNA_NOT_APPLICABLE, "shape mismatch");
     q4rdna::TensorLaunch L{};
     if ((rc = q4rdna::check_mul_mat_ex(up, gate, x, nullptr, y, nullptr, &L)) != Q4RDNA_OK) return rc;
-    return launch_one(L, up, gate->tiles, x, nullptr, y, static_cast<hipStream_t>(stream));
+    if ((rc = launch_one(L, up, gate->tiles, x, nullptr, y, static_cast<hipStream_t>(stream))) == Q4RDNA_OK)
+        count_launch(up->tiles, gate->tiles);
+    return rc;
 }
 
 int q4rdna_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x, const float *add, float *y,
@@ -559,7 +641,10 @@ int q4rdna_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const f
     q4rdna::TensorLaunch L{};
     int rc = q4rdna::check_mul_mat_ex(w, gate, x, add, y, options, &L);
     if (rc != Q4RDNA_OK) return rc;
-    return launch_one(L, w, gate ? gate->tiles : nullptr, x, add, y, static_cast<hipStream_t>(stream));
+    if ((rc = launch_one(L, w, gate ? gate->tiles : nullptr, x, add, y, static_cast<hipStream_t>(stream))) ==
+        Q4RDNA_OK)
+        count_launch(w->tiles, gate ? gate->tiles : nullptr);
+    return rc;
 }
 
 namespace {
@@ -671,7 +756,17 @@ int q4rdna_mul_mat_group(const q4rdna_group_desc *descs, uint32_t count, const f
     const uint32_t split_k = options ? options->split_k : 0;
     if (split_k > kMaxSplit) return set_error(Q4RDNA_ERR_ARGUMENT, "split_k %u exceeds %u", split_k, kMaxSplit);
     if ((rc = check_options(options)) != Q4RDNA_OK) return rc;
-    return launch_group_valu(descs, count, x, glu, split_k, static_cast<hipStream_t>(stream));
+    if (options != nullptr && options->kernel == Q4RDNA_KERNEL_SEQUENTIAL)
+        return set_error(Q4RDNA_ERR_ARGUMENT, "a group launch runs the split-K kernel, not the sequential one");
+    if ((rc = launch_group_valu(descs, count, x, glu, split_k, static_cast<hipStream_t>(stream))) == Q4RDNA_OK) {
+        const uint8_t *t[2 * Q4RDNA_MAX_GROUP];
+        for (uint32_t i = 0; i < count; ++i) {
+            t[2 * i] = descs[i].weight.tiles;
+            t[2 * i + 1] = descs[i].gate_tiles;
+        }
+        count_launch(t, 2 * count);
+    }
+    return rc;
 }
 
 int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x, uint32_t n,
@@ -687,22 +782,26 @@ int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, cons
     if (n < 1 || n > Q4RDNA_MAX_BATCH) return set_error(Q4RDNA_ERR_ARGUMENT, "batch %u is outside 1..%d", n, Q4RDNA_MAX_BATCH);
     uint32_t split = options ? options->split_k : 0;
     if (split > kMaxSplit) return set_error(Q4RDNA_ERR_ARGUMENT, "split_k %u exceeds %u", split, kMaxSplit);
+    if ((rc = check_options(options)) != Q4RDNA_OK) return rc;
+    const bool sequential = options != nullptr && options->kernel == Q4RDNA_KERNEL_SEQUENTIAL;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const uint8_t *gt = gate ? gate->tiles : nullptr;
     const uint32_t groups = w->columns / kGroup;
     // Every K chunk of the n-vector kernel fits its x stage.  Longer rows than
-    // 64 such chunks go one launch per vector.
+    // 64 such chunks, and the sequential kernel, go one launch per vector.
     const uint32_t stage = q4rdna::gemv_multi_stage_groups(n);
     const uint32_t need = (groups + stage - 1) / stage;
-    if (n == 1 || need > std::min(groups, kMaxSplit)) {
+    if (n == 1 || sequential || need > std::min(groups, kMaxSplit)) {
         const size_t M = w->rows, K = w->columns;
         q4rdna_launch_options one{};
         one.split_k = split;
+        one.kernel = options ? options->kernel : Q4RDNA_KERNEL_POLICY;
         q4rdna::TensorLaunch L{};
         if ((rc = q4rdna::check_mul_mat_ex(w, gate, x, add, y, &one, &L)) != Q4RDNA_OK) return rc;
         for (uint32_t v = 0; v < n; ++v)
             if ((rc = launch_one(L, w, gt, x + v * K, add ? add + v * M : nullptr, y + v * M, s)) != Q4RDNA_OK)
                 return rc;
+        count_launch(w->tiles, gt, n);
         return Q4RDNA_OK;
     }
     if (split == 0) split = policy_split(w->rows, w->columns, w->device);
@@ -730,6 +829,7 @@ int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, cons
     }
     hipError_t e = q4rdna::launch_gemv_multi(args, s);
     if (e != hipSuccess) return hip_fail(e, "batched GEMV launch");
+    count_launch(w->tiles, gt);
     return Q4RDNA_OK;
 }
 
@@ -754,6 +854,10 @@ int q4rdna_plan_create_batch(const q4rdna_gemv_desc *descs, uint32_t count, uint
     plan->batch = n;
     plan->both_streams = L.both_streams;
     plan->count = count;
+    for (uint32_t i = 0; i < count; ++i) {
+        plan->weights.push_back(descs[i].weight.tiles);
+        if (descs[i].gate_tiles != nullptr) plan->weights.push_back(descs[i].gate_tiles);
+    }
     plan->items = L.items;
     plan->groups = L.groups;
     plan->workgroups = L.workgroups;
@@ -827,6 +931,7 @@ int q4rdna_plan_sweep(q4rdna_plan *plan, void *stream) {
                        : q4rdna::launch_plan_batch(plan->descs, plan->items, plan->batch, plan->workgroups,
                                                    plan->sched, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "plan sweep launch");
+    count_launch(plan->weights.data(), plan->weights.size());
     return Q4RDNA_OK;
 }
 
@@ -846,6 +951,46 @@ void q4rdna_plan_destroy(q4rdna_plan *plan) {
 }
 
 uint32_t q4rdna_plan_workgroups(const q4rdna_plan *plan) { return plan ? plan->workgroups : 0u; }
+
+uint64_t q4rdna_launch_count(void) { return g_launches.load(std::memory_order_relaxed); }
+
+uint64_t q4rdna_sidecar_hits(const q4rdna_sidecar *sidecar, uint32_t index) {
+    if (sidecar == nullptr || index >= sidecar->entries.size()) return 0;
+    return sidecar->hits[index].load(std::memory_order_relaxed);
+}
+
+// The reference's report (source/q4rdna.cu:75-112), in its words and
+// shape buckets, over the entries of every open sidecar in data order.
+void q4rdna_report_stats(void) {
+    const uint64_t launches = g_launches.load(std::memory_order_relaxed);
+    if (launches != 0)
+        std::fprintf(stderr, "Q4_RDNA: launched %llu decode GEMV kernels\n", static_cast<unsigned long long>(launches));
+    const bool trace = std::getenv("LLAMA_Q4_RDNA_TRACE") != nullptr;
+    uint64_t s12288_4096 = 0, s4096_12288 = 0, s4096_4096 = 0, s1024_4096 = 0, other = 0;
+    uint32_t unique = 0;
+    std::lock_guard<std::mutex> lock(g_stats_mutex);
+    for (const q4rdna_sidecar *sc : g_open) {
+        for (uint32_t idx : sc->by_offset) {
+            const Entry &e = sc->entries[idx];
+            const uint64_t hits = sc->hits[idx].load(std::memory_order_relaxed);
+            if (hits == 0) continue;
+            ++unique;
+            if (e.rows == 12288 && e.columns == 4096) s12288_4096 += hits;
+            else if (e.rows == 4096 && e.columns == 12288) s4096_12288 += hits;
+            else if (e.rows == 4096 && e.columns == 4096) s4096_4096 += hits;
+            else if (e.rows == 1024 && e.columns == 4096) s1024_4096 += hits;
+            else other += hits;
+            if (trace)
+                std::fprintf(stderr, "Q4_RDNA: hit %-31s %llu\n", e.name.c_str(), static_cast<unsigned long long>(hits));
+        }
+    }
+    std::fprintf(stderr,
+                 "Q4_RDNA: unique=%u, hits by rows x columns: 12288x4096=%llu, 4096x12288=%llu, "
+                 "4096x4096=%llu, 1024x4096=%llu, other=%llu\n",
+                 unique, static_cast<unsigned long long>(s12288_4096), static_cast<unsigned long long>(s4096_12288),
+                 static_cast<unsigned long long>(s4096_4096), static_cast<unsigned long long>(s1024_4096),
+                 static_cast<unsigned long long>(other));
+}
 
 int q4rdna_pack(const float *w, uint32_t rows, uint32_t columns, int algorithm, uint8_t *tiles, void *stream) {
     if (w == nullptr || tiles == nullptr) return set_error(Q4RDNA_ERR_ARGUMENT, "NULL input or output");

@@ -22,6 +22,7 @@ struct TensorLaunch {
     size_t partial_floats;
     size_t counters;
     size_t slots;
+    bool sequential;  // Q4RDNA_KERNEL_SEQUENTIAL: split 1, no workspace
 };
 
 // Validate q4rdna_mul_mat_ex's arguments (the same statuses as that entry
@@ -33,6 +34,11 @@ int check_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const fl
 // least launch.partial_floats floats, launch.counters counters and
 // launch.slots slot words (each ignored when its count is zero); counters
 // and slots zero on entry, both left zero.
+// Count one GEMV launch over W (and its SwiGLU gate, may be null) in the
+// library's launch statistics (q4rdna_launch_count, q4rdna_sidecar_hits).
+// Allocates nothing.
+void count_gemv_launch(const uint8_t *w, const uint8_t *gate);
+
 int launch_tensor_in(const TensorLaunch &launch, const q4rdna_weight *w, const uint8_t *gate, const float *x,
                      const float *add, float *y, float *partial, uint32_t *counters, uint32_t *slots,
                      hipStream_t stream);

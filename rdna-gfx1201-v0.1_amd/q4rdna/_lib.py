@@ -45,6 +45,7 @@ EXPORTS = (
     "q4rdna_plan_prepare",
     "q4rdna_plan_sweep", "q4rdna_plan_destroy",
     "q4rdna_plan_workgroups", "q4rdna_pack", "q4rdna_dequantize",
+    "q4rdna_launch_count", "q4rdna_sidecar_hits", "q4rdna_report_stats",
 )
 
 
@@ -63,6 +64,7 @@ class Weight(ctypes.Structure):
 
 KERNEL_POLICY = 0
 KERNEL_VALU = 1
+KERNEL_SEQUENTIAL = 3
 MAX_GROUP = 8
 
 
@@ -124,6 +126,9 @@ def load() -> ctypes.CDLL:
         "q4rdna_plan_workgroups": (u32, [vp]),
         "q4rdna_pack": (i32, [vp, u32, u32, i32, vp, vp]),
         "q4rdna_dequantize": (i32, [WP, vp, vp]),
+        "q4rdna_launch_count": (u64, []),
+        "q4rdna_sidecar_hits": (u64, [vp, u32]),
+        "q4rdna_report_stats": (None, []),
     }
     for name, (res, args) in proto.items():
         fn = getattr(L, name)

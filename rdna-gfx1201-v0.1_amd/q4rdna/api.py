@@ -131,7 +131,8 @@ def mul_mat_ex(w: QWeight, x: torch.Tensor, y: torch.Tensor, gate: QWeight | Non
                add: torch.Tensor | None = None, split_k: int = 0, stream: int | None = None,
                kernel: int = _lib.KERNEL_POLICY) -> bool:
     """GEMV with explicit launch options: split_k (0 = the shape policy),
-    kernel (KERNEL_VALU, or 0 = the policy, which is that kernel)."""
+    kernel (KERNEL_VALU, or 0 = the policy, which is that kernel, or
+    KERNEL_SEQUENTIAL: the reference's old mapping, split_k 0 or 1)."""
     _f32_buf(x, "x", w.cols, w.device)
     _f32_buf(y, "y", w.rows, w.device)
     if add is not None:
@@ -147,7 +148,8 @@ def mul_mat_ex(w: QWeight, x: torch.Tensor, y: torch.Tensor, gate: QWeight | Non
 
 
 def mul_mat_batch(w: QWeight, x: torch.Tensor, y: torch.Tensor, gate: QWeight | None = None,
-                  add: torch.Tensor | None = None, split_k: int = 0, stream: int | None = None) -> bool:
+                  add: torch.Tensor | None = None, split_k: int = 0, stream: int | None = None,
+                  kernel: int = _lib.KERNEL_POLICY) -> bool:
     """n activation vectors against one weight, one launch: x [n][cols], y and
     add [n][rows] (contiguous float32 on the weight's device)."""
     if x.dim() != 2 or not x.is_contiguous() or x.dtype != torch.float32:
@@ -163,6 +165,7 @@ def mul_mat_batch(w: QWeight, x: torch.Tensor, y: torch.Tensor, gate: QWeight | 
             raise ValueError(f"{name} must live on the weight's device cuda:{w.device}")
     opts = LaunchOptions()
     opts.split_k = split_k
+    opts.kernel = kernel
     s = _stream(x.device) if stream is None else stream
     return check(load().q4rdna_mul_mat_batch(ctypes.byref(w.raw), ctypes.byref(gate.raw) if gate else None,
                                              x.data_ptr(), x.shape[0], _ptr(add), y.data_ptr(),
@@ -286,6 +289,20 @@ class Sidecar:
         if not check(load().q4rdna_find(self._h, name.encode(), ne0, ne1, ctypes.byref(raw))):
             return None
         return QWeight(raw, owner=self)
+
+    def hits(self, index: int) -> int:
+        """GEMV launches that streamed entry `index` (q4rdna_sidecar_hits)."""
+        return int(load().q4rdna_sidecar_hits(self._h, index))
+
+
+def launch_count() -> int:
+    """GEMV kernel launches made through the library (q4rdna_launch_count)."""
+    return int(load().q4rdna_launch_count())
+
+
+def report_stats() -> None:
+    """The reference's launch report on stderr (q4rdna_report_stats)."""
+    load().q4rdna_report_stats()
 
 
 def inspect_sidecar(image: bytes, file_size: int | None = None) -> int:

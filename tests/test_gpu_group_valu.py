@@ -148,7 +148,7 @@ def test_valu_group_replays_from_a_hip_graph(cuda):
 
 def test_valu_group_options(cuda):
     """An explicit VALU kernel equals the policy; unknown kernels (2, the
-    withdrawn burst kernel, and 3), nonzero reserved words and oversize
+    withdrawn burst kernel, and 4), nonzero reserved words and oversize
     splits are argument errors that launch nothing."""
     L = q4rdna.load()
     cols = 4096
@@ -163,7 +163,7 @@ def test_valu_group_options(cuda):
     arr = (_lib.GroupDesc * 1)()
     arr[0].weight = w.raw
     arr[0].y = y_valu.data_ptr()
-    for kernel, split, reserved in ((2, 0, 0), (3, 0, 0), (_lib.KERNEL_VALU, 65, 0), (0, 0, 1)):
+    for kernel, split, reserved in ((2, 0, 0), (4, 0, 0), (_lib.KERNEL_VALU, 65, 0), (0, 0, 1)):
         o = _lib.LaunchOptions()
         o.kernel = kernel
         o.split_k = split
