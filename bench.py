@@ -894,6 +894,38 @@ def floors(tensors, data, replays: int = 20):
     return out
 
 
+def stage_launches(tensors) -> dict:
+    """Each decoder-layer stage's GEMV launched once per layer, eagerly (no
+    HIP graph, no normalization kernels), on fresh N(0, 1) activations: q/k/v
+    as one group launch, o + add, the gate/up SwiGLU site, down + add -- the
+    grouped chain's four kernels, one dispatch each per layer, for counter
+    collection (rocprofv3 --pmc) per stage."""
+    import torch
+    from q4rdna import api
+    by = {t["name"]: t for t in tensors}
+    layers = len(tensors) // 7
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x51EED000)
+
+    def w(l, part):
+        return by[f"blk.{l}.{part}.weight"]["w"]
+
+    def vec(n):
+        return torch.randn(n, generator=gen, device=dev)
+
+    for l in range(layers):
+        x, h = vec(4096), vec(4096)
+        q, k, v = torch.empty(4096, device=dev), torch.empty(1024, device=dev), torch.empty(1024, device=dev)
+        api.mul_mat_group([(w(l, "attn_q"), q), (w(l, "attn_k"), k), (w(l, "attn_v"), v)], x)
+        api.mul_mat_add(w(l, "attn_output"), q, x, torch.empty(4096, device=dev))
+        act = torch.empty(12288, device=dev)
+        api.mul_mat_glu(w(l, "ffn_up"), w(l, "ffn_gate"), h, act)
+        api.mul_mat_add(w(l, "ffn_down"), vec(12288), h, torch.empty(4096, device=dev))
+    torch.cuda.synchronize()
+    return {"layers": layers, "launches_per_layer": 4}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -924,6 +956,9 @@ def main() -> int:
     ap.add_argument("--floors", action="store_true",
                     help="plain-read and launch floors (stack read, empty launch, per-stage reads and four "
                          "dependent stage reads per layer); prints one JSON line instead of the stack bench")
+    ap.add_argument("--stage-launches", action="store_true",
+                    help="each decoder-layer stage's GEMV once per layer, eagerly, for rocprofv3 --pmc "
+                         "(no graph, no normalizations); prints one JSON line")
     ap.add_argument("--tensors", action="store_true",
                     help="per-tensor launch figures (projection shapes, lm_head, long-K split sweep with "
                          "outlier groups); prints one JSON line with the table instead of the stack bench")
@@ -947,6 +982,9 @@ def main() -> int:
         return 0
     if args.floors:
         print(json.dumps({"floors": floors(tensors, _data)}), flush=True)
+        return 0
+    if args.stage_launches:
+        print(json.dumps({"stage_launches": stage_launches(tensors)}), flush=True)
         return 0
     if args.batches:
         sizes = [int(v) for v in args.batches.split(",") if v]
