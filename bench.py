@@ -131,6 +131,14 @@ class KernelEvent:
 _BENCH_LIB = None
 
 
+SWEEP_ARITHMETIC = ("fp32 activations, outputs and accumulation; the sweep multiplies the 4-bit codes on int8 MFMA "
+                    "against each 64-element activation group re-encoded as three int8 digits of a 22-bit block "
+                    "fixed-point value (rounding <= 2^-23 of the group maximum), then applies the fp16 scales in fp32")
+SWEEP_ARITHMETIC_VALU = ("fp32 activations, outputs and accumulation; the sweep (VALU build) multiplies each 4-bit "
+                         "code, as an fp16 subnormal, by the fp32 activation in v_fma_mix_f32, offset removed by "
+                         "-8 times the group's activation sum, then applies the fp16 scales in fp32")
+
+
 def bench_lib():
     """libq4rdna_bench_gfx950.so: the measurement kernels (a plain stream
     read, an empty launch) and the decoder-layer bench's RMS normalization;
@@ -953,6 +961,10 @@ def main() -> int:
                     help="the stack as dependent decoder layers (q/k/v -> o -> gate/up -> down, 36 layers, HIP graph): "
                          "us per layer for the reference's per-tensor dispatch and for the grouped dispatch; prints one "
                          "JSON line instead of the stack bench")
+    ap.add_argument("--library", type=str, default="",
+                    help="load this build of the library instead of the default (e.g. "
+                         "rdna-gfx1201-v0.1_amd/q4rdna/libq4rdna_valu_sweep_gfx950.so, the sweep in the VALU "
+                         "formulation, for the MFMA-against-VALU measurement)")
     ap.add_argument("--floors", action="store_true",
                     help="plain-read and launch floors (stack read, empty launch, per-stage reads and four "
                          "dependent stage reads per layer); prints one JSON line instead of the stack bench")
@@ -968,6 +980,9 @@ def main() -> int:
               "(this GEMV path runs on a single GPU; it is not sharded across GPUs)", file=sys.stderr)
         return 2
 
+    if args.library:
+        import q4rdna._lib as qlib
+        qlib.LIB_PATH = os.path.abspath(args.library)
     import torch
     from q4rdna import api
 
@@ -1051,9 +1066,8 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "arithmetic": ("fp32 activations, outputs and accumulation; the sweep multiplies the 4-bit codes on int8 MFMA "
-                       "against each 64-element activation group re-encoded as three int8 digits of a 22-bit block "
-                       "fixed-point value (rounding <= 2^-23 of the group maximum), then applies the fp16 scales in fp32"),
+        "arithmetic": SWEEP_ARITHMETIC_VALU if "valu_sweep" in os.path.basename(args.library) else SWEEP_ARITHMETIC,
+        "library": os.path.basename(args.library) if args.library else "libq4rdna_gfx950.so",
         "data": "synthetic",
         "config": {"workload": f"qwen3-8b {args.layers}-layer stack: {len(tensors)} Q4_RDNA group-64 GEMVs at batch 1, "
                                "descriptors in layer order, fresh x per tensor, one multi-tensor plan per step",

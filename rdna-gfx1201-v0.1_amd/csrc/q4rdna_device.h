@@ -144,6 +144,62 @@ __device__ __forceinline__ bool exchange_pair(uint32_t *slots, uint32_t row, flo
     return true;
 }
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// A lane's tile slice: dword j of the 1,024 code bytes at 32 * (a + 8j) +
+// 4q holds rows 4q..4q+3 at k-pair a + 8j (a = lane >> 3, q = lane & 7 in
+// the kernels that read it).  Its 32 codes as fp16 subnormals: for k-pair
+// a + 8j, l02[j] = (u of row 4q, u of row 4q+2) at even k, h02[j] = 16u of
+// the same rows at odd k, l13/h13 the same for rows 4q+1 and 4q+3.
+struct TileCodes {
+    f16x2 l02[4], h02[4], l13[4], h13[4];
+};
+
+__device__ __forceinline__ TileCodes split_codes(const uint32_t (&dw)[4]) {
+    TileCodes w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        // (d & mask) ^ offset is one v_bitop3_b32 each.
+        const uint32_t d = dw[j], o = d >> 8;
+        w.l02[j] = __builtin_bit_cast(f16x2, (d & 0x000f000fu) ^ 0x00080008u);
+        w.h02[j] = __builtin_bit_cast(f16x2, (d & 0x00f000f0u) ^ 0x00800080u);
+        w.l13[j] = __builtin_bit_cast(f16x2, (o & 0x000f000fu) ^ 0x00080008u);
+        w.h13[j] = __builtin_bit_cast(f16x2, (o & 0x00f000f0u) ^ 0x00800080u);
+    }
+    return w;
+}
+
+// acc[r] += scale(row 4q + r) * (c + sum over the lane's 8 k of u * x), the
+// row's products in k order: for each k-pair the even k, then the odd k.
+// xl = even-k x * 2^24, xh = odd-k x * 2^20.
+__device__ __forceinline__ void apply_codes(const TileCodes &w, uint32_t s01, uint32_t s23, const float4 xl,
+                                            const float4 xh, const float c, float (&acc)[4]) {
+    const float xlv[4] = {xl.x, xl.y, xl.z, xl.w};
+    const float xhv[4] = {xh.x, xh.y, xh.z, xh.w};
+    float p0 = c, p1 = c, p2 = c, p3 = c;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        p0 = fmaf(static_cast<float>(w.l02[j].x), xlv[j], p0);
+        p1 = fmaf(static_cast<float>(w.l13[j].x), xlv[j], p1);
+        p2 = fmaf(static_cast<float>(w.l02[j].y), xlv[j], p2);
+        p3 = fmaf(static_cast<float>(w.l13[j].y), xlv[j], p3);
+        p0 = fmaf(static_cast<float>(w.h02[j].x), xhv[j], p0);
+        p1 = fmaf(static_cast<float>(w.h13[j].x), xhv[j], p1);
+        p2 = fmaf(static_cast<float>(w.h02[j].y), xhv[j], p2);
+        p3 = fmaf(static_cast<float>(w.h13[j].y), xhv[j], p3);
+    }
+    acc[0] = fmaf(half_bits_to_float(s01), p0, acc[0]);
+    acc[1] = fmaf(half_bits_to_float(s01 >> 16), p1, acc[1]);
+    acc[2] = fmaf(half_bits_to_float(s23), p2, acc[2]);
+    acc[3] = fmaf(half_bits_to_float(s23 >> 16), p3, acc[3]);
+}
+
+// Activation factors for apply_codes: x * 2^24 at even k, x * 2^20 at odd
+// k (the 1/16 of the high nibbles folded in); every product is then exactly
+// u * x.  The staged values are finite for |x| < 2^104.
+constexpr float kEvenScale = 16777216.0f;  // 2^24
+constexpr float kOddScale = 1048576.0f;    // 2^20 = 2^24 / 16
+
 // Workgroups are dealt to the 8 XCDs round robin; remap so consecutive
 // logical indices run on one XCD.  A bijection on [0, n).
 __device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t n) {

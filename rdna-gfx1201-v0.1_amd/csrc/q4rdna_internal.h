@@ -74,7 +74,17 @@ struct PlanDesc {
     uint32_t pair;  // single vector, no gate, one chunk: an item covers two 64-row blocks (128 rows)
 };
 
-constexpr uint32_t kPrepBytes = 272;
+// The single-vector sweep's arithmetic: the int8-MFMA formulation, or, in
+// the library built with -DQ4RDNA_SWEEP_VALU (make valu-sweep; kept for
+// the MFMA-against-VALU measurement of the sweep), the per-tensor kernels'
+// VALU formulation on fp32 activations laid out by the prepare launch.
+#if defined(Q4RDNA_SWEEP_VALU)
+constexpr bool kSweepValu = true;
+constexpr uint32_t kPrepBytes = 288;  // VALU layout: 16 float4 of scaled x + 8 lane sums
+#else
+constexpr bool kSweepValu = false;
+constexpr uint32_t kPrepBytes = 272;  // int8 digits (256) + the group factor (16)
+#endif
 // K chunk of a single-vector plan item: 192 groups holds a whole 12288-wide
 // row in one item, so such GEMVs need no split-K partials.
 constexpr uint32_t kChunkGroups = 192;

@@ -173,6 +173,33 @@ __global__ __launch_bounds__(256) void prep_kernel(const float *const *__restric
                                     (gptr_wi32x4)(out + 256));
 }
 
+// The VALU sweep's prepare (kSweepValu): per group (kPrepBytes = 288), for
+// lane slot a = 0..7 (k-pairs a + 8j, j = 0..3) the float4 of its even-k
+// x * 2^24 at 16a, the float4 of its odd-k x * 2^20 at 128 + 16a and
+// c = -8 * the sum of its eight x at 256 + 4a: what the per-tensor kernels
+// stage in LDS, in the same order of additions.  One thread per (group,
+// slot); nontemporal stores, as the digit prepare's.
+__global__ __launch_bounds__(256) void prep_valu_kernel(const float *const *__restrict__ group_x,
+                                                        uint8_t *__restrict__ prep, uint32_t groups) {
+    const uint32_t item = blockIdx.x * 256u + threadIdx.x;
+    if (item >= groups * 8u) return;
+    const uint32_t g = item >> 3, a = item & 7u;
+    const gptr_cf32 x = (gptr_cf32)group_x[g] + 2 * a;
+    float l[4], h[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        l[j] = x[16 * j];
+        h[j] = x[16 * j + 1];
+    }
+    gptr_u8 out = (gptr_u8)(prep + static_cast<size_t>(g) * kPrepBytes);
+    const f32x4 xl = {l[0] * kEvenScale, l[1] * kEvenScale, l[2] * kEvenScale, l[3] * kEvenScale};
+    const f32x4 xh = {h[0] * kOddScale, h[1] * kOddScale, h[2] * kOddScale, h[3] * kOddScale};
+    __builtin_nontemporal_store(xl, (__attribute__((address_space(1))) f32x4 *)(out + 16 * a));
+    __builtin_nontemporal_store(xh, (__attribute__((address_space(1))) f32x4 *)(out + 128 + 16 * a));
+    const float c = -8.0f * (((((((l[0] + h[0]) + l[1]) + h[1]) + l[2]) + h[2]) + l[3]) + h[3]);
+    __builtin_nontemporal_store(c, (gptr_f32)(out + 256 + 4 * a));
+}
+
 // 4x4 byte transpose: d[c] holds k-pair c for rows 0..3 (one byte each);
 // t[r] returns row r's k-pairs 0..3.  v_perm_b32 picks bytes of {S0:S1}
 // (selector 0..3 = S1 bytes, 4..7 = S0 bytes).
@@ -350,6 +377,66 @@ __device__ __forceinline__ void compute_wave_batched(const WaveRegs &r, float (&
     }
 }
 
+// ---- the VALU formulation of a step (kSweepValu) ----------------------------
+//
+// The same eight tiles in the wave's LDS stage (group gB = c/2, row tile
+// T = c%2 at kStageStride*c), read in the per-tensor kernels' lane layout:
+// lane (q = lane & 7, a = lane >> 3) takes dwords 32*(a + 8j) + 4q, j = 0..3
+// (rows 4q..4q+3 at k-pairs a + 8j; the 64 lanes of one read hit 64
+// consecutive dwords), and accumulates
+// acc[T][r] += scale(row 4q + r) * (c + sum of u * x) with v_fma_mix_f32
+// on fp16-subnormal codes, as gemv_kernel does.  Scales (8 bytes per tile)
+// and the prepared x of the step's four groups go to registers.
+struct ValuAux {
+    u32x2 sc[8];               // tile c: fp16 scales of rows 4q..4q+3
+    f32x4 xl[4], xh[4];        // group gB: even-k x * 2^24, odd-k x * 2^20 at the lane's k-pairs
+    float xc[4];               // group gB: -8 * the sum of the lane's eight x
+};
+struct ValuRegs {
+    i32x4 code[8];  // the tiles' code bytes as loaded, 16 per lane (a step loaded across an item's end)
+    ValuAux aux;
+};
+
+// Scales of tiles (group g0 + c/2 clamped to g_last, row tile c%2) and the
+// prepared x of groups g0..g0+3 (clamped).
+__device__ __forceinline__ void load_valu_aux(ValuAux &r, const uint8_t *rt0, const uint8_t *rt1,
+                                              const uint8_t *prep, uint32_t g0, uint32_t g_last, int q, int a) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const uint32_t g = min(g0 + (c >> 1), g_last);
+        r.sc[c] = __builtin_nontemporal_load(
+            (gptr_u32x2)(((c & 1) ? rt1 : rt0) + static_cast<size_t>(g) * kTileBytes + 8 * q));
+    }
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+        const uint8_t *px = prep + static_cast<size_t>(min(g0 + gi, g_last)) * kPrepBytes;
+        r.xl[gi] = *(gptr_f32x4)(px + 16 * a);
+        r.xh[gi] = *(gptr_f32x4)(px + 128 + 16 * a);
+        r.xc[gi] = *(gptr_cf32)(px + 256 + 4 * a);
+    }
+}
+
+// MASK: groups gi >= valid_groups of the step lie past the chunk.
+template <bool MASK>
+__device__ __forceinline__ void compute_valu(const uint8_t *stage, const ValuAux &r, float (&acc)[2][4], int q,
+                                             int a, uint32_t valid_groups) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const int gi = c >> 1, T = c & 1;
+        uint32_t d[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            d[j] = *reinterpret_cast<const uint32_t *>(stage + kStageStride * c + 32 * (a + 8 * j) + 4 * q);
+        float t[4] = {acc[T][0], acc[T][1], acc[T][2], acc[T][3]};
+        apply_codes(split_codes(d), r.sc[c].x, r.sc[c].y, make_float4(r.xl[gi][0], r.xl[gi][1], r.xl[gi][2], r.xl[gi][3]),
+                    make_float4(r.xh[gi][0], r.xh[gi][1], r.xh[gi][2], r.xh[gi][3]), r.xc[gi], t);
+        if (!MASK || static_cast<uint32_t>(gi) < valid_groups) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) acc[T][k] = t[k];
+        }
+    }
+}
+
 // Where an item's 64 sums go: y directly when the block has one item, else
 // part `part` of the block's per = streams * chunks parts.
 struct ItemOut {
@@ -373,6 +460,9 @@ using Red = float[2][kWaves][kStepGroups][kBlockRows];
 // with one item); y = (sum + add) * silu(gate sum), the arrival chain's
 // epilogue without the chain.
 // `last` is the workgroup's word for the arrival result.
+template <bool GLU, int G>
+__device__ __forceinline__ void finish_item_sum(Red &red, uint32_t &last, const ItemOut &o);
+
 template <bool GLU>
 __device__ __forceinline__ void finish_item(Red &red, uint32_t &last, const ItemOut &o, const float (&acc)[16],
                                             const float (&gacc)[16], const LaneRole &ln, int wave) {
@@ -386,6 +476,15 @@ __device__ __forceinline__ void finish_item(Red &red, uint32_t &last, const Item
             for (int n = 0; n < 16; ++n) gdst[n] = gacc[n];
         }
     }
+    finish_item_sum<GLU, kStepGroups>(red, last, o);
+}
+
+// After the publish: thread t < 64 sums row t's partials red[.][w][g][t]
+// for w < kWaves, g < G in that order (G = kStepGroups for the MFMA
+// formulation, whose lanes publish per group; 1 for the VALU one, whose
+// lanes sum their groups themselves) and finishes the item.
+template <bool GLU, int G>
+__device__ __forceinline__ void finish_item_sum(Red &red, uint32_t &last, const ItemOut &o) {
     __syncthreads();
     const uint32_t row = o.block * kBlockRows + threadIdx.x;
     const bool mine = threadIdx.x < kBlockRows && row < o.rows;
@@ -394,12 +493,12 @@ __device__ __forceinline__ void finish_item(Red &red, uint32_t &last, const Item
 #pragma unroll
         for (int w = 0; w < kWaves; ++w)
 #pragma unroll
-            for (int g = 0; g < kStepGroups; ++g) v += red[0][w][g][threadIdx.x];
+            for (int g = 0; g < G; ++g) v += red[0][w][g][threadIdx.x];
         if constexpr (GLU) {
 #pragma unroll
             for (int w = 0; w < kWaves; ++w)
 #pragma unroll
-                for (int g = 0; g < kStepGroups; ++g) gv += red[1][w][g][threadIdx.x];
+                for (int g = 0; g < G; ++g) gv += red[1][w][g][threadIdx.x];
         }
     }
     if (o.per == 1) {
@@ -445,6 +544,9 @@ struct Shared {
 // 128 * o.block): acc0 / acc1 hold the blocks' sums in the useful lanes;
 // thread t < 128 sums row t's 16 (wave, group) partials in the fixed order
 // and writes y (+ add).
+template <int G>
+__device__ __forceinline__ void finish_pair_sum(Red &red, const ItemOut &o);
+
 __device__ __forceinline__ void finish_pair(Red &red, const ItemOut &o, const float (&acc0)[16],
                                             const float (&acc1)[16], const LaneRole &ln, int wave) {
     if (ln.useful) {
@@ -456,6 +558,11 @@ __device__ __forceinline__ void finish_pair(Red &red, const ItemOut &o, const fl
             dst1[n] = acc1[n];
         }
     }
+    finish_pair_sum<kStepGroups>(red, o);
+}
+
+template <int G>
+__device__ __forceinline__ void finish_pair_sum(Red &red, const ItemOut &o) {
     __syncthreads();
     if (threadIdx.x < 2 * kBlockRows) {
         const uint32_t rb = threadIdx.x / kBlockRows, r = threadIdx.x % kBlockRows;
@@ -463,12 +570,24 @@ __device__ __forceinline__ void finish_pair(Red &red, const ItemOut &o, const fl
 #pragma unroll
         for (int w = 0; w < kWaves; ++w)
 #pragma unroll
-            for (int g = 0; g < kStepGroups; ++g) v += red[rb][w][g][r];
+            for (int g = 0; g < G; ++g) v += red[rb][w][g][r];
         const uint32_t row = o.block * 2 * kBlockRows + threadIdx.x;
         if (row < o.rows) {
             if (o.add != nullptr) v += ((gptr_cf32)o.add)[row];
             __builtin_nontemporal_store(v, (gptr_f32)o.y + row);
         }
+    }
+}
+
+// VALU formulation: each lane's sums over its groups, reduced over the
+// lanes sharing lane & 7 (lane l then holds row 4 (l & 7) + (l >> 4) of row
+// tile T), published as red[s][wave][0][32 T + row].
+__device__ __forceinline__ void publish_valu(float (&dst)[kWaves][kStepGroups][kBlockRows], const float (&acc)[2][4],
+                                             int wave, int lane) {
+#pragma unroll
+    for (int T = 0; T < 2; ++T) {
+        const float tot = add_over_a4(acc[T]);
+        if ((lane & 8) == 0) dst[wave][0][32 * T + 4 * (lane & 7) + (lane >> 4)] = tot;
     }
 }
 
@@ -658,6 +777,111 @@ __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ 
             finish_item<true>(red, sh.last, cur.o, acc, acc1, ln, wave);
         else
             finish_item<false>(red, sh.last, cur.o, acc, acc1, ln, wave);
+        if (k >= end) break;
+        cur = next;
+    }
+}
+
+// ---- the sweep in the VALU formulation (kSweepValu) -------------------------
+//
+// plan_kernel's items, deal, loads and finish with compute_valu's arithmetic:
+// each step's eight tiles go straight to the wave's LDS stage as in the
+// MFMA sweep, scales and prepared x to registers; one step in flight; the
+// next item's first step loaded across an item's end.
+
+__device__ __forceinline__ void stage_codes(const i32x4 (&code)[8], uint8_t *stage, int lane) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) *reinterpret_cast<i32x4 *>(stage + kStageStride * c + 16 * lane) = code[c];
+    __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ void load_step_valu(ValuRegs &r, const uint8_t *rt0, const uint8_t *rt1, const uint8_t *prep,
+                                               uint32_t g, uint32_t g_last, int lane) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const uint32_t gc = min(g + (c >> 1), g_last);
+        r.code[c] = __builtin_nontemporal_load(
+            (gptr_i32x4)(((c & 1) ? rt1 : rt0) + static_cast<size_t>(gc) * kTileBytes + 64 + 16 * lane));
+    }
+    load_valu_aux(r.aux, rt0, rt1, prep, g, g_last, lane & 7, lane >> 3);
+}
+
+__device__ __forceinline__ void item_steps_valu(const uint8_t *rt0, const uint8_t *rt1, const uint8_t *prep,
+                                                uint32_t g_begin, uint32_t g_end, int wave, int lane, uint8_t *stage,
+                                                float (&acc)[2][4], ValuRegs &pre, bool have_pre) {
+    const int q = lane & 7, a = lane >> 3;
+    const uint32_t steps = (g_end - g_begin) / kWgStepGroups;
+    uint32_t t = 0;
+    if (have_pre) {
+        stage_codes(pre.code, stage, lane);
+        compute_valu<false>(stage, pre.aux, acc, q, a, kStepGroups);
+        wait_lds_all();
+        t = 1;
+    }
+    for (; t < steps; ++t) {
+        const uint32_t g = g_begin + kWgStepGroups * t + kStepGroups * wave;
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            code_to_lds(((c & 1) ? rt1 : rt0) + static_cast<size_t>(g + (c >> 1)) * kTileBytes, stage + kStageStride * c,
+                        lane);
+        ValuAux r;
+        load_valu_aux(r, rt0, rt1, prep, g, g_end - 1, q, a);
+        wait_vm_all();
+        compute_valu<false>(stage, r, acc, q, a, kStepGroups);
+        wait_lds_all();  // every read of the stage is done before the next step's loads into it
+    }
+    for (uint32_t g = g_begin + steps * kWgStepGroups + kStepGroups * wave; g < g_end; g += kWgStepGroups) {
+        ValuRegs rr;
+        load_step_valu(rr, rt0, rt1, prep, g, g_end - 1, lane);
+        stage_codes(rr.code, stage, lane);
+        compute_valu<true>(stage, rr.aux, acc, q, a, g_end - g);
+        wait_lds_all();
+    }
+}
+
+template <bool BOTH>
+__global__ __launch_bounds__(256) void plan_valu_kernel(const PlanDesc *__restrict__ descs,
+                                                        const uint32_t *__restrict__ deal) {
+    __shared__ Shared sh;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint2 *entry = reinterpret_cast<const uint2 *>(deal + ((gridDim.x + 2) & ~1u));
+    const uint32_t end = deal[blockIdx.x + 1];
+    uint32_t k = deal[blockIdx.x];
+    if (k >= end) return;
+    auto locate = [&](uint2 e) { return decode_item<BOTH>(descs[e.x], e.y); };
+    ItemCtx cur = locate(entry[k]);
+    ValuRegs pre;
+    bool have_pre = false;
+    uint32_t parity = 0;
+    for (;;) {
+        const uint2 next_entry = k + 1 < end ? entry[k + 1] : make_uint2(0, 0);
+        float acc[2][4] = {}, acc1[2][4] = {};
+        item_steps_valu(cur.rt[0], cur.rt[1], cur.prep, cur.g_begin, cur.g_end, wave, lane, sh.stage[wave], acc, pre,
+                        have_pre);
+        if (cur.kind != kOnePass)
+            item_steps_valu(cur.rt[2], cur.rt[3], cur.prep, cur.g_begin, cur.g_end, wave, lane, sh.stage[wave], acc1,
+                            pre, false);
+        ++k;
+        ItemCtx next;
+        have_pre = false;
+        if (k < end) {
+            next = locate(next_entry);
+            if (next.g_end - next.g_begin >= kWgStepGroups) {
+                load_step_valu(pre, next.rt[0], next.rt[1], next.prep, next.g_begin + kStepGroups * wave,
+                               next.g_end - 1, lane);
+                have_pre = true;
+            }
+        }
+        Red &red = sh.red[parity];
+        parity ^= 1;
+        publish_valu(red[0], acc, wave, lane);
+        if (cur.kind != kOnePass) publish_valu(red[1], acc1, wave, lane);
+        if (cur.kind == kPairPass)
+            finish_pair_sum<1>(red, cur.o);
+        else if (BOTH && cur.kind == kBothPass)
+            finish_item_sum<true, 1>(red, sh.last, cur.o);
+        else
+            finish_item_sum<false, 1>(red, sh.last, cur.o);
         if (k >= end) break;
         cur = next;
     }
@@ -914,16 +1138,27 @@ __global__ __launch_bounds__(64 * kBatchWaves) void plan_batch_kernel(const Plan
 
 hipError_t launch_prep(const float *const *group_x, uint8_t *prep, uint32_t groups, hipStream_t stream) {
     if (groups == 0) return hipSuccess;
-    hipLaunchKernelGGL(prep_kernel, dim3((groups + 63) / 64), dim3(256), 0, stream, group_x, prep, groups);
+    if constexpr (kSweepValu)
+        hipLaunchKernelGGL(prep_valu_kernel, dim3((groups * 8 + 255) / 256), dim3(256), 0, stream, group_x, prep,
+                           groups);
+    else
+        hipLaunchKernelGGL(prep_kernel, dim3((groups + 63) / 64), dim3(256), 0, stream, group_x, prep, groups);
     return hipGetLastError();
 }
 
 hipError_t launch_plan(const PlanDesc *descs, const uint32_t *deal, uint32_t workgroups, bool both_streams,
                        hipStream_t stream) {
-    if (both_streams)
-        hipLaunchKernelGGL(plan_kernel<true>, dim3(workgroups), dim3(256), 0, stream, descs, deal);
-    else
-        hipLaunchKernelGGL(plan_kernel<false>, dim3(workgroups), dim3(256), 0, stream, descs, deal);
+    if constexpr (kSweepValu) {
+        if (both_streams)
+            hipLaunchKernelGGL(plan_valu_kernel<true>, dim3(workgroups), dim3(256), 0, stream, descs, deal);
+        else
+            hipLaunchKernelGGL(plan_valu_kernel<false>, dim3(workgroups), dim3(256), 0, stream, descs, deal);
+    } else {
+        if (both_streams)
+            hipLaunchKernelGGL(plan_kernel<true>, dim3(workgroups), dim3(256), 0, stream, descs, deal);
+        else
+            hipLaunchKernelGGL(plan_kernel<false>, dim3(workgroups), dim3(256), 0, stream, descs, deal);
+    }
     return hipGetLastError();
 }
 
