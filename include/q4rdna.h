@@ -151,8 +151,7 @@ int q4rdna_mul_mat_glu(const q4rdna_weight *up, const q4rdna_weight *gate, const
  * :579-584); kernel = Q4RDNA_KERNEL_POLICY or Q4RDNA_KERNEL_VALU (the same
  * kernel) or Q4RDNA_KERNEL_SEQUENTIAL (any other value, 2 included, which
  * ABI 1 used for a kernel since withdrawn, is an argument error); reserved
- * words must be
- * zero.  Zero-initialised options mean "policy" throughout. */
+ * words must be zero.  Zero-initialised options mean "policy" throughout. */
 #define Q4RDNA_KERNEL_POLICY 0
 #define Q4RDNA_KERNEL_VALU 1 /* the split-K VALU kernel (split_k applies) */
 /* The reference's old mapping (LLAMA_Q4_RDNA_MAPPING=old, source/q4rdna.cu:
