@@ -682,7 +682,7 @@ def chain_parity(y, tiles, rows, cols, xin, add=None, gate_tiles=None):
 
 
 def layer_chain(tensors, replays: int, check_layers=(0, 17, 35),
-                dispatches=("reference", "grouped", "ffn")):
+                dispatches=("reference", "grouped")):
     """The stack as a decoder runs it: layer l+1's input depends on layer l,
     so every projection waits for the one before.  Per layer: x_l RMS-
     normalized feeds q, k and v; o on q's output plus the residual x_l (o's
@@ -699,8 +699,6 @@ def layer_chain(tensors, replays: int, check_layers=(0, 17, 35),
                  the VALU kernel), then o(+add), gate/up SwiGLU and
                  down(+add) through the per-tensor entry points: four
                  launches
-      ffn        as grouped, with gate/up SwiGLU and down(+add) as one
-                 q4rdna_mul_mat_ffn launch: three launches
     us_per_layer is the whole chain's time per layer, normalizations
     included; norm_us_per_layer is a graph of the normalizations alone over
     the same buffers, and gemv_us_per_layer the difference, the GEMV
@@ -752,10 +750,7 @@ def layer_chain(tensors, replays: int, check_layers=(0, 17, 35),
                                        (w(l, "attn_v"), b["v"])], b["xn"], stream=stream)
                 api.mul_mat_add(w(l, "attn_output"), b["q"], x, b["h"], stream=stream)
             norm(b["h"], b["hn"])
-            if gemvs and dispatch == "ffn":
-                assert api.mul_mat_ffn(w(l, "ffn_up"), w(l, "ffn_gate"), w(l, "ffn_down"), b["hn"], add=b["h"],
-                                       mid=b["act"], y=b["out"], stream=stream) is not None
-            elif gemvs:
+            if gemvs:
                 api.mul_mat_glu(w(l, "ffn_up"), w(l, "ffn_gate"), b["hn"], b["act"], stream=stream)
                 api.mul_mat_add(w(l, "ffn_down"), b["act"], b["h"], b["out"], stream=stream)
 
@@ -815,8 +810,7 @@ def layer_chain(tensors, replays: int, check_layers=(0, 17, 35),
         layer_bytes = sum(algorithmic_bytes(by[f"blk.0.{p}.weight"]["rows"], by[f"blk.0.{p}.weight"]["cols"])
                           for p in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"))
         gemv_us = us - norm_us
-        out[dispatch] = dict(launches_per_layer={"reference": 6, "grouped": 4, "ffn": 3}[dispatch],
-                             us_per_layer=round(us, 2),
+        out[dispatch] = dict(launches_per_layer=6 if dispatch == "reference" else 4, us_per_layer=round(us, 2),
                              norm_us_per_layer=round(norm_us, 2), gemv_us_per_layer=round(gemv_us, 2),
                              gb_per_s=round(layer_bytes / gemv_us / 1e3, 1),
                              pct_of_peak=round(layer_bytes / gemv_us / 1e3 / 80, 2),
@@ -954,7 +948,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-per-tensor", action="store_true")
     ap.add_argument("--no-layer-chain", action="store_true",
-                    help="skip the dependent decoder-layer chain (reference, grouped and FFN dispatch) in the stack bench")
+                    help="skip the dependent decoder-layer chain (reference and grouped dispatch) in the stack bench")
     ap.add_argument("--no-fused", action="store_true",
                     help="skip the SwiGLU-fused stack (216 GEMVs, gate/up as one SwiGLU GEMV per layer)")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -965,7 +959,7 @@ def main() -> int:
                          "vectors per GEMV and print one JSON line with the table instead of the stack bench")
     ap.add_argument("--layer-chain", action="store_true",
                     help="the stack as dependent decoder layers (q/k/v -> o -> gate/up -> down, 36 layers, HIP graph): "
-                         "us per layer for the reference's per-tensor dispatch, the grouped dispatch and the FFN dispatch; prints one "
+                         "us per layer for the reference's per-tensor dispatch and for the grouped dispatch; prints one "
                          "JSON line instead of the stack bench")
     ap.add_argument("--library", type=str, default="",
                     help="load this build of the library instead of the default (e.g. "
@@ -1051,11 +1045,11 @@ def main() -> int:
     chain = None
     if not args.no_layer_chain:
         # One decoder layer after another (each layer's input is the
-        # previous one's output): the reference's six launches per layer, the
-        # grouped four and the three with the FFN block as one launch, from
-        # HIP graphs of all 36 layers.
+        # previous one's output): the reference's six launches per layer and
+        # the grouped four, from HIP graphs of all 36 layers.
         layers = len(tensors) // 7
-        chain = layer_chain(tensors, 50, check_layers=sorted({0, layers // 2 - 1 if layers > 2 else 0, layers - 1}))
+        chain = layer_chain(tensors, 50, check_layers=sorted({0, layers // 2 - 1 if layers > 2 else 0, layers - 1}),
+                            dispatches=("reference", "grouped"))
 
     value = stack_bytes / (ms_per_step / 1000.0) / 1e9
     achieved = stack_bytes / (sweep_us / 1e6) / 1e9

@@ -145,23 +145,6 @@ int q4rdna_mul_mat_add(const q4rdna_weight *w, const float *x, int64_t x_ne0, co
 int q4rdna_mul_mat_glu(const q4rdna_weight *up, const q4rdna_weight *gate, const float *x,
                        int64_t x_ne0, int glu_op, float *y, int64_t y_ne0, void *stream);
 
-/* The FFN block in one launch: mid = (W_up x) * silu(W_gate x), then
- * y = W_down mid (+ add).  up and gate are M x K, down is N x M; x [K], mid
- * [M], y and add [N], fp32, device.  Down's workgroups stream their weights
- * while the SwiGLU's run and wait only for the mid rows their K chunk
- * reads, so the pair takes less than q4rdna_mul_mat_glu followed by
- * q4rdna_mul_mat_add.  mid and y equal that pair of launches bit for bit
- * where both run at the same splits with eight-wave workgroups (the Qwen3
- * shapes do).  add may be y itself; otherwise mid, x, y and add must not
- * overlap.  NOT_APPLICABLE for mismatched shapes (x_ne0 != K, y_ne0 != N,
- * down's K != M).  No reference counterpart: the reference's patch hooks
- * the GLU and the ADD fusion sites separately
- * (source/llama-cpp-q4rdna-integration.patch:28-33,42-46); a runtime that
- * knows its FFN block calls this in their place. */
-int q4rdna_mul_mat_ffn(const q4rdna_weight *up, const q4rdna_weight *gate, const q4rdna_weight *down,
-                       const float *x, int64_t x_ne0, float *mid, const float *add, float *y, int64_t y_ne0,
-                       void *stream);
-
 /* Launch options: split_k = number of K chunks reduced across workgroups of
  * the per-tensor kernel (0 = the shape policy, the reference's launch policy
  * at source/q4rdna.cu:578-680 and its LLAMA_Q4_RDNA_COOP override

@@ -98,14 +98,8 @@ __device__ __forceinline__ void store_agent(uint32_t *p, uint32_t v) {
 __device__ __forceinline__ float load_agent(const float *p) {
     return __hip_atomic_load((gptr_cf32)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ uint32_t load_agent(const uint32_t *p) {
-    return __hip_atomic_load((gptr_au32)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ uint32_t add_agent(uint32_t *p, uint32_t v) {
     return __hip_atomic_fetch_add((gptr_au32)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t sub_agent(uint32_t *p, uint32_t v) {
-    return __hip_atomic_fetch_sub((gptr_au32)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Wait until this wave's stores have completed (visible at device scope for
 // sc1 stores); the memory clobber keeps the compiler from moving memory

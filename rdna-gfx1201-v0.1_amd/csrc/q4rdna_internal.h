@@ -170,34 +170,6 @@ struct GemvGroupArgs {
 };
 hipError_t launch_gemv_group(const GemvGroupArgs &args, hipStream_t stream);
 
-// SwiGLU then down in one launch (q4rdna_mul_mat_ffn): mid[m] = (up x) *
-// silu(gate x) with up, gate m x k; y[n] = down mid (+ add) with down n x m.
-// The SwiGLU runs split into split_a K chunks (at most 64 groups each), down
-// into split_b (likewise).  Each phase meets its chunks as gemv_kernel does,
-// in its own regions: slots_a (2m words) or partial_a (2 * split_a * m) and
-// counters_a (m / 32) for the SwiGLU, slots_b (n) or partial_b (split_b *
-// n) and counters_b (n / 32) for down, all zero on entry and left zero.
-// sync (split_b * sync_stride words, zero on entry, left zero) orders
-// down's chunks after the SwiGLU rows they read: chunk c's two counters sit
-// at c * sync_stride.  Units run in the order A(0..lag-1), then A(j), B(j -
-// lag) for j = lag..; a down unit polls at most spin_limit times, sleeping
-// poll_sleep short sleeps between polls; past that its rows come out NaN.
-struct FfnArgs {
-    const uint8_t *up, *gate, *down;
-    const float *x, *add;
-    float *mid, *y;
-    uint32_t m, k, n;
-    uint32_t split_a, magic_a, split_b, magic_b;
-    uint32_t *slots_a, *counters_a;
-    float *partial_a;
-    uint32_t *slots_b, *counters_b;
-    float *partial_b;
-    uint32_t *sync;
-    uint32_t sync_stride, lag, first_sleep, poll_sleep, spin_limit;
-};
-constexpr uint32_t kFfnChunkGroups = 64;  // largest K chunk of either phase
-hipError_t launch_ffn(const FfnArgs &args, hipStream_t stream);
-
 hipError_t launch_dequant(const uint8_t *w, uint32_t rows, uint32_t cols, float *out,
                           hipStream_t stream);
 hipError_t launch_pack(const float *w, uint32_t rows, uint32_t cols, int algorithm, uint8_t *tiles,

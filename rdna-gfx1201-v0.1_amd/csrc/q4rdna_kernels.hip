@@ -312,26 +312,19 @@ __device__ __forceinline__ float epilogue(float v, float gv, const float *__rest
 // larger splits publish the chunk's partials with device-scope stores, wait
 // for them to complete, then count arrivals, and the last workgroup of the
 // row tile sums the chunks in chunk order and resets the counter.  `add` may
-// be null (ADD false makes it so at compile time).  COHERENT: y is written
-// with device-scope stores, for a reader in the same launch on another XCD.
-template <bool COHERENT>
-__device__ __forceinline__ void put_row(float *__restrict__ y, uint32_t row, float v) {
-    if constexpr (COHERENT) store_agent(&y[row], v);
-    else y[row] = v;
-}
-template <bool GATE, bool ADD, class Sh, bool COHERENT = false>
+// be null (ADD false makes it so at compile time).
+template <bool GATE, bool ADD, class Sh>
 __device__ __forceinline__ void finish_rows(Sh &sh, float *__restrict__ y, const float *__restrict__ add,
                                             float *__restrict__ partial, uint32_t *__restrict__ counters,
                                             uint32_t *__restrict__ slots, uint32_t rows, uint32_t split, uint32_t s,
                                             uint32_t rt, float v, float gv) {
     const uint32_t row = rt * kTileRows + (threadIdx.x & 31);
     if (split == 1) {
-        if (threadIdx.x < 32) put_row<COHERENT>(y, row, epilogue<GATE, ADD>(v, gv, add, row));
+        if (threadIdx.x < 32) y[row] = epilogue<GATE, ADD>(v, gv, add, row);
         return;
     }
     if (split == 2) {
-        if (threadIdx.x < 32 && exchange_pair<GATE>(slots, row, v, gv))
-            put_row<COHERENT>(y, row, epilogue<GATE, ADD>(v, gv, add, row));
+        if (threadIdx.x < 32 && exchange_pair<GATE>(slots, row, v, gv)) y[row] = epilogue<GATE, ADD>(v, gv, add, row);
         return;
     }
     if (threadIdx.x < 32) {
@@ -350,7 +343,7 @@ __device__ __forceinline__ void finish_rows(Sh &sh, float *__restrict__ y, const
             sum += load_agent(&partial[static_cast<size_t>(c) * rows + row]);
             if constexpr (GATE) gsum += load_agent(&partial[static_cast<size_t>(split + c) * rows + row]);
         }
-        put_row<COHERENT>(y, row, epilogue<GATE, ADD>(sum, gsum, add, row));
+        y[row] = epilogue<GATE, ADD>(sum, gsum, add, row);
     }
     if (threadIdx.x == 0) store_agent(&counters[rt], 0u);
 }
@@ -401,157 +394,6 @@ __global__ __launch_bounds__(64 * W) void gemv_group_kernel(GemvGroupArgs a) {
         finish_rows<GATE, true>(sh, G.y, G.add, G.partial, G.counters, G.slots, G.rows, split, s, rt, v, gv);
     else
         finish_rows<GATE, false>(sh, G.y, nullptr, G.partial, G.counters, G.slots, G.rows, split, s, rt, v, gv);
-}
-
-// ---- SwiGLU then down in one launch (q4rdna_mul_mat_ffn) -------------------
-//
-// mid = (up x) * silu(gate x) (m rows, k columns), then y = down mid (+ add)
-// (n rows, m columns).  Down's K chunk c reads only mid rows [64 gb(c),
-// 64 gb(c + 1)) (gb = its group bounds), so its workgroups can start as soon
-// as the SwiGLU units that write those rows are done, while the rest of the
-// SwiGLU still streams.  One unit per workgroup, in workgroup order:
-//
-//   A(0), ..., A(L-1), A(L), B(0), A(L+1), B(1), ..., B(C-1)
-//
-// with C = down's split, L >= 1 the lag, A(c) the SwiGLU (row tile, K chunk)
-// units of chunk c's mid rows (the chunks of a row tile adjacent) and B(c)
-// down's row tiles at chunk c.  Every unit a B unit waits for has a smaller workgroup index.
-// Each XCD dispatches its workgroups in index order and A units wait for
-// nothing, so the lowest-indexed undispatched A unit always gets a slot once
-// the units ahead of it on its XCD finish: every wait ends.  A B unit issues
-// its tile loads first, then waits for its chunk with a bounded poll.
-//
-// Chunk c's counters sit at sync + c * sync_stride: the first counts the
-// A(c) units done (each adds 1 once its mid stores have completed), the
-// second the B(c) units finished, and the last of them subtracts A(c)'s
-// total from the first and zeroes the second.  So
-// both are zero between launches, also after a poll that gave up (its rows
-// come out NaN; the A units still all arrive).  Each phase's arithmetic and
-// chunk reduction are gemv_kernel's at the same split, so mid and y equal a
-// q4rdna_mul_mat_glu launch and a q4rdna_mul_mat_add launch at those splits
-// bit for bit.
-
-// Down's partial sums for row tile rt over groups [g_begin, g_end) of mid
-// (at most W*T): the tiles are issued first, then the workgroup waits for
-// the chunk's mid rows and stages them with device-scope loads.  Returns
-// whether the wait succeeded.
-template <int T, int W>
-__device__ __forceinline__ bool ffn_down_partial(Shared &sh, const FfnArgs &f, uint32_t rt, uint32_t c,
-                                                 uint32_t g_begin, uint32_t g_end, float &out) {
-    const uint32_t groups = f.m / kGroup;
-    const int lane = threadIdx.x & 63, wave = wave_id();
-    const int q = lane & 7, a = lane >> 3;
-    const int ng = static_cast<int>(g_end - g_begin);
-    const uint8_t *wt = f.down + (static_cast<size_t>(rt) * groups + g_begin) * kTileBytes;
-    TileRegs t[T];
-#pragma unroll
-    for (int i = 0; i < T; ++i) {
-        const int gg = min(wave + W * i, ng - 1);
-        t[i] = load_tile(wt + static_cast<size_t>(gg) * kTileBytes, q, a);
-    }
-    if (threadIdx.x == 0) {
-        const uint32_t need = 2u * (g_end - g_begin) * f.split_a;
-        const uint32_t *ready = f.sync + static_cast<size_t>(c) * f.sync_stride;
-        for (uint32_t z = 0; z < f.first_sleep; ++z) __builtin_amdgcn_s_sleep(8);
-        uint32_t ok = 0u;
-        for (uint32_t polls = 0; polls < f.spin_limit; ++polls) {
-            if (load_agent(ready) >= need) {
-                ok = 1u;
-                break;
-            }
-            for (uint32_t z = 0; z < f.poll_sleep; ++z) __builtin_amdgcn_s_sleep(8);
-        }
-        sh.last = ok;
-    }
-    __syncthreads();
-    const bool ok = sh.last != 0u;
-    // Thread t stages x items (group t/8 + 8Wm, lane slot t%8), m < XI.
-    constexpr int XI = (T + 7) / 8;
-    const int xa = threadIdx.x & 7;
-#pragma unroll
-    for (int m = 0; m < XI; ++m) {
-        const int xg = (threadIdx.x >> 3) + 8 * W * m;
-        if (xg < ng) {
-            const float *b = f.mid + (static_cast<size_t>(g_begin) + xg) * kGroup + 2 * xa;
-            float l[4], h[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                l[j] = load_agent(b + 16 * j);
-                h[j] = load_agent(b + 16 * j + 1);
-            }
-            sh.st.v[xg][xa] = make_float4(l[0] * kEvenScale, l[1] * kEvenScale, l[2] * kEvenScale, l[3] * kEvenScale);
-            sh.st.v[xg][8 + xa] = make_float4(h[0] * kOddScale, h[1] * kOddScale, h[2] * kOddScale, h[3] * kOddScale);
-            sh.st.c[xg][xa] = -8.0f * (((((((l[0] + h[0]) + l[1]) + h[1]) + l[2]) + h[2]) + l[3]) + h[3]);
-        }
-    }
-    __syncthreads();
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    float gacc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < T; ++i) {
-        const int gg = wave + W * i;
-        if (gg < ng) tile_fma(t[i], sh.st.v[gg][a], sh.st.v[gg][8 + a], sh.st.c[gg][a], acc);
-    }
-    float gout = 0.f;
-    reduce_rows<false, W>(sh, acc, gacc, out, gout);
-    return ok;
-}
-
-template <int TA, int TB, bool ADD>
-__global__ __launch_bounds__(64 * kShortWaves) void ffn_kernel(FfnArgs f) {
-    constexpr int W = kShortWaves;
-    __shared__ Shared sh;
-    const uint32_t ga = f.k / kGroup, gm = f.m / kGroup;
-    const uint32_t C = f.split_b, tiles_b = f.n / kTileRows;
-    // The unit of this workgroup (a wave-uniform walk over at most 2C + 1
-    // segments of the order above).
-    uint32_t u = blockIdx.x, c = 0;
-    bool down = false;
-    for (uint32_t j = 0; j < C + f.lag; ++j) {
-        if (j < C) {
-            const uint32_t units =
-                2u * (div_split((j + 1) * gm, C, f.magic_b) - div_split(j * gm, C, f.magic_b)) * f.split_a;
-            if (u < units) {
-                c = j;
-                break;
-            }
-            u -= units;
-        }
-        if (j >= f.lag) {
-            if (u < tiles_b) {
-                c = j - f.lag;
-                down = true;
-                break;
-            }
-            u -= tiles_b;
-        }
-    }
-    if (!down) {
-        const uint32_t r = div_split(u, f.split_a, f.magic_a);
-        const uint32_t rt = 2u * div_split(c * gm, C, f.magic_b) + r, s = u - r * f.split_a;
-        const uint32_t g_begin = div_split(s * ga, f.split_a, f.magic_a);
-        const uint32_t g_end = div_split((s + 1) * ga, f.split_a, f.magic_a);
-        float v = 0.f, gv = 0.f;
-        tile_row_partial_short<true, TA, W>(sh, f.up, f.gate, f.x, f.k, rt, g_begin, g_end, v, gv);
-        finish_rows<true, false, Shared, true>(sh, f.mid, nullptr, f.partial_a, f.counters_a, f.slots_a, f.m,
-                                               f.split_a, s, rt, v, gv);
-        wait_stores();
-        __syncthreads();
-        if (threadIdx.x == 0) add_agent(f.sync + static_cast<size_t>(c) * f.sync_stride, 1u);
-        return;
-    }
-    const uint32_t g_begin = div_split(c * gm, C, f.magic_b), g_end = div_split((c + 1) * gm, C, f.magic_b);
-    float v = 0.f;
-    if (!ffn_down_partial<TB, W>(sh, f, u, c, g_begin, g_end, v)) v = __builtin_nanf("");
-    finish_rows<false, ADD>(sh, f.y, f.add, f.partial_b, f.counters_b, f.slots_b, f.n, f.split_b, c, u, v, 0.f);
-    // Past its wait for good: the last B(c) unit here resets chunk c's counts.
-    if (threadIdx.x == 0) {
-        uint32_t *ready = f.sync + static_cast<size_t>(c) * f.sync_stride;
-        if (add_agent(ready + 1, 1u) == tiles_b - 1) {
-            sub_agent(ready, 2u * (g_end - g_begin) * f.split_a);
-            store_agent(ready + 1, 0u);
-        }
-    }
 }
 
 // ---- several activation vectors against one weight (n = 2..8) -------------
@@ -1155,24 +997,6 @@ hipError_t launch_gemv_sequential(const GemvArgs &args, hipStream_t stream) {
 }
 
 uint32_t gemv_multi_stage_groups(uint32_t vectors) { return vectors > 4 ? 16u : 32u; }
-
-hipError_t launch_ffn(const FfnArgs &f, hipStream_t stream) {
-    const uint32_t chunk_a = (f.k / kGroup + f.split_a - 1) / f.split_a;
-    const uint32_t chunk_b = (f.m / kGroup + f.split_b - 1) / f.split_b;
-    if (chunk_a > kFfnChunkGroups || chunk_b > kFfnChunkGroups) return hipErrorInvalidValue;
-    const dim3 grid(f.split_a * (f.m / kTileRows) + f.split_b * (f.n / kTileRows)), block(64 * kShortWaves);
-    const bool wide_a = chunk_a > 4u * kShortWaves, wide_b = chunk_b > 4u * kShortWaves;
-    auto go = [&](auto ta, auto tb) {
-        constexpr int TA = decltype(ta)::value, TB = decltype(tb)::value;
-        if (f.add != nullptr) hipLaunchKernelGGL((ffn_kernel<TA, TB, true>), grid, block, 0, stream, f);
-        else hipLaunchKernelGGL((ffn_kernel<TA, TB, false>), grid, block, 0, stream, f);
-    };
-    using T4 = std::integral_constant<int, 4>;
-    using T8 = std::integral_constant<int, 8>;
-    if (wide_a) wide_b ? go(T8{}, T8{}) : go(T8{}, T4{});
-    else wide_b ? go(T4{}, T8{}) : go(T4{}, T4{});
-    return hipGetLastError();
-}
 
 uint32_t gemv_waves(uint32_t groups, uint32_t split, uint64_t workgroups, uint32_t cus) {
     const uint32_t chunk = (groups + split - 1) / split;

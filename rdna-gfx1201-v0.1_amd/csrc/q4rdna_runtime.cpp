@@ -47,7 +47,6 @@ int set_error(int code, const char *fmt, ...) {
 namespace {
 
 using q4rdna::kGroup;
-using q4rdna::kFfnChunkGroups;
 using q4rdna::kGroupChunkGroups;
 using q4rdna::kTileBytes;
 using q4rdna::kTileRows;
@@ -93,16 +92,6 @@ int current_device() {
 // Compute units per device, looked up once (a fixed table: the lookup
 // allocates nothing, so allocation-free entry points may use it).
 constexpr int kMaxDevices = 64;
-// Polls of the FFN launch's down units before they give up (NaN rows): each
-// poll is a device-scope load and a short sleep, so this is far beyond any
-// wait a launch that runs to completion has (its SwiGLU units never wait).
-constexpr uint32_t kFfnSpinLimit = 1u << 20;
-// Every SwiGLU unit before every down unit (a lag of down's split), each
-// chunk's counters 4 KB apart, about 0.85 us of sleep between polls: the
-// fastest of the orders, spacings and poll rates measured.
-constexpr uint32_t kFfnLag = 64;
-constexpr uint32_t kFfnSyncStride = 1024;
-constexpr uint32_t kFfnPollSleep = 4;
 std::atomic<uint32_t> g_cus[kMaxDevices];
 
 uint32_t cu_count(int device) {
@@ -645,85 +634,6 @@ int q4rdna_mul_mat_glu(const q4rdna_weight *up, const q4rdna_weight *gate, const
     if ((rc = launch_one(L, up, gate->tiles, x, nullptr, y, static_cast<hipStream_t>(stream))) == Q4RDNA_OK)
         count_launch(up->tiles, gate->tiles);
     return rc;
-}
-
-int q4rdna_mul_mat_ffn(const q4rdna_weight *up, const q4rdna_weight *gate, const q4rdna_weight *down,
-                       const float *x, int64_t x_ne0, float *mid, const float *add, float *y, int64_t y_ne0,
-                       void *stream) {
-    int rc = check_weight(up);
-    if (rc != Q4RDNA_OK) return rc;
-    if ((rc = check_weight(gate)) != Q4RDNA_OK) return rc;
-    if ((rc = check_weight(down)) != Q4RDNA_OK) return rc;
-    if (up->rows != gate->rows || up->columns != gate->columns || up->device != gate->device)
-        return set_error(Q4RDNA_NOT_APPLICABLE, "up and gate shapes differ");
-    if (down->columns != up->rows || down->device != up->device)
-        return set_error(Q4RDNA_NOT_APPLICABLE, "down's K (%u) is not up's rows (%u)", down->columns, up->rows);
-    if (x_ne0 != static_cast<int64_t>(up->columns) || y_ne0 != static_cast<int64_t>(down->rows))
-        return set_error(Q4RDNA_NOT_APPLICABLE, "shape mismatch");
-    if ((rc = check_io(x, y)) != Q4RDNA_OK) return rc;
-    if (mid == nullptr || !aligned(mid, 4) || (add != nullptr && !aligned(add, 4)))
-        return set_error(Q4RDNA_ERR_ARGUMENT, "NULL or misaligned mid, or misaligned add");
-    // mid is written while x is read and before add is read; y while mid is
-    // read.  add may be y itself (each row's add is read by its writer).
-    auto overlap = [](const void *a, size_t na, const void *b, size_t nb) {
-        const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
-        return a0 < b0 + 4 * nb && b0 < a0 + 4 * na;
-    };
-    const uint32_t M = up->rows, K = up->columns, N = down->rows;
-    if (overlap(mid, M, x, K) || overlap(mid, M, y, N) || (add != nullptr && overlap(mid, M, add, N)) ||
-        overlap(y, N, x, K) || (add != nullptr && add != y && overlap(y, N, add, N)))
-        return set_error(Q4RDNA_ERR_ARGUMENT, "mid, x, y and add overlap");
-    // Each phase at the split its own launch would take, raised until every
-    // K chunk fits the short-range kernel.
-    const uint32_t ga = K / kGroup, gm = M / kGroup;
-    const uint32_t split_a = std::min(std::max(resolve_split(up, 0), (ga + kFfnChunkGroups - 1) / kFfnChunkGroups),
-                                      std::min(ga, kMaxSplit));
-    const uint32_t split_b = std::min(std::max(resolve_split(down, 0), (gm + kFfnChunkGroups - 1) / kFfnChunkGroups),
-                                      std::min(gm, kMaxSplit));
-    if ((ga + split_a - 1) / split_a > kFfnChunkGroups || (gm + split_b - 1) / split_b > kFfnChunkGroups)
-        return set_error(Q4RDNA_NOT_APPLICABLE, "rows of %u or %u groups need more than %u K chunks", ga, gm, kMaxSplit);
-    if (!q4rdna::gemv_shape_fits(M / kTileRows, ga, split_a) || !q4rdna::gemv_shape_fits(N / kTileRows, gm, split_b) ||
-        static_cast<uint64_t>(split_a) * (M / kTileRows) + static_cast<uint64_t>(split_b) * (N / kTileRows) >
-            0x7fffffffull)
-        return set_error(Q4RDNA_ERR_ARGUMENT, "FFN shapes are beyond the kernels' index range");
-    const size_t pa = split_a > 2 ? 2ull * split_a * M : 0, pb = split_b > 2 ? static_cast<size_t>(split_b) * N : 0;
-    const size_t ca = M / kTileRows, cb = N / kTileRows;
-    Workspace *ws = nullptr;
-    if ((rc = get_workspace(up->device, static_cast<hipStream_t>(stream), std::max<size_t>(pa + pb, 1),
-                            ca + cb + static_cast<size_t>(kFfnSyncStride) * split_b, 2ull * M + N, &ws)) != Q4RDNA_OK)
-        return rc;
-    q4rdna::FfnArgs f{};
-    f.up = up->tiles;
-    f.gate = gate->tiles;
-    f.down = down->tiles;
-    f.x = x;
-    f.add = add;
-    f.mid = mid;
-    f.y = y;
-    f.m = M;
-    f.k = K;
-    f.n = N;
-    f.split_a = split_a;
-    f.magic_a = q4rdna::split_magic(split_a);
-    f.split_b = split_b;
-    f.magic_b = q4rdna::split_magic(split_b);
-    f.partial_a = ws->partial;
-    f.partial_b = ws->partial + pa;
-    f.counters_a = ws->counters;
-    f.counters_b = ws->counters + ca;
-    f.sync = ws->counters + ca + cb;
-    f.slots_a = ws->slots;
-    f.slots_b = ws->slots + 2ull * M;
-    f.sync_stride = kFfnSyncStride;
-    f.lag = std::min(std::max<uint32_t>(kFfnLag, 1), split_b);
-    f.first_sleep = 0;
-    f.poll_sleep = kFfnPollSleep;
-    f.spin_limit = kFfnSpinLimit;
-    hipError_t e = q4rdna::launch_ffn(f, static_cast<hipStream_t>(stream));
-    if (e != hipSuccess) return hip_fail(e, "FFN launch");
-    const uint8_t *t[3] = {up->tiles, gate->tiles, down->tiles};
-    count_launch(t, 3);
-    return Q4RDNA_OK;
 }
 
 int q4rdna_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x, const float *add, float *y,

@@ -45,7 +45,7 @@ EXPORTS = (
     "q4rdna_plan_prepare",
     "q4rdna_plan_sweep", "q4rdna_plan_destroy",
     "q4rdna_plan_workgroups", "q4rdna_pack", "q4rdna_dequantize",
-    "q4rdna_launch_count", "q4rdna_sidecar_hits", "q4rdna_report_stats", "q4rdna_mul_mat_ffn",
+    "q4rdna_launch_count", "q4rdna_sidecar_hits", "q4rdna_report_stats",
 )
 
 
@@ -112,7 +112,6 @@ def load() -> ctypes.CDLL:
         "q4rdna_mul_mat": (i32, [WP, vp, i64, vp, i64, vp]),
         "q4rdna_mul_mat_add": (i32, [WP, vp, i64, vp, i64, vp, i64, vp]),
         "q4rdna_mul_mat_glu": (i32, [WP, WP, vp, i64, i32, vp, i64, vp]),
-        "q4rdna_mul_mat_ffn": (i32, [WP, WP, WP, vp, i64, vp, vp, vp, i64, vp]),
         "q4rdna_mul_mat_ex": (i32, [WP, WP, vp, vp, vp, ctypes.POINTER(LaunchOptions), vp]),
         "q4rdna_mul_mat_batch": (i32, [WP, WP, vp, u32, vp, vp, ctypes.POINTER(LaunchOptions), vp]),
         "q4rdna_policy_split_k": (u32, [u32, u32, i32]),

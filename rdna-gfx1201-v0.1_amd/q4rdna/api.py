@@ -127,26 +127,6 @@ def mul_mat_glu(up: QWeight, gate: QWeight, x: torch.Tensor, y: torch.Tensor | N
     return y if ok else None
 
 
-def mul_mat_ffn(up: QWeight, gate: QWeight, down: QWeight, x: torch.Tensor, add: torch.Tensor | None = None,
-                mid: torch.Tensor | None = None, y: torch.Tensor | None = None, stream: int | None = None):
-    """The FFN block in one launch: mid = (W_up x) * silu(W_gate x), then
-    y = W_down mid (+ add).  Returns (y, mid), or None when not applicable."""
-    x = _f32_vec(x, "x")
-    if mid is None:
-        mid = torch.empty(up.rows, dtype=torch.float32, device=x.device)
-    if y is None:
-        y = torch.empty(down.rows, dtype=torch.float32, device=x.device)
-    _f32_buf(mid, "mid", up.rows, up.device)  # the ABI takes mid's size from up
-    _f32_vec(y, "y")
-    if add is not None:
-        _f32_buf(add, "add", down.rows, down.device)
-    s = _stream(x.device) if stream is None else stream
-    ok = check(load().q4rdna_mul_mat_ffn(ctypes.byref(up.raw), ctypes.byref(gate.raw), ctypes.byref(down.raw),
-                                         x.data_ptr(), x.numel(), mid.data_ptr(), _ptr(add), y.data_ptr(),
-                                         y.numel(), s))
-    return (y, mid) if ok else None
-
-
 def mul_mat_ex(w: QWeight, x: torch.Tensor, y: torch.Tensor, gate: QWeight | None = None,
                add: torch.Tensor | None = None, split_k: int = 0, stream: int | None = None,
                kernel: int = _lib.KERNEL_POLICY) -> bool:
