@@ -576,7 +576,7 @@ def tensor_table(seed: int):
     launch, the fused sites, and the long-K split sweep (S = 1..32) with 1%
     outlier groups."""
     import torch
-    from q4rdna import _lib, api
+    from q4rdna import api
     rows_out = []
     shapes = [("q/o_proj", 4096, 4096), ("k/v_proj", 1024, 4096), ("gate/up_proj", 12288, 4096),
               ("down_proj", 4096, 12288), ("lm_head", 151936, 4096)]
@@ -598,14 +598,11 @@ def tensor_table(seed: int):
         for n in (2, 4, 8):
             x = torch.randn(n, c, device="cuda")
             y = torch.empty(n, r, device="cuda")
-            # Both kernels: the n-vector VALU kernel and the MFMA items (the
-            # policy's choice from four vectors).
-            for kernel, kname in ((_lib.KERNEL_VALU, "valu"), (_lib.KERNEL_MFMA, "mfma")):
-                us = time_launches(lambda i: api.mul_mat_batch(ws[i % copies], x, y, kernel=kernel), max(40, copies))
-                gbs = algorithmic_bytes(r, c, n) / us / 1e3
-                rows_out.append(dict(kind="batched", kernel=kname, name=name, rows=r, cols=c, n=n, us=round(us, 2),
-                                     gb_per_s=round(gbs, 1), copies=copies))
-                log(f"[tensors] {name} {r}x{c} N={n} {kname}: {us:.2f} us {gbs:.0f} GB/s")
+            us = time_launches(lambda i: api.mul_mat_batch(ws[i % copies], x, y), max(40, copies))
+            gbs = algorithmic_bytes(r, c, n) / us / 1e3
+            rows_out.append(dict(kind="batched", name=name, rows=r, cols=c, n=n, us=round(us, 2),
+                                 gb_per_s=round(gbs, 1), copies=copies))
+            log(f"[tensors] {name} {r}x{c} N={n}: {us:.2f} us {gbs:.0f} GB/s")
         del ws, buf, tiles
     # The reference's fused sites: SwiGLU gate/up (two weight streams) and
     # the bias add, one launch each.

@@ -149,9 +149,9 @@ int q4rdna_mul_mat_glu(const q4rdna_weight *up, const q4rdna_weight *gate, const
  * the per-tensor kernel (0 = the shape policy, the reference's launch policy
  * at source/q4rdna.cu:578-680 and its LLAMA_Q4_RDNA_COOP override
  * :579-584); kernel = Q4RDNA_KERNEL_POLICY or Q4RDNA_KERNEL_VALU (the same
- * kernel), Q4RDNA_KERNEL_SEQUENTIAL or Q4RDNA_KERNEL_MFMA (any other value,
- * 2 included, which ABI 1 used for a kernel since withdrawn, is an argument
- * error); reserved words must be zero.  Zero-initialised options mean "policy" throughout. */
+ * kernel) or Q4RDNA_KERNEL_SEQUENTIAL (any other value, 2 included, which
+ * ABI 1 used for a kernel since withdrawn, is an argument error); reserved
+ * words must be zero.  Zero-initialised options mean "policy" throughout. */
 #define Q4RDNA_KERNEL_POLICY 0
 #define Q4RDNA_KERNEL_VALU 1 /* the split-K VALU kernel (split_k applies) */
 /* The reference's old mapping (LLAMA_Q4_RDNA_MAPPING=old, source/q4rdna.cu:
@@ -162,15 +162,6 @@ int q4rdna_mul_mat_glu(const q4rdna_weight *up, const q4rdna_weight *gate, const
  * refuses it (argument error).  Slow: an ablation and a bit-exact
  * reference, not a decode path. */
 #define Q4RDNA_KERNEL_SEQUENTIAL 3
-/* The int8-MFMA kernel of the batched multi-tensor sweep, for one weight
- * (q4rdna_mul_mat_batch, any n; q4rdna_mul_mat_ex as n = 1): a launch
- * converts the n vectors into three int8 digits per element (22-bit block
- * fixed point per 64-element group, rounding <= 2^-23 of the group
- * maximum), then 256-row items multiply them on v_mfma_i32_16x16x64_i8;
- * split_k (0 = about two items per CU) is the number of K chunks.  The
- * batch policy runs it for n >= 4.  q4rdna_mul_mat_group and the
- * allocation-free entry point refuse it. */
-#define Q4RDNA_KERNEL_MFMA 4
 typedef struct q4rdna_launch_options {
     uint32_t split_k;
     uint32_t kernel;

@@ -140,13 +140,6 @@ hipError_t launch_prep_batch(const PlanDesc *descs, const uint32_t *owner, uint3
                              hipStream_t stream);
 hipError_t launch_plan_batch(const PlanDesc *descs, uint32_t items, uint32_t n, uint32_t workgroups, uint32_t *sched,
                              hipStream_t stream);
-// One GEMV with n = 1..8 vectors on the batched sweep's items (the MFMA
-// kernel of q4rdna_mul_mat_batch): d describes it as a plan descriptor with
-// x [n][cols] (4-byte aligned), prep holding cols / 64 * ceil(n / 4) *
-// kBatchQuadBytesHost bytes, K chunks of chunk_groups groups (d.chunks of
-// them), and, when d.streams * d.chunks > 1, partial (streams * chunks * n *
-// rows floats) and counters (one per 256-row block, zero on entry, left zero).
-hipError_t launch_batch_call(const PlanDesc &d, const float *x, uint32_t n, uint32_t chunk_groups, hipStream_t stream);
 constexpr uint32_t kMaxGroup = 8;  // GEMVs of one group launch (Q4RDNA_MAX_GROUP)
 
 // A VALU group launch (gemv_kernel's arithmetic): up to kMaxGroup GEMVs

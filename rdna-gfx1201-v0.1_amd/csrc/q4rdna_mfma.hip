@@ -984,17 +984,16 @@ __device__ __forceinline__ void compute_batch(const BatchRegs &r, const i32x4 (&
     }
 }
 
-// One item: (256-row block, stream, K chunk of chunk_groups groups).
 template <int NQ>
 __device__ __forceinline__ void run_batch_item(BatchShared<NQ> &sh, const PlanDesc &d, uint32_t local, uint32_t nvec,
-                                               int lane, int wave, uint32_t chunk_groups) {
+                                               int lane, int wave) {
     const uint32_t groups = d.cols / kGroup;
     const uint32_t tiles = d.rows / kTileRows;
     const uint32_t per = d.streams * d.chunks;
     const uint32_t block = local / per, part = local - block * per;
     const uint32_t stream = part / d.chunks, chunk = part - stream * d.chunks;
-    const uint32_t g_begin = chunk * chunk_groups;
-    const uint32_t g_end = min(groups, g_begin + chunk_groups);
+    const uint32_t g_begin = chunk * kBatchChunkGroups;
+    const uint32_t g_end = min(groups, g_begin + kBatchChunkGroups);
     const size_t row_tile_bytes = static_cast<size_t>(groups) * kTileBytes;
     const uint8_t *base = stream != 0 ? d.gate : d.w;
     const int kslot = lane >> 4, j = lane & 15, T = j >> 1, h = j & 1;
@@ -1124,7 +1123,7 @@ __global__ __launch_bounds__(64 * kBatchWaves) void plan_batch_kernel(const Plan
     while (item < items) {
         if (threadIdx.x == 0) sh.next_item[slot ^ 1] = add_agent(&sched[0], 1u);
         while (item >= descs[d + 1].item_begin) ++d;
-        run_batch_item<NQ>(sh, descs[d], item - descs[d].item_begin, nvec, lane, wave, kBatchChunkGroups);
+        run_batch_item<NQ>(sh, descs[d], item - descs[d].item_begin, nvec, lane, wave);
         __syncthreads();
         slot ^= 1;
         item = sh.next_item[slot];
@@ -1135,58 +1134,7 @@ __global__ __launch_bounds__(64 * kBatchWaves) void plan_batch_kernel(const Plan
     }
 }
 
-// ---- one GEMV with n = 1..8 activation vectors (q4rdna_mul_mat_batch) -------
-//
-// The batched sweep's items for one GEMV, one workgroup each: a prepare
-// launch writes the vectors' digits in the batched layout, then a plain grid
-// of (256-row block, stream, K chunk) items runs run_batch_item with K chunks
-// sized for the launch, meeting in d.partial / d.counters as plan items do.
-// x is [n][cols] and only 4-byte aligned: each lane's loads are
-// unconditional (a lane past the last pair reads pair 0's group).
-__global__ __launch_bounds__(256) void prep_batch_call_kernel(const float *__restrict__ x, uint32_t n, uint32_t cols,
-                                                              uint8_t *__restrict__ prep) {
-    const int lane = threadIdx.x & 63, kslot = lane & 3;
-    const uint32_t groups = cols / kGroup;
-    const uint32_t pair = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + (lane >> 2);
-    const bool valid = pair < groups * n;
-    const uint32_t pq = valid ? pair : 0;
-    const uint32_t g = pq / n, vec = pq - g * n;
-    const uint32_t quads = (n + 3) / 4, slot = vec & 3;
-    float xs[16];
-    load_kslot_f32_always(x + static_cast<size_t>(vec) * cols + static_cast<size_t>(g) * kGroup, kslot, valid, xs);
-    i32x4 rows[3];
-    bool bad;
-    int e;
-    kslot_digits(xs, valid, rows, bad, e);
-    if (!valid) return;
-    gptr_u8 quad = (gptr_u8)(prep + (static_cast<size_t>(g) * quads + vec / 4) * kBatchQuadBytes);
-    gptr_u8 out = quad + 256 * kslot + 64 * slot;
-#pragma unroll
-    for (int d = 0; d < 3; ++d) __builtin_nontemporal_store(rows[d], (gptr_wi32x4)(out + 16 * d));
-    __builtin_nontemporal_store(i32x4{0, 0, 0, 0}, (gptr_wi32x4)(out + 48));
-    if (kslot == 0) __builtin_nontemporal_store(digit_factor(bad, e), (gptr_f32)(quad + 1024 + 4 * slot));
-}
-
-template <int NQ>
-__global__ __launch_bounds__(64 * kBatchWaves) void batch_call_kernel(PlanDesc d, uint32_t nvec, uint32_t chunk_groups) {
-    __shared__ BatchShared<NQ> sh;
-    run_batch_item<NQ>(sh, d, blockIdx.x, nvec, threadIdx.x & 63, threadIdx.x >> 6, chunk_groups);
-}
-
 }  // namespace
-
-hipError_t launch_batch_call(const PlanDesc &d, const float *x, uint32_t n, uint32_t chunk_groups,
-                             hipStream_t stream) {
-    const uint32_t groups = d.cols / kGroup;
-    hipLaunchKernelGGL(prep_batch_call_kernel, dim3((groups * n + 63) / 64), dim3(256), 0, stream, x, n, d.cols,
-                       d.prep);
-    const dim3 grid(((d.rows + kBatchRows - 1) / kBatchRows) * d.streams * d.chunks), block(64 * kBatchWaves);
-    if (n <= 4)
-        hipLaunchKernelGGL(batch_call_kernel<1>, grid, block, 0, stream, d, n, chunk_groups);
-    else
-        hipLaunchKernelGGL(batch_call_kernel<2>, grid, block, 0, stream, d, n, chunk_groups);
-    return hipGetLastError();
-}
 
 hipError_t launch_prep(const float *const *group_x, uint8_t *prep, uint32_t groups, hipStream_t stream) {
     if (groups == 0) return hipSuccess;

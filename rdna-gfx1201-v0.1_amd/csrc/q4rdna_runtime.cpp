@@ -92,8 +92,6 @@ int current_device() {
 // Compute units per device, looked up once (a fixed table: the lookup
 // allocates nothing, so allocation-free entry points may use it).
 constexpr int kMaxDevices = 64;
-// q4rdna_mul_mat_batch's policy runs the MFMA kernel from this many vectors.
-constexpr uint32_t kBatchMfmaMin = 4;
 std::atomic<uint32_t> g_cus[kMaxDevices];
 
 uint32_t cu_count(int device) {
@@ -230,7 +228,7 @@ int check_io(const float *x, const float *y) {
 int check_options(const q4rdna_launch_options *options) {
     if (options == nullptr) return Q4RDNA_OK;
     if (options->kernel != Q4RDNA_KERNEL_POLICY && options->kernel != Q4RDNA_KERNEL_VALU &&
-        options->kernel != Q4RDNA_KERNEL_SEQUENTIAL && options->kernel != Q4RDNA_KERNEL_MFMA)
+        options->kernel != Q4RDNA_KERNEL_SEQUENTIAL)
         return set_error(Q4RDNA_ERR_ARGUMENT, "unknown kernel %u", options->kernel);
     for (uint32_t r : options->reserved)
         if (r != 0) return set_error(Q4RDNA_ERR_ARGUMENT, "reserved launch options must be zero");
@@ -255,8 +253,6 @@ int check_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const fl
     const uint32_t s = options ? options->split_k : 0;
     if (s > kMaxSplit) return set_error(Q4RDNA_ERR_ARGUMENT, "split_k %u exceeds %u", s, kMaxSplit);
     if ((rc = check_options(options)) != Q4RDNA_OK) return rc;
-    if (options != nullptr && options->kernel == Q4RDNA_KERNEL_MFMA)
-        return set_error(Q4RDNA_ERR_ARGUMENT, "the MFMA kernel runs through q4rdna_mul_mat_ex and q4rdna_mul_mat_batch only");
     TensorLaunch L{};
     if (options != nullptr && options->kernel == Q4RDNA_KERNEL_SEQUENTIAL) {
         // The old mapping sums each row in one thread: no K chunks.
@@ -642,8 +638,6 @@ int q4rdna_mul_mat_glu(const q4rdna_weight *up, const q4rdna_weight *gate, const
 
 int q4rdna_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x, const float *add, float *y,
                       const q4rdna_launch_options *options, void *stream) {
-    if (options != nullptr && options->kernel == Q4RDNA_KERNEL_MFMA)
-        return q4rdna_mul_mat_batch(w, gate, x, 1, add, y, options, stream);
     q4rdna::TensorLaunch L{};
     int rc = q4rdna::check_mul_mat_ex(w, gate, x, add, y, options, &L);
     if (rc != Q4RDNA_OK) return rc;
@@ -762,9 +756,8 @@ int q4rdna_mul_mat_group(const q4rdna_group_desc *descs, uint32_t count, const f
     const uint32_t split_k = options ? options->split_k : 0;
     if (split_k > kMaxSplit) return set_error(Q4RDNA_ERR_ARGUMENT, "split_k %u exceeds %u", split_k, kMaxSplit);
     if ((rc = check_options(options)) != Q4RDNA_OK) return rc;
-    if (options != nullptr &&
-        (options->kernel == Q4RDNA_KERNEL_SEQUENTIAL || options->kernel == Q4RDNA_KERNEL_MFMA))
-        return set_error(Q4RDNA_ERR_ARGUMENT, "a group launch runs the split-K VALU kernel only");
+    if (options != nullptr && options->kernel == Q4RDNA_KERNEL_SEQUENTIAL)
+        return set_error(Q4RDNA_ERR_ARGUMENT, "a group launch runs the split-K kernel, not the sequential one");
     if ((rc = launch_group_valu(descs, count, x, glu, split_k, static_cast<hipStream_t>(stream))) == Q4RDNA_OK) {
         const uint8_t *t[2 * Q4RDNA_MAX_GROUP];
         for (uint32_t i = 0; i < count; ++i) {
@@ -775,53 +768,6 @@ int q4rdna_mul_mat_group(const q4rdna_group_desc *descs, uint32_t count, const f
     }
     return rc;
 }
-
-namespace {
-
-// n = 1..8 vectors against one weight on the batched sweep's MFMA items:
-// 256-row blocks, both SwiGLU streams as items of their own, K chunks sized
-// for about two items per CU (at least 8 groups each) unless split_k names
-// the chunk count.  The digits and the partials live in the stream's
-// workspace.
-int launch_batch_mfma(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x, uint32_t n,
-                      const float *add, float *y, uint32_t split, hipStream_t s) {
-    const uint32_t M = w->rows, groups = w->columns / kGroup, streams = gate ? 2u : 1u;
-    const uint32_t blocks = (M + q4rdna::kBatchBlockRows - 1) / q4rdna::kBatchBlockRows;
-    uint32_t chunks = split;
-    if (chunks == 0) {
-        const uint32_t target = 2 * cu_count(w->device);
-        chunks = std::min((target + blocks * streams - 1) / (blocks * streams), std::max<uint32_t>(1, groups / 8));
-    }
-    chunks = std::min(std::max<uint32_t>(chunks, 1), groups);
-    const uint32_t chunk_groups = (groups + chunks - 1) / chunks;
-    chunks = (groups + chunk_groups - 1) / chunk_groups;
-    const uint32_t per = streams * chunks;
-    const size_t prep_floats =
-        (static_cast<size_t>(groups) * ((n + 3) / 4) * q4rdna::kBatchQuadBytesHost / sizeof(float) + 63) & ~size_t{63};
-    const size_t partial_floats = per > 1 ? static_cast<size_t>(per) * n * M : 0;
-    Workspace *ws = nullptr;
-    int rc = get_workspace(w->device, s, prep_floats + partial_floats, per > 1 ? blocks : 0, 0, &ws);
-    if (rc != Q4RDNA_OK) return rc;
-    q4rdna::PlanDesc d{};
-    d.w = w->tiles;
-    d.gate = gate ? gate->tiles : nullptr;
-    d.x = x;
-    d.add = add;
-    d.y = y;
-    d.prep = reinterpret_cast<uint8_t *>(ws->partial);
-    d.partial = ws->partial + prep_floats;
-    d.counters = ws->counters;
-    d.rows = M;
-    d.cols = w->columns;
-    d.chunks = chunks;
-    d.streams = streams;
-    d.per = per;
-    hipError_t e = q4rdna::launch_batch_call(d, x, n, chunk_groups, s);
-    if (e != hipSuccess) return hip_fail(e, "MFMA batch launch");
-    return Q4RDNA_OK;
-}
-
-}  // namespace
 
 int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x, uint32_t n,
                          const float *add, float *y, const q4rdna_launch_options *options, void *stream) {
@@ -841,11 +787,6 @@ int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, cons
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const uint8_t *gt = gate ? gate->tiles : nullptr;
     const uint32_t groups = w->columns / kGroup;
-    const uint32_t kernel = options ? options->kernel : Q4RDNA_KERNEL_POLICY;
-    if (kernel == Q4RDNA_KERNEL_MFMA || (kernel == Q4RDNA_KERNEL_POLICY && n >= kBatchMfmaMin)) {
-        if ((rc = launch_batch_mfma(w, gate, x, n, add, y, split, s)) == Q4RDNA_OK) count_launch(w->tiles, gt);
-        return rc;
-    }
     // Every K chunk of the n-vector kernel fits its x stage.  Longer rows than
     // 64 such chunks, and the sequential kernel, go one launch per vector.
     const uint32_t stage = q4rdna::gemv_multi_stage_groups(n);

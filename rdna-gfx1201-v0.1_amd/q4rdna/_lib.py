@@ -65,7 +65,6 @@ class Weight(ctypes.Structure):
 KERNEL_POLICY = 0
 KERNEL_VALU = 1
 KERNEL_SEQUENTIAL = 3
-KERNEL_MFMA = 4
 MAX_GROUP = 8
 
 

@@ -148,9 +148,8 @@ def test_valu_group_replays_from_a_hip_graph(cuda):
 
 def test_valu_group_options(cuda):
     """An explicit VALU kernel equals the policy; unknown kernels (2, the
-    withdrawn burst kernel, and 5), nonzero reserved words and oversize
-    splits are argument errors that launch nothing, and so is the MFMA
-    kernel (4) for a group launch."""
+    withdrawn burst kernel, and 4), nonzero reserved words and oversize
+    splits are argument errors that launch nothing."""
     L = q4rdna.load()
     cols = 4096
     _, w = weight(1024, cols, 760)
@@ -164,11 +163,7 @@ def test_valu_group_options(cuda):
     arr = (_lib.GroupDesc * 1)()
     arr[0].weight = w.raw
     arr[0].y = y_valu.data_ptr()
-    o = _lib.LaunchOptions()
-    o.kernel = _lib.KERNEL_MFMA
-    rc = L.q4rdna_mul_mat_group(arr, 1, x.data_ptr(), cols, ctypes.byref(o), torch.cuda.current_stream().cuda_stream)
-    assert rc == q4rdna.ERR_ARGUMENT
-    for kernel, split, reserved in ((2, 0, 0), (5, 0, 0), (_lib.KERNEL_VALU, 65, 0), (0, 0, 1)):
+    for kernel, split, reserved in ((2, 0, 0), (4, 0, 0), (_lib.KERNEL_VALU, 65, 0), (0, 0, 1)):
         o = _lib.LaunchOptions()
         o.kernel = kernel
         o.split_k = split

@@ -18,7 +18,7 @@ import pytest
 import torch
 
 import oracle as O
-from q4rdna import _lib, api
+from q4rdna import api
 from conftest import assert_gemv_parity
 
 pytestmark = pytest.mark.gpu
@@ -55,77 +55,29 @@ def check_batch(y: torch.Tensor, tiles, rows, cols, xs, gate_tiles=None, add=Non
                            add=None if add is None else add[v], label=(label, v))
 
 
-@pytest.mark.parametrize("kernel", [_lib.KERNEL_VALU, _lib.KERNEL_MFMA], ids=["valu", "mfma"])
 @pytest.mark.parametrize("n", [2, 4, 8])
-def test_mul_mat_batch_at_the_ffn_sites(cuda, layer, n, kernel):
+def test_mul_mat_batch_at_the_ffn_sites(cuda, layer, n):
     """q4rdna_mul_mat_batch at gate/up 12288 x 4096 (plain and SwiGLU) and
-    down 4096 x 12288 + add, on the n-vector VALU kernel and on the MFMA
-    kernel (the batch policy's choice from four vectors)."""
+    down 4096 x 12288 + add."""
     up, up_t = layer["up"]
     gate, gate_t = layer["gate"]
     down, down_t = layer["down"]
     x = xs_for(4096, n, 0x5B00 + n)
     xd = torch.from_numpy(x).cuda()
     y = torch.full((n, 12288), float("nan"), device="cuda")
-    assert api.mul_mat_batch(up, xd, y, kernel=kernel)
+    assert api.mul_mat_batch(up, xd, y)
     torch.cuda.synchronize()
     check_batch(y, up_t, 12288, 4096, x, label=("up", n))
     y.fill_(float("nan"))
-    assert api.mul_mat_batch(up, xd, y, gate=gate, kernel=kernel)
+    assert api.mul_mat_batch(up, xd, y, gate=gate)
     torch.cuda.synchronize()
     check_batch(y, up_t, 12288, 4096, x, gate_tiles=gate_t, label=("swiglu", n))
     xh = xs_for(12288, n, 0x5C00 + n)
     res = xs_for(4096, n, 0x5D00 + n)
     yd = torch.full((n, 4096), float("nan"), device="cuda")
-    assert api.mul_mat_batch(down, torch.from_numpy(xh).cuda(), yd, add=torch.from_numpy(res).cuda(), kernel=kernel)
+    assert api.mul_mat_batch(down, torch.from_numpy(xh).cuda(), yd, add=torch.from_numpy(res).cuda())
     torch.cuda.synchronize()
     check_batch(yd, down_t, 4096, 12288, xh, add=res, label=("down + add", n))
-
-
-def random_tiles(rows: int, cols: int, seed: int) -> np.ndarray:
-    rng = np.random.default_rng(seed)
-    t = rng.integers(0, 256, (rows // 32, cols // 64, 1088), dtype=np.uint8)
-    s = (rng.uniform(1e-3, 3e-2, (rows // 32, cols // 64, 32)) *
-         rng.choice([-1.0, 1.0], (rows // 32, cols // 64, 32))).astype(np.float16)
-    t[:, :, :64] = s.view(np.uint8).reshape(rows // 32, cols // 64, 64)
-    return t.reshape(-1)
-
-
-# (rows, cols, n, split_k, epilogue): rows that end inside a 256-row block,
-# K of one group and of 65 groups, partial vector quads (n = 1, 3, 5, 7),
-# explicit K chunk counts including one chunk (no partials) and the largest
-# (64, three groups per chunk), and the add / SwiGLU epilogues.  Run in this
-# order on one stream, so a call with fewer vectors follows one with more
-# (stale digits in the workspace's unused vector slots must not matter).
-MFMA_CASES = [(96, 512, 8, 0, None), (96, 512, 3, 0, "add"), (2112, 4160, 5, 0, "glu"), (2112, 4160, 1, 1, None),
-              (4096, 4096, 7, 3, "add"), (1024, 4096, 4, 2, "glu"), (256, 64, 2, 0, None), (160, 12288, 6, 64, "add")]
-
-
-@pytest.mark.parametrize("case", MFMA_CASES, ids=lambda c: "-".join(map(str, c)))
-def test_mfma_batch_edge_shapes(cuda, case):
-    rows, cols, n, split, kind = case
-    seed = rows + cols + n
-    t = random_tiles(rows, cols, seed)
-    w = api.QWeight.from_tiles(torch.from_numpy(t).cuda(), rows, cols)
-    x = xs_for(cols, n, seed + 1)
-    gt = gate = add = res = None
-    if kind == "glu":
-        gt = random_tiles(rows, cols, seed + 2)
-        gate = api.QWeight.from_tiles(torch.from_numpy(gt).cuda(), rows, cols)
-    if kind == "add":
-        res = xs_for(rows, n, seed + 3)
-        add = torch.from_numpy(res).cuda()
-    y = torch.full((n, rows), float("nan"), device="cuda")
-    assert api.mul_mat_batch(w, torch.from_numpy(x).cuda(), y, gate=gate, add=add, kernel=_lib.KERNEL_MFMA,
-                             split_k=split)
-    torch.cuda.synchronize()
-    check_batch(y, t, rows, cols, x, gate_tiles=gt, add=res, label=case)
-    if n == 1:  # q4rdna_mul_mat_ex with the MFMA kernel is the same launch
-        y1 = torch.full((rows,), float("nan"), device="cuda")
-        assert api.mul_mat_ex(w, torch.from_numpy(x[0]).cuda(), y1, gate=gate, add=None if add is None else add[0],
-                              kernel=_lib.KERNEL_MFMA, split_k=split)
-        torch.cuda.synchronize()
-        assert torch.equal(y1, y[0])
 
 
 @pytest.mark.parametrize("n", [2, 4, 8])
