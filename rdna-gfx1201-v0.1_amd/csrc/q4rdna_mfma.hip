@@ -100,11 +100,13 @@ __device__ __forceinline__ void kslot_digits(const float (&xs)[16], bool have, i
         nonfinite |= !isfinite(xs[i]);
         m = fmaxf(m, isfinite(xs[i]) ? fabsf(xs[i]) : 0.0f);
     }
-    m = fmaxf(m, __shfl_xor(m, 1));
-    m = fmaxf(m, __shfl_xor(m, 2));
+    // The group's four lanes are a DPP quad: xor 1 and xor 2 as quad
+    // permutes ([1,0,3,2] and [2,3,0,1]), no LDS round trip.
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0xB1, 0xf, 0xf, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0x4E, 0xf, 0xf, false)));
     int nf = nonfinite ? 1 : 0;
-    nf |= __shfl_xor(nf, 1);
-    nf |= __shfl_xor(nf, 2);
+    nf |= __builtin_amdgcn_mov_dpp(nf, 0xB1, 0xf, 0xf, false);
+    nf |= __builtin_amdgcn_mov_dpp(nf, 0x4E, 0xf, 0xf, false);
     int e = 0;
     if (m > 0.0f) (void)frexpf(m, &e);
     if (e < -100) e = -100;
