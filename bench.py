@@ -825,6 +825,66 @@ def layer_chain(tensors, replays: int, check_layers=(0, 17, 35),
     return out
 
 
+def sweep_clocks(plan, launches: int = 20):
+    """Per-workgroup start and end of the stack sweep, from the clock build
+    of the library (`--library .../libq4rdna_sweep_clocks_gfx950.so`): each
+    sweep workgroup reads the GPU's 100 MHz real-time counter at its start
+    and after its last item.  Workgroup b runs on XCD b % 8 and is the first
+    (b < CUs) or second workgroup of its CU, as the plan's deal assumes.
+    After 0.5 s of settling, `launches` prepare + sweep steps, each read back.
+    Per launch, relative to the first workgroup's start: the span (last end)
+    against the sweep's own HIP events, the spread of the starts, the ends'
+    10th / 50th / 90th percentile and maximum, the mean end of each CU slot
+    and of each XCD; medians over the launches, and the correlation of the
+    workgroups' ends between consecutive launches."""
+    import ctypes
+    import numpy as np
+    import torch
+    from q4rdna import _lib
+    L = _lib.load()
+    if not hasattr(L, "q4rdna_sweep_clocks"):
+        raise SystemExit("--clocks needs the clock build: --library "
+                         "rdna-gfx1201-v0.1_amd/q4rdna/libq4rdna_sweep_clocks_gfx950.so")
+    fn = L.q4rdna_sweep_clocks
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_uint32]
+    wg = plan.workgroups
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    settle(plan, 0.5)
+    s = torch.cuda.current_stream().cuda_stream
+    buf = np.zeros(2 * wg, dtype=np.uint64)
+    rows, ends = [], []
+    for _ in range(launches):
+        plan.prepare(s)
+        a, e = KernelEvent(), KernelEvent()
+        a.record(s)
+        plan.sweep(s)
+        e.record(s)
+        torch.cuda.synchronize()
+        if fn(buf.ctypes.data, wg) != 0:
+            raise RuntimeError("q4rdna_sweep_clocks failed")
+        start = buf[0::2].astype(np.int64)
+        end = buf[1::2].astype(np.int64)
+        t0 = start.min()
+        su, eu = (start - t0) / 100.0, (end - t0) / 100.0
+        ends.append(eu)
+        b = np.arange(wg)
+        rows.append(dict(events_us=a.elapsed_ms(e) * 1000.0, span_us=float(eu.max()), start_spread_us=float(su.max()),
+                         end_p10=float(np.percentile(eu, 10)), end_p50=float(np.percentile(eu, 50)),
+                         end_p90=float(np.percentile(eu, 90)), end_max=float(eu.max()),
+                         slot_mean_end=[float(eu[b < cus].mean()), float(eu[b >= cus].mean())],
+                         xcd_mean_end=[float(eu[b % 8 == x].mean()) for x in range(8)]))
+    med = lambda key: round(float(np.median([r[key] for r in rows])), 2)  # noqa: E731
+    corr = [float(np.corrcoef(ends[i], ends[i + 1])[0, 1]) for i in range(len(ends) - 1)]
+    return dict(workgroups=wg, cus=cus, launches=launches,
+                events_us=med("events_us"), span_us=med("span_us"), start_spread_us=med("start_spread_us"),
+                end_p10=med("end_p10"), end_p50=med("end_p50"), end_p90=med("end_p90"), end_max=med("end_max"),
+                slot_mean_end=[round(float(np.median([r["slot_mean_end"][i] for r in rows])), 2) for i in range(2)],
+                xcd_mean_end=[round(float(np.median([r["xcd_mean_end"][x] for r in rows])), 2) for x in range(8)],
+                end_correlation_between_launches=round(float(np.median(corr)), 3),
+                per_workgroup_end_std_us=round(float(np.median(np.std(np.stack(ends), axis=0))), 2))
+
+
 def floors(tensors, data, replays: int = 20):
     """What the GEMV launches are measured against, from plain reads of the
     same bytes (bench library kernels; graph replays, each read a different
@@ -965,6 +1025,9 @@ def main() -> int:
                     help="load this build of the library instead of the default (e.g. "
                          "rdna-gfx1201-v0.1_amd/q4rdna/libq4rdna_valu_sweep_gfx950.so, the sweep in the VALU "
                          "formulation, for the MFMA-against-VALU measurement)")
+    ap.add_argument("--clocks", action="store_true",
+                    help="per-workgroup start and end clocks of the stack sweep (needs --library with the clock "
+                         "build, libq4rdna_sweep_clocks_gfx950.so); prints one JSON line instead of the stack bench")
     ap.add_argument("--floors", action="store_true",
                     help="plain-read and launch floors (stack read, empty launch, per-stage reads and four "
                          "dependent stage reads per layer); prints one JSON line instead of the stack bench")
@@ -1007,6 +1070,9 @@ def main() -> int:
         return 0
     plan = api.Plan([(t["w"], t["x"], t["y"]) for t in tensors])
     log(f"[bench] plan: {len(tensors)} GEMVs, {plan.workgroups} workgroups")
+    if args.clocks:
+        print(json.dumps({"sweep_clocks": sweep_clocks(plan, max(args.steps, 10))}), flush=True)
+        return 0
     if args.pmc_probe:
         for _ in range(5):
             plan.launch()

@@ -85,6 +85,16 @@ constexpr uint32_t kPrepBytes = 288;  // VALU layout: 16 float4 of scaled x + 8 
 constexpr bool kSweepValu = false;
 constexpr uint32_t kPrepBytes = 272;  // int8 digits (256) + the group factor (16)
 #endif
+// The library built with -DQ4RDNA_SWEEP_CLOCKS (make sweep-clocks) records
+// each single-vector sweep workgroup's first and last clock (s_memrealtime,
+// 100 MHz) of the latest launch, for up to kMaxSweepClocks workgroups; the
+// product build records nothing.
+#if defined(Q4RDNA_SWEEP_CLOCKS)
+constexpr bool kSweepClocks = true;
+#else
+constexpr bool kSweepClocks = false;
+#endif
+constexpr uint32_t kMaxSweepClocks = 4096;
 // K chunk of a single-vector plan item: 192 groups holds a whole 12288-wide
 // row in one item, so such GEMVs need no split-K partials.
 constexpr uint32_t kChunkGroups = 192;

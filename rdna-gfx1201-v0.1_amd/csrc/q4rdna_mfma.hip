@@ -723,6 +723,10 @@ __device__ __forceinline__ ItemCtx decode_item(const PlanDesc &d, uint32_t local
     return c;
 }
 
+#if defined(Q4RDNA_SWEEP_CLOCKS)
+__device__ uint64_t g_sweep_clocks[2 * kMaxSweepClocks];
+#endif
+
 // Persistent grid: workgroup b runs the items the plan dealt it, entries
 // [deal[b], deal[b + 1]) of the (descriptor, item within it) pairs that
 // follow the gridDim.x + 1 offsets (padded to an even count), longest GEMVs
@@ -737,6 +741,9 @@ __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ 
                                                    const uint32_t *__restrict__ deal) {
     __shared__ Shared sh;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#if defined(Q4RDNA_SWEEP_CLOCKS)
+    const uint64_t clock_start = __builtin_amdgcn_s_memrealtime();
+#endif
     const LaneRole ln = lane_role(lane);
     const uint2 *entry = reinterpret_cast<const uint2 *>(deal + ((gridDim.x + 2) & ~1u));
     const uint32_t end = deal[blockIdx.x + 1];
@@ -782,6 +789,15 @@ __global__ __launch_bounds__(256) void plan_kernel(const PlanDesc *__restrict__ 
         if (k >= end) break;
         cur = next;
     }
+#if defined(Q4RDNA_SWEEP_CLOCKS)
+    // After the last item's stores have left: this workgroup's end.
+    __syncthreads();
+    if (threadIdx.x == 0 && blockIdx.x < kMaxSweepClocks) {
+        const uint64_t clock_end = __builtin_amdgcn_s_memrealtime();
+        g_sweep_clocks[2 * blockIdx.x] = clock_start;
+        g_sweep_clocks[2 * blockIdx.x + 1] = clock_end;
+    }
+#endif
 }
 
 // ---- the sweep in the VALU formulation (kSweepValu) -------------------------
@@ -1137,6 +1153,18 @@ __global__ __launch_bounds__(64 * kBatchWaves) void plan_batch_kernel(const Plan
 }
 
 }  // namespace
+
+#if defined(Q4RDNA_SWEEP_CLOCKS)
+}  // namespace q4rdna
+// Clock build only: the latest sweep's per-workgroup (start, end) clocks,
+// 2 * count values for workgroups 0..count-1 (count <= kMaxSweepClocks).
+extern "C" int q4rdna_sweep_clocks(uint64_t *out, uint32_t count) {
+    if (out == nullptr || count > q4rdna::kMaxSweepClocks) return -1;
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(q4rdna::g_sweep_clocks), 2 * sizeof(uint64_t) * count, 0,
+                               hipMemcpyDeviceToHost) == hipSuccess ? 0 : -4;
+}
+namespace q4rdna {
+#endif
 
 hipError_t launch_prep(const float *const *group_x, uint8_t *prep, uint32_t groups, hipStream_t stream) {
     if (groups == 0) return hipSuccess;
