@@ -120,7 +120,9 @@ int q4rdna_scope_allows(const char *scope, const char *name);
  * y[M] = W[M][K] x[K] in fp32 accumulation.  x_ne0 must equal K and y_ne0 M
  * (the reference's src1->ne[0] / dst->ne[0] checks); any mismatch, a weight
  * on another device or a NULL weight returns NOT_APPLICABLE with nothing
- * launched.  x and y are contiguous fp32 device buffers (4-byte aligned).
+ * launched.  x and y are contiguous fp32 device buffers (4-byte aligned);
+ * y may not overlap x, and an add vector is either y itself or apart from
+ * it (argument errors otherwise).
  *
  * Launches with split K use a scratch buffer per (device, stream).  The
  * first call that needs more than the stream has allocates it (and waits

@@ -223,6 +223,19 @@ int check_io(const float *x, const float *y) {
     return Q4RDNA_OK;
 }
 
+// The kernels read x while other workgroups write y, so the two may not
+// share memory; add may be y itself (each row's add is read by the thread
+// that writes that row) but may not overlap it otherwise.  Sizes in floats.
+int check_overlap(const float *x, size_t nx, const float *y, size_t ny, const float *add) {
+    const uintptr_t x0 = reinterpret_cast<uintptr_t>(x), y0 = reinterpret_cast<uintptr_t>(y);
+    if (y0 < x0 + 4 * nx && x0 < y0 + 4 * ny) return set_error(Q4RDNA_ERR_ARGUMENT, "y overlaps x");
+    if (add != nullptr && add != y) {
+        const uintptr_t a0 = reinterpret_cast<uintptr_t>(add);
+        if (a0 < y0 + 4 * ny && y0 < a0 + 4 * ny) return set_error(Q4RDNA_ERR_ARGUMENT, "add overlaps y without being y");
+    }
+    return Q4RDNA_OK;
+}
+
 // Launch options beyond split_k: the kernel is the VALU kernel (0 = the
 // policy, which is that kernel) and the reserved words are zero.
 int check_options(const q4rdna_launch_options *options) {
@@ -250,6 +263,7 @@ int check_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const fl
     }
     if ((rc = check_io(x, y)) != Q4RDNA_OK) return rc;
     if (add != nullptr && !aligned(add, 4)) return set_error(Q4RDNA_ERR_ARGUMENT, "misaligned add");
+    if ((rc = check_overlap(x, w->columns, y, w->rows, add)) != Q4RDNA_OK) return rc;
     const uint32_t s = options ? options->split_k : 0;
     if (s > kMaxSplit) return set_error(Q4RDNA_ERR_ARGUMENT, "split_k %u exceeds %u", s, kMaxSplit);
     if ((rc = check_options(options)) != Q4RDNA_OK) return rc;
@@ -780,6 +794,9 @@ int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, cons
     if ((rc = check_io(x, y)) != Q4RDNA_OK) return rc;
     if (add != nullptr && !aligned(add, 4)) return set_error(Q4RDNA_ERR_ARGUMENT, "misaligned add");
     if (n < 1 || n > Q4RDNA_MAX_BATCH) return set_error(Q4RDNA_ERR_ARGUMENT, "batch %u is outside 1..%d", n, Q4RDNA_MAX_BATCH);
+    if ((rc = check_overlap(x, static_cast<size_t>(n) * w->columns, y, static_cast<size_t>(n) * w->rows, add)) !=
+        Q4RDNA_OK)
+        return rc;
     uint32_t split = options ? options->split_k : 0;
     if (split > kMaxSplit) return set_error(Q4RDNA_ERR_ARGUMENT, "split_k %u exceeds %u", split, kMaxSplit);
     if ((rc = check_options(options)) != Q4RDNA_OK) return rc;

@@ -13,7 +13,7 @@ import torch
 
 import oracle as O
 import q4rdna
-from q4rdna import api
+from q4rdna import _lib, api
 from conftest import GATE_TOL, REL_L2_TOL, assert_gemv_parity, bf16_to_f32
 
 pytestmark = pytest.mark.gpu
@@ -294,6 +294,33 @@ def test_not_applicable_leaves_output_untouched(cuda):
     torch.cuda.synchronize()
     assert (y.cpu() == 7.0).all() and (y2.cpu() == 7.0).all()
     assert "shape mismatch" in q4rdna.last_error()
+
+
+def test_overlapping_buffers_are_refused(cuda):
+    """y overlapping x, and an add that overlaps y without being y, are
+    argument errors that launch nothing (the kernels read x and add while
+    other workgroups write y); add may be y itself, the in-place residual."""
+    rows, cols = 256, 512
+    t = random_tiles(rows, cols, 31)
+    w = api.QWeight.from_tiles(dev_u8(t), rows, cols)
+    buf = torch.full((cols + rows,), 7.0, device="cuda")
+    with pytest.raises(_lib.Q4RdnaError):          # y's first rows are x's last columns
+        api.mul_mat(w, buf[:cols], buf[cols - 16:cols - 16 + rows])
+    y = torch.full((rows,), 7.0, device="cuda")
+    add = torch.full((rows + 8,), 1.0, device="cuda")
+    with pytest.raises(_lib.Q4RdnaError):          # add shifted by 8 rows against y
+        api.mul_mat_add(w, dev_f32(O.gaussian_x(cols, 32)), add[8:], add[:rows])
+    xb = torch.zeros(2, cols, device="cuda")
+    with pytest.raises(_lib.Q4RdnaError):          # n vectors: y inside x's second vector
+        api.mul_mat_batch(w, xb, xb.view(-1)[cols:cols + 2 * rows].view(2, rows))
+    torch.cuda.synchronize()
+    assert (buf.cpu() == 7.0).all() and (y.cpu() == 7.0).all() and (xb.cpu() == 0.0).all()
+    x = O.gaussian_x(cols, 33)
+    res = O.gaussian_x(rows, 34)
+    y_in = dev_f32(res)                             # add is y: the residual in place
+    assert api.mul_mat_add(w, dev_f32(x), y_in, y_in) is not None
+    torch.cuda.synchronize()
+    assert_gemv_parity(y_in.cpu().numpy(), t, rows, cols, x, add=res, label="in place")
 
 
 # ----------------------------------------------------------------- sidecar
