@@ -248,9 +248,12 @@ int q4rdna_mul_mat_ex_noalloc(const q4rdna_weight *w, const q4rdna_weight *gate,
 /* ---- multi-tensor stack --------------------------------------------------
  * One launch that sweeps many independent GEMVs (a decode step's weight
  * streaming).  The GEMVs run concurrently and in an order the plan picks
- * (longest K chunks first), so no descriptor's x, add or y may alias
- * another's y.  No reference counterpart: the reference launches one kernel
- * per tensor (source/q4rdna.cu:736-741). */
+ * (longest K chunks first), so no descriptor's x, add or y may overlap
+ * another's y, and an add is its own y or apart from it (plan creation
+ * refuses these with an argument error).  A descriptor's x may overlap its
+ * own y: the prepare launch reads every x before the sweep writes.  No
+ * reference counterpart: the reference launches one kernel per tensor
+ * (source/q4rdna.cu:736-741). */
 typedef struct q4rdna_gemv_desc {
     q4rdna_weight weight;      /* W (the up projection for SwiGLU) */
     const uint8_t *gate_tiles; /* SwiGLU gate tiles of the same shape, or NULL */

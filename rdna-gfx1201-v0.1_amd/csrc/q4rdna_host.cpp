@@ -245,6 +245,50 @@ int layout_plan(const q4rdna_gemv_desc *descs, uint32_t count, uint32_t n, int d
         if (d.weight.device != device)
             return fail(error, Q4RDNA_ERR_ARGUMENT, "descriptor %u lives on device %d", i, d.weight.device);
     }
+    // The GEMVs run concurrently: no y may overlap another descriptor's y,
+    // x or add, and a descriptor's add is its own y or apart from it.  The
+    // outputs are checked sorted by address (they must be disjoint), then
+    // each input range against them by binary search.  A descriptor's x may
+    // overlap its own y: the prepare launch reads every x before the sweep
+    // writes any y.
+    {
+        struct Range {
+            uintptr_t lo, hi;
+            uint32_t owner;
+        };
+        std::vector<Range> ys(count);
+        for (uint32_t i = 0; i < count; ++i) {
+            const uintptr_t y0 = reinterpret_cast<uintptr_t>(descs[i].y);
+            ys[i] = {y0, y0 + 4ull * n * descs[i].weight.rows, i};
+        }
+        std::sort(ys.begin(), ys.end(), [](const Range &a, const Range &b) { return a.lo < b.lo; });
+        for (uint32_t i = 1; i < count; ++i)
+            if (ys[i].lo < ys[i - 1].hi)
+                return fail(error, Q4RDNA_ERR_ARGUMENT, "descriptors %u and %u: outputs overlap", ys[i - 1].owner,
+                            ys[i].owner);
+        // Every output that [lo, hi) meets, owner by owner.
+        auto meets = [&](uintptr_t lo, uintptr_t hi, uint32_t self, bool is_add, const float *own_y) -> int {
+            auto it = std::upper_bound(ys.begin(), ys.end(), lo, [](uintptr_t v, const Range &r) { return v < r.hi; });
+            for (; it != ys.end() && it->lo < hi; ++it) {
+                if (it->owner != self)
+                    return fail(error, Q4RDNA_ERR_ARGUMENT, "descriptor %u: its %s overlaps descriptor %u's y", self,
+                                is_add ? "add" : "x", it->owner);
+                if (is_add && reinterpret_cast<uintptr_t>(own_y) != lo)
+                    return fail(error, Q4RDNA_ERR_ARGUMENT, "descriptor %u: add overlaps y without being y", self);
+            }
+            return Q4RDNA_OK;
+        };
+        for (uint32_t i = 0; i < count; ++i) {
+            const q4rdna_gemv_desc &d = descs[i];
+            const uintptr_t x0 = reinterpret_cast<uintptr_t>(d.x);
+            int rc = meets(x0, x0 + 4ull * n * d.weight.columns, i, false, d.y);
+            if (rc == Q4RDNA_OK && d.add != nullptr) {
+                const uintptr_t a0 = reinterpret_cast<uintptr_t>(d.add);
+                rc = meets(a0, a0 + 4ull * n * d.weight.rows, i, true, d.y);
+            }
+            if (rc != Q4RDNA_OK) return rc;
+        }
+    }
     PlanLayout L;
     L.count = count;
     L.batch = n;

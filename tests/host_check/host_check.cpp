@@ -208,6 +208,37 @@ int run_layout() {
     bad = make_descs({{32, 64, false, false}}, 1);
     bad[0].weight.device = 1;
     expect(q4rdna::host::layout_plan(bad.data(), 1, 1, 0, 256, &L, &error) == Q4RDNA_ERR_ARGUMENT, "other device", "errors");
+    // Aliasing: outputs overlapping each other, another descriptor's x or
+    // add on a y, an add that overlaps its own y without being it.  Shared
+    // x, a descriptor's x on its own y and an add that is its own y are fine.
+    const std::vector<Shape> two = {{64, 512, false, true}, {64, 512, false, true}};
+    std::vector<q4rdna_gemv_desc> d2 = make_descs(two, 2);
+    expect(q4rdna::host::layout_plan(d2.data(), 2, 2, 0, 256, &L, &error) == Q4RDNA_OK, "disjoint", "aliasing");
+    bad = d2;
+    bad[1].y = bad[0].y + 32;
+    expect(q4rdna::host::layout_plan(bad.data(), 2, 2, 0, 256, &L, &error) == Q4RDNA_ERR_ARGUMENT, "outputs overlap",
+           "aliasing");
+    bad = d2;
+    bad[1].x = reinterpret_cast<const float *>(bad[0].y);
+    expect(q4rdna::host::layout_plan(bad.data(), 2, 2, 0, 256, &L, &error) == Q4RDNA_ERR_ARGUMENT,
+           "x on another's y", "aliasing");
+    bad = d2;
+    bad[1].add = bad[0].y + 1;
+    expect(q4rdna::host::layout_plan(bad.data(), 2, 2, 0, 256, &L, &error) == Q4RDNA_ERR_ARGUMENT,
+           "add on another's y", "aliasing");
+    bad = d2;
+    bad[0].add = bad[0].y + 4;
+    expect(q4rdna::host::layout_plan(bad.data(), 2, 2, 0, 256, &L, &error) == Q4RDNA_ERR_ARGUMENT,
+           "add shifted on its own y", "aliasing");
+    std::vector<q4rdna_gemv_desc> ok = d2;
+    ok[1].x = ok[0].x;    // a shared activation
+    ok[0].add = ok[0].y;  // the residual in place
+    expect(q4rdna::host::layout_plan(ok.data(), 2, 2, 0, 256, &L, &error) == Q4RDNA_OK, "shared x, add is y",
+           "aliasing");
+    ok = d2;
+    ok[0].x = reinterpret_cast<const float *>(ok[0].y);  // read by the prepare launch before the sweep writes y
+    expect(q4rdna::host::layout_plan(ok.data(), 2, 2, 0, 256, &L, &error) == Q4RDNA_OK, "x on its own y",
+           "aliasing");
     std::printf("{\"failures\": %d}\n", g_failures);
     return g_failures == 0 ? 0 : 1;
 }
