@@ -825,6 +825,62 @@ def layer_chain(tensors, replays: int, check_layers=(0, 17, 35),
     return out
 
 
+def shard_stacks(steps: int, warmup: int, tps=(2, 4, 8), layers: int = 36, seed: int = 0x51EE0000):
+    """One GPU's share of the stack under tensor parallelism over TP GPUs,
+    at its real shapes: q, k, v, gate and up split by rows (rows / TP, a
+    pointer offset into the packed tensor), o and down split along K
+    (columns / TP, repacked per GPU), every GEMV at batch 1 with its own x.
+    The collective that would follow o and down (an fp32 all-reduce of 16 KB
+    per layer) is outside this measurement.  For each TP: the per-GPU stack
+    of 7 * layers shard GEMVs as one plan per step (0.5 s settle, then warmup
+    and timed steps as the main bench), the same GEMVs as one launch per
+    tensor replayed from a HIP graph, and three shard GEMVs against the fp64
+    oracle."""
+    import torch
+    from q4rdna import api
+    dev = torch.device("cuda", 0)
+    out = []
+    for tp in tps:
+        shapes = []
+        for _ in range(layers):
+            shapes += [("q", 4096 // tp, 4096), ("k", 1024 // tp, 4096), ("v", 1024 // tp, 4096),
+                       ("o", 4096, 4096 // tp), ("gate", 12288 // tp, 4096), ("up", 12288 // tp, 4096),
+                       ("down", 4096, 12288 // tp)]
+        gen = torch.Generator(device=dev)
+        tensors = []
+        for i, (name, rows, cols) in enumerate(shapes):
+            gen.manual_seed(seed + 97 * tp + i)
+            w = torch.randn(rows, cols, generator=gen, device=dev).mul_(0.02)
+            tiles = api.pack(w)
+            del w
+            x = torch.randn(cols, generator=gen, device=dev)
+            tensors.append(dict(name=name, rows=rows, cols=cols, w=api.QWeight.from_tiles(tiles, rows, cols), x=x,
+                                y=torch.empty(rows, device=dev)))
+        torch.cuda.synchronize()
+        nbytes = sum(algorithmic_bytes(t["rows"], t["cols"]) for t in tensors)
+        plan = api.Plan([(t["w"], t["x"], t["y"]) for t in tensors])
+        settle(plan, 0.5)
+        ms, sweep_ms, prep_ms = time_plan(plan, steps, warmup)
+        parity = check_parity(tensors, [0, 3, 6])
+        per_tensor_us, same = time_per_tensor_graph(tensors, max(5, steps // 5), 3)
+        row = dict(tp=tp, gemvs=len(tensors), algorithmic_bytes=nbytes,
+                   shapes={n: [r, c] for n, r, c in shapes[:7]},
+                   plan_us_per_stack=round(ms * 1000.0, 2), plan_sweep_us=round(mean(sweep_ms) * 1000.0, 2),
+                   plan_gb_per_s=round(nbytes / (ms / 1000.0) / 1e9, 1),
+                   plan_pct_of_peak=round(100.0 * nbytes / (ms / 1000.0) / 1e9 / PEAK_GBS, 2),
+                   per_tensor_us_per_stack=round(per_tensor_us, 2),
+                   per_tensor_gb_per_s=round(nbytes / per_tensor_us / 1e3, 1), graph_replays_equal_eager=same,
+                   parity_gate_max=parity, workgroups=plan.workgroups)
+        log(f"[shards] TP{tp}: {len(tensors)} GEMVs, {nbytes} B per GPU: plan {row['plan_us_per_stack']} us "
+            f"({row['plan_gb_per_s']} GB/s), per-tensor graph {row['per_tensor_us_per_stack']} us, "
+            f"parity gate {parity:.2e}")
+        out.append(row)
+        plan.close()
+        del tensors, plan
+        torch.cuda.empty_cache()
+    return out
+
+
 def sweep_clocks(plan, launches: int = 20):
     """Per-workgroup start and end of the stack sweep, from the clock build
     of the library (`--library .../libq4rdna_sweep_clocks_gfx950.so`): each
@@ -1025,6 +1081,10 @@ def main() -> int:
                     help="load this build of the library instead of the default (e.g. "
                          "rdna-gfx1201-v0.1_amd/q4rdna/libq4rdna_valu_sweep_gfx950.so, the sweep in the VALU "
                          "formulation, for the MFMA-against-VALU measurement)")
+    ap.add_argument("--shards", action="store_true",
+                    help="one GPU's share of the stack under tensor parallelism (TP 2, 4, 8: row- and K-split "
+                         "shapes), as a plan and as per-tensor launches; prints one JSON line instead of the stack "
+                         "bench")
     ap.add_argument("--clocks", action="store_true",
                     help="per-workgroup start and end clocks of the stack sweep (needs --library with the clock "
                          "build, libq4rdna_sweep_clocks_gfx950.so); prints one JSON line instead of the stack bench")
@@ -1051,6 +1111,9 @@ def main() -> int:
 
     if args.tensors:
         print(json.dumps({"per_tensor": tensor_table(args.seed)}), flush=True)
+        return 0
+    if args.shards:
+        print(json.dumps({"shards": shard_stacks(args.steps, args.warmup, layers=args.layers)}), flush=True)
         return 0
 
     tensors, _data = build_stack(args.layers, args.seed)
