@@ -199,8 +199,9 @@ int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, cons
  * x is read once per workgroup in the kernel (no separate prepare launch).
  * options->split_k applies (0 = the shape policy for the group's total rows,
  * raised until every K chunk holds at most 64 groups; K above 262,144
- * columns, 64 chunks of 64 groups, is NOT_APPLICABLE).  Each output equals q4rdna_mul_mat_ex of its
- * weight at the group's split bit for bit when both launches run the same
+ * columns, 64 chunks of 64 groups, is NOT_APPLICABLE).  Each output equals
+ * q4rdna_mul_mat_ex of its weight at the group's split bit for bit when
+ * both launches run the same
  * workgroup width: eight waves, which each launch uses while it has at most
  * four workgroups per CU (rows / 32 * split of the whole group, or of the one
  * weight), and four waves above that.  The split-K scratch is the stream's,
