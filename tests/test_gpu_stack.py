@@ -1,8 +1,9 @@
 """GPU parity at the bench's own scale, through the C ABI: the lm_head shape
 (151936 x 4096) through the per-tensor kernel and a plan, the full Qwen3-8B
 36-layer stack as the 252-GEMV plan and as the 216-GEMV SwiGLU-fused plan
-at their real item deal (512 workgroups, two per CU), and plans of more
-items than workgroups with every item kind, single-vector and batched.
+at their real item deal (512 workgroups, two per CU), plans of more
+items than workgroups with every item kind, single-vector and batched, and
+one decoder layer at an 8-way tensor-parallel GPU's shard shapes.
 
 Bars (tests/conftest.py): per row 1e-3 of max(|y64|, 0.01 rms) against the
 fp64 oracle, and relative L2 <= 1e-5 against the reference bench's
@@ -338,3 +339,45 @@ def test_batched_plan_with_many_items(cuda):
         for v in range(3):
             assert_gemv_parity(yh[v], g["t"], g["rows"], g["cols"], g["xs"][v], gate_tiles=g["gt"],
                                add=None if g["adds"] is None else g["adds"][v], label=(g["kind"], v))
+
+
+@pytest.mark.gpu
+def test_tensor_parallel_shard_layer(cuda):
+    """One decoder layer at an 8-way tensor-parallel GPU's shard shapes (the
+    shapes bench.py --shards measures): q / k / v / gate / up split by rows
+    (512, 128, 128, 1536, 1536 rows of K = 4096), o and down split along K
+    (4096 x 512 with the residual add, 4096 x 1536 + add), gate/up as one
+    SwiGLU GEMV.  Per-tensor launches and one plan, every output against
+    both bars; the plan's outputs equal each other across two launches."""
+    shapes = [("q", 512, 4096, None), ("k", 128, 4096, None), ("v", 128, 4096, None), ("o", 4096, 512, "add"),
+              ("ffn", 1536, 4096, "glu"), ("down", 4096, 1536, "add")]
+    items, checks = [], []
+    for i, (name, rows, cols, kind) in enumerate(shapes):
+        t = random_tiles(rows, cols, 2100 + i)
+        x = O.gaussian_x(cols, 2200 + i)
+        gt = add_np = None
+        w = api.QWeight.from_tiles(dev_u8(t), rows, cols)
+        gate = add = None
+        if kind == "glu":
+            gt = random_tiles(rows, cols, 2300 + i)
+            gate = api.QWeight.from_tiles(dev_u8(gt), rows, cols)
+        if kind == "add":
+            add_np = O.gaussian_x(rows, 2400 + i)
+            add = dev_f32(add_np)
+        xd = dev_f32(x)
+        y1 = torch.full((rows,), float("nan"), device="cuda")
+        assert api.mul_mat_ex(w, xd, y1, gate=gate, add=add)
+        y = torch.full((rows,), float("nan"), device="cuda")
+        items.append((w, xd, y, gate, add))
+        checks.append((name, t, gt, x, add_np, rows, cols, y, y1))
+    plan = api.Plan(items)
+    assert plan.launch()
+    torch.cuda.synchronize()
+    first = [c[7].clone() for c in checks]
+    assert plan.launch()
+    torch.cuda.synchronize()
+    for (name, t, gt, x, add_np, rows, cols, y, y1), f in zip(checks, first):
+        assert torch.equal(y, f), name
+        assert_gemv_parity(y.cpu().numpy(), t, rows, cols, x, gate_tiles=gt, add=add_np, label=("plan", name))
+        assert_gemv_parity(y1.cpu().numpy(), t, rows, cols, x, gate_tiles=gt, add=add_np, label=("per tensor", name))
+    plan.close()
