@@ -150,9 +150,11 @@ def bench_lib():
         lib = ctypes.CDLL(path)
         lib.q4bench_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
         lib.q4bench_empty.argtypes = [ctypes.c_uint32, ctypes.c_void_p]
+        lib.q4bench_stream_runs.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                            ctypes.c_void_p, ctypes.c_void_p]
         lib.q4bench_rms_norm.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_float,
                                          ctypes.c_void_p]
-        for f in (lib.q4bench_stream_read, lib.q4bench_empty, lib.q4bench_rms_norm):
+        for f in (lib.q4bench_stream_read, lib.q4bench_empty, lib.q4bench_rms_norm, lib.q4bench_stream_runs):
             f.restype = ctypes.c_int
         _BENCH_LIB = lib
     return _BENCH_LIB
@@ -527,23 +529,29 @@ def time_tensor(rows: int, cols: int, split: int, seed: int, reps: int = 40):
     return us, copies
 
 
+def batch_plan(tensors, n: int, seed: int):
+    """The stack's GEMVs with n fresh N(0, 1) activation vectors each, as one
+    batched plan: (plan, [(weight, x [n, K], y [n, M])])."""
+    import torch
+    from q4rdna import api
+    gen = torch.Generator(device="cuda")
+    items = []
+    for i, t in enumerate(tensors):
+        gen.manual_seed(seed + 0x4000 + 1000 * n + i)
+        x = torch.randn(n, t["cols"], generator=gen, device="cuda", dtype=torch.float32)
+        y = torch.empty(n, t["rows"], device="cuda", dtype=torch.float32)
+        items.append((t["w"], x, y))
+    return api.Plan(items, batch=n), items
+
+
 def batch_table(tensors, batches, steps: int, warmup: int, seed: int):
     """The stack's 252 GEMVs with N activation vectors each (the small-batch
     decode shapes): one batched plan per N over the same weights, timed like
     the main bench; parity of every vector of three tensors vs the oracle."""
-    import torch
     import oracle as O
-    from q4rdna import api
     out = []
-    gen = torch.Generator(device="cuda")
     for n in batches:
-        items = []
-        for i, t in enumerate(tensors):
-            gen.manual_seed(seed + 0x4000 + 1000 * n + i)
-            x = torch.randn(n, t["cols"], generator=gen, device="cuda", dtype=torch.float32)
-            y = torch.empty(n, t["rows"], device="cuda", dtype=torch.float32)
-            items.append((t["w"], x, y))
-        plan = api.Plan(items, batch=n)
+        plan, items = batch_plan(tensors, n, seed)
         settle(plan, 0.2)
         ms_per_step, sweep_ms, prep_ms = time_plan(plan, steps, warmup)
         step_bytes = sum(algorithmic_bytes(t["rows"], t["cols"], n) for t in tensors)
@@ -941,6 +949,47 @@ def sweep_clocks(plan, launches: int = 20):
                 per_workgroup_end_std_us=round(float(np.median(np.std(np.stack(ends), axis=0))), 2))
 
 
+def stream_runs(data, launches: int = 5):
+    """The sweeps' access pattern as a plain read of the stack buffer
+    (bench library `stream_runs_kernel`): 2 workgroups per CU, four waves
+    each, one step of eight 1 KB loads per wave in flight; each workgroup
+    reads its share as R contiguous runs (R = 2: the single-vector sweep's
+    two row tiles per workgroup; R = 8: the batched sweep's eight).  After
+    0.5 s of settling, each R is timed over `launches` launches between HIP
+    events, in two passes (R ascending, then descending)."""
+    import torch
+    lib = bench_lib()
+    sink = torch.zeros(512, dtype=torch.int32, device="cuda")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    wgs = 2 * cus
+    lines = (data.numel() // 1024 // wgs) // 32 * 32
+    nbytes = wgs * lines * 1024
+    s = torch.cuda.current_stream().cuda_stream
+
+    def launch(r):
+        bench_call(lib.q4bench_stream_runs(data.data_ptr(), wgs, lines, r, sink.data_ptr(), s), "stream runs")
+
+    t_end = time.perf_counter() + 0.5
+    while time.perf_counter() < t_end:
+        launch(2)
+        torch.cuda.synchronize()
+    runs = (1, 2, 4, 8, 16, 32)
+    us = {r: [] for r in runs}
+    for order in (runs, runs[::-1]):
+        for r in order:
+            launch(r)
+            a, e = KernelEvent(), KernelEvent()
+            a.record(s)
+            for _ in range(launches):
+                launch(r)
+            e.record(s)
+            torch.cuda.synchronize()
+            us[r].append(a.elapsed_ms(e) * 1000.0 / launches)
+    return dict(workgroups=wgs, lines_per_workgroup=lines, bytes=nbytes,
+                rows=[dict(runs=r, us=[round(v, 2) for v in us[r]],
+                           gb_per_s=round(nbytes / min(us[r]) / 1e3, 1)) for r in runs])
+
+
 def floors(tensors, data, replays: int = 20):
     """What the GEMV launches are measured against, from plain reads of the
     same bytes (bench library kernels; graph replays, each read a different
@@ -1087,10 +1136,14 @@ def main() -> int:
                          "bench")
     ap.add_argument("--clocks", action="store_true",
                     help="per-workgroup start and end clocks of the stack sweep (needs --library with the clock "
-                         "build, libq4rdna_sweep_clocks_gfx950.so); prints one JSON line instead of the stack bench")
+                         "build, libq4rdna_sweep_clocks_gfx950.so), of the batched sweeps with --batches; prints "
+                         "one JSON line instead of the stack bench")
     ap.add_argument("--floors", action="store_true",
                     help="plain-read and launch floors (stack read, empty launch, per-stage reads and four "
                          "dependent stage reads per layer); prints one JSON line instead of the stack bench")
+    ap.add_argument("--stream-runs", action="store_true",
+                    help="the sweeps' access pattern as a plain read of the stack buffer, with each workgroup "
+                         "reading 1..32 contiguous runs; prints one JSON line")
     ap.add_argument("--stage-launches", action="store_true",
                     help="each decoder-layer stage's GEMV once per layer, eagerly, for rocprofv3 --pmc "
                          "(no graph, no normalizations); prints one JSON line")
@@ -1124,11 +1177,23 @@ def main() -> int:
     if args.floors:
         print(json.dumps({"floors": floors(tensors, _data)}), flush=True)
         return 0
+    if args.stream_runs:
+        print(json.dumps({"stream_runs": stream_runs(_data)}), flush=True)
+        return 0
     if args.stage_launches:
         print(json.dumps({"stage_launches": stage_launches(tensors)}), flush=True)
         return 0
     if args.batches:
         sizes = [int(v) for v in args.batches.split(",") if v]
+        if args.clocks:
+            rows = []
+            for n in sizes:
+                plan, _items = batch_plan(tensors, n, args.seed)
+                rows.append(dict(batch=n, **sweep_clocks(plan, max(args.steps, 10))))
+                log(f"[clocks] N={n}: {rows[-1]}")
+                plan.close()
+            print(json.dumps({"batched_sweep_clocks": rows}), flush=True)
+            return 0
         print(json.dumps({"batched": batch_table(tensors, sizes, args.steps, args.warmup, args.seed)}), flush=True)
         return 0
     plan = api.Plan([(t["w"], t["x"], t["y"]) for t in tensors])

@@ -195,16 +195,16 @@ int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, cons
  * 1..Q4RDNA_MAX_GROUP; every weight has K = x_ne0 columns (else
  * NOT_APPLICABLE) and lives on the current device; gate_tiles is given for
  * every descriptor or for none, each of its weight's shape; no y may overlap
- * x, another descriptor's y or another descriptor's add (argument error).
- * x is read once per workgroup in the kernel (no separate prepare launch).
- * options->split_k applies (0 = the shape policy for the group's total rows,
- * raised until every K chunk holds at most 64 groups; K above 262,144
- * columns, 64 chunks of 64 groups, is NOT_APPLICABLE).  Each output equals
- * q4rdna_mul_mat_ex of its weight at the group's split bit for bit when
- * both launches run the same
- * workgroup width: eight waves, which each launch uses while it has at most
- * four workgroups per CU (rows / 32 * split of the whole group, or of the one
- * weight), and four waves above that.  The split-K scratch is the stream's,
+ * x, another descriptor's y or another descriptor's add, and a descriptor's
+ * add is its own y or apart from it (argument error).  x is read once per
+ * workgroup in the kernel (no separate prepare launch).  options->split_k
+ * applies (0 = the shape policy for the group's total rows, raised until
+ * every K chunk holds at most 64 groups; K above 262,144 columns, 64 chunks
+ * of 64 groups, is NOT_APPLICABLE).  Each output equals q4rdna_mul_mat_ex of
+ * its weight at the group's split bit for bit when both launches run the
+ * same workgroup width: eight waves, which each launch uses while it has at
+ * most four workgroups per CU (rows / 32 * split of the whole group, or of
+ * the one weight), and four waves above that.  The split-K scratch is the stream's,
  * as for q4rdna_mul_mat.  No reference counterpart: the reference launches
  * one kernel per projection and fuses only gate/up
  * (source/q4rdna.cu:736-741,769-793). */

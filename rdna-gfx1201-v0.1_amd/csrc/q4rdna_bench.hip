@@ -36,6 +36,44 @@ __global__ __launch_bounds__(kReadThreads) void stream_read_kernel(const uint32_
     if (flag != 0 && acc == flag) sink[threadIdx.x] = acc;
 }
 
+// The sweeps' access pattern, as a plain read: `gridDim.x` persistent
+// workgroups of four waves, each wave with one step of eight 1 KB loads
+// (64 lanes x 16 bytes, nontemporal) in flight at a time.  Workgroup b reads
+// `lines` 1 KB lines from b * lines on as `runs` contiguous runs of
+// lines / runs; load c of wave w in workgroup step s reads run
+// (8w + c) % runs at line s * (32 / runs) + (8w + c) / runs.  runs = 2 is
+// the single-vector sweep's pattern (two row tiles per workgroup, four
+// consecutive groups per wave step), runs = 8 the batched sweep's (eight row
+// tiles, one group per wave step).  lines is a multiple of 32 and runs
+// divides 32; the XOR goes to `sink` only when it equals `flag`, which the
+// caller never passes nonzero.
+__global__ __launch_bounds__(256) void stream_runs_kernel(const uint8_t *__restrict__ p, uint32_t lines,
+                                                          uint32_t runs, uint32_t *sink, uint32_t flag) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint8_t *base = p + static_cast<uint64_t>(blockIdx.x) * lines * 1024 + 16 * lane;
+    const uint32_t run_lines = lines / runs, per_step = 32 / runs;
+    uint32_t run_off[8], pos_off[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const uint32_t i = 8 * wave + c;
+        run_off[c] = (i % runs) * run_lines;
+        pos_off[c] = i / runs;
+    }
+    uint32_t acc = 0;
+#pragma unroll 1
+    for (uint32_t s = 0; s < lines / 32; ++s) {
+        q4rdna::i32x4 v[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            v[c] = __builtin_nontemporal_load(
+                (q4rdna::gptr_i32x4)(base + static_cast<uint64_t>(run_off[c] + s * per_step + pos_off[c]) * 1024));
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc ^= static_cast<uint32_t>(v[c][0] ^ v[c][1] ^ v[c][2] ^ v[c][3]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (flag != 0 && acc == flag) sink[threadIdx.x] = acc;
+}
+
 __global__ void empty_kernel() {}
 
 // y = x * rsqrt(mean(x^2) + eps) by one workgroup of 1024 threads.
@@ -70,6 +108,19 @@ int q4bench_stream_read(const void *p, uint64_t bytes, uint32_t *sink, hipStream
     if (blocks > 0x7fffffffull) return static_cast<int>(hipErrorInvalidValue);
     hipLaunchKernelGGL(stream_read_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kReadThreads), 0, stream,
                        static_cast<const uint32_t *>(p), bytes / 4, sink, 0u);
+    return static_cast<int>(hipGetLastError());
+}
+
+// One launch of stream_runs_kernel: `workgroups` x 256 threads, each
+// workgroup reading `lines` 1 KB lines as `runs` runs; the buffer at p must
+// hold workgroups * lines KB.
+int q4bench_stream_runs(const void *p, uint32_t workgroups, uint32_t lines, uint32_t runs, uint32_t *sink,
+                        hipStream_t stream) {
+    if (p == nullptr || sink == nullptr || workgroups == 0 || lines == 0 || lines % 32 != 0 || runs == 0 ||
+        32 % runs != 0)
+        return static_cast<int>(hipErrorInvalidValue);
+    hipLaunchKernelGGL(stream_runs_kernel, dim3(workgroups), dim3(256), 0, stream, static_cast<const uint8_t *>(p),
+                       lines, runs, sink, 0u);
     return static_cast<int>(hipGetLastError());
 }
 

@@ -753,17 +753,20 @@ int q4rdna_mul_mat_group(const q4rdna_group_desc *descs, uint32_t count, const f
         if (y0 < x1 && x0 < y1) return set_error(Q4RDNA_ERR_ARGUMENT, "descriptor %u: y overlaps x", i);
     }
     // Workgroups of different GEMVs run unordered: an output may not overlap
-    // another GEMV's output or bias.
+    // another GEMV's output or bias.  A GEMV's own add is read, row by row,
+    // by the thread that writes that row of y, so it may be y itself but may
+    // not overlap it otherwise.
     for (uint32_t i = 0; i < count; ++i) {
         const uintptr_t a0 = reinterpret_cast<uintptr_t>(descs[i].y), a1 = a0 + 4ull * descs[i].weight.rows;
         for (uint32_t j = 0; j < count; ++j) {
-            if (j == i) continue;
             const uintptr_t b0 = reinterpret_cast<uintptr_t>(descs[j].y), b1 = b0 + 4ull * descs[j].weight.rows;
-            if (a0 < b1 && b0 < a1) return set_error(Q4RDNA_ERR_ARGUMENT, "descriptors %u and %u: outputs overlap", i, j);
-            if (descs[j].add != nullptr) {
-                const uintptr_t c0 = reinterpret_cast<uintptr_t>(descs[j].add), c1 = c0 + 4ull * descs[j].weight.rows;
-                if (a0 < c1 && c0 < a1)
-                    return set_error(Q4RDNA_ERR_ARGUMENT, "descriptor %u: y overlaps descriptor %u's add", i, j);
+            if (j != i && a0 < b1 && b0 < a1)
+                return set_error(Q4RDNA_ERR_ARGUMENT, "descriptors %u and %u: outputs overlap", i, j);
+            if (descs[j].add == nullptr || (j == i && descs[j].add == descs[i].y)) continue;
+            const uintptr_t c0 = reinterpret_cast<uintptr_t>(descs[j].add), c1 = c0 + 4ull * descs[j].weight.rows;
+            if (a0 < c1 && c0 < a1) {
+                if (j == i) return set_error(Q4RDNA_ERR_ARGUMENT, "descriptor %u: add overlaps y without being y", i);
+                return set_error(Q4RDNA_ERR_ARGUMENT, "descriptor %u: y overlaps descriptor %u's add", i, j);
             }
         }
     }

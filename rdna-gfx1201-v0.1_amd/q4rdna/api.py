@@ -37,6 +37,14 @@ def _f32_vec(t: torch.Tensor, name: str) -> torch.Tensor:
     return t
 
 
+def _on_device(device: int, **tensors: torch.Tensor | None) -> None:
+    """The weight's device is where the kernels read and write: a buffer on
+    another device is refused here rather than passed by address."""
+    for name, t in tensors.items():
+        if t is not None and t.device.index != device:
+            raise ValueError(f"{name} lives on cuda:{t.device.index}, the weight on cuda:{device}")
+
+
 def _f32_buf(t: torch.Tensor, name: str, numel: int, device: int) -> torch.Tensor:
     """A device buffer the kernels read or write numel floats of: checked
     here, since the library sees only its address and a short or misplaced
@@ -95,6 +103,7 @@ def mul_mat(w: QWeight, x: torch.Tensor, y: torch.Tensor | None = None, stream: 
     if y is None:
         y = torch.empty(w.rows, dtype=torch.float32, device=x.device)
     _f32_vec(y, "y")
+    _on_device(w.device, x=x, y=y)
     s = _stream(x.device) if stream is None else stream
     ok = check(load().q4rdna_mul_mat(ctypes.byref(w.raw), x.data_ptr(), x.numel(), y.data_ptr(), y.numel(), s))
     return y if ok else None
@@ -108,6 +117,7 @@ def mul_mat_add(w: QWeight, x: torch.Tensor, add: torch.Tensor, y: torch.Tensor 
     if y is None:
         y = torch.empty(w.rows, dtype=torch.float32, device=x.device)
     _f32_vec(y, "y")
+    _on_device(w.device, x=x, add=add, y=y)
     s = _stream(x.device) if stream is None else stream
     ok = check(load().q4rdna_mul_mat_add(ctypes.byref(w.raw), x.data_ptr(), x.numel(), add.data_ptr(), add.numel(),
                                          y.data_ptr(), y.numel(), s))
@@ -121,6 +131,7 @@ def mul_mat_glu(up: QWeight, gate: QWeight, x: torch.Tensor, y: torch.Tensor | N
     if y is None:
         y = torch.empty(up.rows, dtype=torch.float32, device=x.device)
     _f32_vec(y, "y")
+    _on_device(up.device, x=x, y=y)
     s = _stream(x.device) if stream is None else stream
     ok = check(load().q4rdna_mul_mat_glu(ctypes.byref(up.raw), ctypes.byref(gate.raw), x.data_ptr(), x.numel(),
                                          glu_op, y.data_ptr(), y.numel(), s))

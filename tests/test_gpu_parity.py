@@ -299,7 +299,9 @@ def test_not_applicable_leaves_output_untouched(cuda):
 def test_overlapping_buffers_are_refused(cuda):
     """y overlapping x, and an add that overlaps y without being y, are
     argument errors that launch nothing (the kernels read x and add while
-    other workgroups write y); add may be y itself, the in-place residual."""
+    other workgroups write y); so are a group's outputs that overlap each
+    other or another descriptor's add.  add may be y itself, the in-place
+    residual, per tensor and in a group."""
     rows, cols = 256, 512
     t = random_tiles(rows, cols, 31)
     w = api.QWeight.from_tiles(dev_u8(t), rows, cols)
@@ -313,14 +315,27 @@ def test_overlapping_buffers_are_refused(cuda):
     xb = torch.zeros(2, cols, device="cuda")
     with pytest.raises(_lib.Q4RdnaError):          # n vectors: y inside x's second vector
         api.mul_mat_batch(w, xb, xb.view(-1)[cols:cols + 2 * rows].view(2, rows))
+    xg = dev_f32(O.gaussian_x(cols, 35))
+    y2 = torch.full((rows,), 7.0, device="cuda")
+    with pytest.raises(_lib.Q4RdnaError):          # group: a descriptor's add shifted against its own y
+        api.mul_mat_group([(w, add[:rows], None, add[8:])], xg)
+    with pytest.raises(_lib.Q4RdnaError):          # group: one descriptor's y is another's add
+        api.mul_mat_group([(w, y, None, None), (w, y2, None, y)], xg)
+    with pytest.raises(_lib.Q4RdnaError):          # group: two outputs overlap
+        api.mul_mat_group([(w, add[:rows]), (w, add[8:])], xg)
     torch.cuda.synchronize()
     assert (buf.cpu() == 7.0).all() and (y.cpu() == 7.0).all() and (xb.cpu() == 0.0).all()
+    assert (y2.cpu() == 7.0).all() and (add.cpu() == 1.0).all()
     x = O.gaussian_x(cols, 33)
     res = O.gaussian_x(rows, 34)
     y_in = dev_f32(res)                             # add is y: the residual in place
     assert api.mul_mat_add(w, dev_f32(x), y_in, y_in) is not None
     torch.cuda.synchronize()
     assert_gemv_parity(y_in.cpu().numpy(), t, rows, cols, x, add=res, label="in place")
+    g_in = dev_f32(res)                             # the same in a group
+    assert api.mul_mat_group([(w, g_in, None, g_in)], dev_f32(x))
+    torch.cuda.synchronize()
+    assert torch.equal(g_in, y_in)
 
 
 # ----------------------------------------------------------------- sidecar
