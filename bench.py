@@ -150,11 +150,14 @@ def bench_lib():
         lib = ctypes.CDLL(path)
         lib.q4bench_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
         lib.q4bench_empty.argtypes = [ctypes.c_uint32, ctypes.c_void_p]
+        lib.q4bench_stream_read_touch.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64,
+                                                  ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
         lib.q4bench_stream_runs.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                             ctypes.c_void_p, ctypes.c_void_p]
         lib.q4bench_rms_norm.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_float,
                                          ctypes.c_void_p]
-        for f in (lib.q4bench_stream_read, lib.q4bench_empty, lib.q4bench_rms_norm, lib.q4bench_stream_runs):
+        for f in (lib.q4bench_stream_read, lib.q4bench_empty, lib.q4bench_rms_norm, lib.q4bench_stream_runs,
+                  lib.q4bench_stream_read_touch):
             f.restype = ctypes.c_int
         _BENCH_LIB = lib
     return _BENCH_LIB
@@ -1001,7 +1004,13 @@ def floors(tensors, data, replays: int = 20):
                       plain read of its weight bytes, µs per launch
       layer_reads     the four stage reads of a layer one after another,
                       36 layers per graph: the floor of four dependent
-                      launches that each stream their weights once."""
+                      launches that each stream their weights once
+      layer_reads_touch  the same chain where each stage's launch also
+                      reads a fraction of the next stage's bytes with
+                      cache-allocating loads (by its own workgroups after
+                      their loads, or by workgroups appended to the launch),
+                      so that the next stage finds them in the Infinity
+                      Cache."""
     import torch
     lib = bench_lib()
     sink = torch.zeros(512, dtype=torch.int32, device="cuda")
@@ -1060,6 +1069,25 @@ def floors(tensors, data, replays: int = 20):
     out["stage_read"] = stage_out
     us = time_graph(lambda: [read(*span(l, f, la)) for l in range(layers) for _, f, la in stages], layers)
     out["layer_reads_us_per_layer"] = round(us, 2)
+    seq = [(l, f, la) for l in range(layers) for _, f, la in stages]
+
+    def touch_chain(inline, frac):
+        for i, (l, f, la) in enumerate(seq):
+            nl, nf, nla = seq[(i + 1) % len(seq)]
+            p, nb = span(l, f, la)
+            tp, tb = span(nl, nf, nla)
+            tb = max(4, int(tb * frac) // 4 * 4)
+            bench_call(lib.q4bench_stream_read_touch(p, nb, tp, tb, inline, sink.data_ptr(), st.cuda_stream),
+                       "stream read touch")
+
+    touch_rows = []
+    for inline in (0, 1):
+        for frac in (0.25, 0.5, 1.0):
+            t_us = time_graph(lambda i=inline, fr=frac: touch_chain(i, fr), layers)
+            touch_rows.append(dict(inline=bool(inline), fraction=frac, us_per_layer=round(t_us, 2)))
+            log(f"[floors] four stage reads touching {frac:.0%} of the next stage "
+                f"({'own workgroups' if inline else 'appended workgroups'}): {t_us:.2f} us per layer")
+    out["layer_reads_touch"] = touch_rows
     log(f"[floors] stack read {out['stack_read']['us']} us ({out['stack_read']['gb_per_s']} GB/s), "
         f"empty launch {out['empty_launch_us']} us, four dependent stage reads {us:.2f} us per layer")
     for name, v in stage_out.items():

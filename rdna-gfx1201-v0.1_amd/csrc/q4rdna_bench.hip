@@ -36,6 +36,53 @@ __global__ __launch_bounds__(kReadThreads) void stream_read_kernel(const uint32_
     if (flag != 0 && acc == flag) sink[threadIdx.x] = acc;
 }
 
+// stream_read_kernel's read of `words` words at p by workgroups
+// 0..own_blocks-1, plus a cache-allocating read of `twords` words at t (the
+// bytes the next launch reads), which leaves them in the Infinity Cache:
+//   * tloads > 0: each reading workgroup, after its own loads, reads its
+//     tloads * 512-word slice of t (slice b of workgroup b);
+//   * tloads == 0: workgroups own_blocks.. (dispatched after every reading
+//     workgroup) read t in 32 KB chunks, 16 loads per thread.
+// Indexes past either end are clamped, so every load is issued; the XOR of
+// the data reaches `sink` only when it equals `flag`, which the caller never
+// passes nonzero.
+__global__ __launch_bounds__(kReadThreads) void stream_read_touch_kernel(const uint32_t *__restrict__ p,
+                                                                         uint64_t words, uint32_t own_blocks,
+                                                                         const uint32_t *__restrict__ t,
+                                                                         uint64_t twords, uint32_t tloads,
+                                                                         uint32_t *sink, uint32_t flag) {
+    uint32_t acc = 0;
+    if (blockIdx.x < own_blocks) {
+        const uint64_t b = q4rdna::xcd_remap(blockIdx.x, own_blocks);
+        const uint64_t base = b * (kReadChunk / 4) + threadIdx.x;
+        uint32_t v[kReadLoads];
+#pragma unroll
+        for (int i = 0; i < kReadLoads; ++i) {
+            const uint64_t w = base + static_cast<uint64_t>(i) * kReadThreads;
+            v[i] = __builtin_nontemporal_load((q4rdna::gptr_u32)(p + (w < words ? w : words - 1)));
+        }
+        const uint64_t tbase = b * tloads * kReadThreads + threadIdx.x;
+#pragma unroll 4
+        for (uint32_t i = 0; i < tloads; ++i) {
+            const uint64_t w = tbase + static_cast<uint64_t>(i) * kReadThreads;
+            acc ^= t[w < twords ? w : twords - 1];
+        }
+#pragma unroll
+        for (int i = 0; i < kReadLoads; ++i) acc ^= v[i];
+    } else {
+        const uint64_t base = static_cast<uint64_t>(blockIdx.x - own_blocks) * (kReadChunk / 4) + threadIdx.x;
+        uint32_t v[kReadLoads];
+#pragma unroll
+        for (int i = 0; i < kReadLoads; ++i) {
+            const uint64_t w = base + static_cast<uint64_t>(i) * kReadThreads;
+            v[i] = t[w < twords ? w : twords - 1];
+        }
+#pragma unroll
+        for (int i = 0; i < kReadLoads; ++i) acc ^= v[i];
+    }
+    if (flag != 0 && acc == flag) sink[threadIdx.x] = acc;
+}
+
 // The sweeps' access pattern, as a plain read: `gridDim.x` persistent
 // workgroups of four waves, each wave with one step of eight 1 KB loads
 // (64 lanes x 16 bytes, nontemporal) in flight at a time.  Workgroup b reads
@@ -108,6 +155,29 @@ int q4bench_stream_read(const void *p, uint64_t bytes, uint32_t *sink, hipStream
     if (blocks > 0x7fffffffull) return static_cast<int>(hipErrorInvalidValue);
     hipLaunchKernelGGL(stream_read_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kReadThreads), 0, stream,
                        static_cast<const uint32_t *>(p), bytes / 4, sink, 0u);
+    return static_cast<int>(hipGetLastError());
+}
+
+// Reads `bytes` at p like q4bench_stream_read and `touch_bytes` at t with
+// cache-allocating loads (both multiples of 4, at least 4): by the reading
+// workgroups after their own loads when `inline_touch` is nonzero, else by
+// workgroups appended to the launch.
+int q4bench_stream_read_touch(const void *p, uint64_t bytes, const void *t, uint64_t touch_bytes, int inline_touch,
+                              uint32_t *sink, hipStream_t stream) {
+    if (p == nullptr || t == nullptr || sink == nullptr || bytes < 4 || bytes % 4 != 0 || touch_bytes < 4 ||
+        touch_bytes % 4 != 0)
+        return static_cast<int>(hipErrorInvalidValue);
+    const uint64_t blocks = (bytes + kReadChunk - 1) / kReadChunk;
+    const uint64_t touch_blocks = (touch_bytes + kReadChunk - 1) / kReadChunk;
+    uint64_t tloads = 0, grid = blocks + touch_blocks;
+    if (inline_touch != 0) {
+        tloads = (touch_bytes / 4 + blocks * kReadThreads - 1) / (blocks * kReadThreads);
+        grid = blocks;
+    }
+    if (grid > 0x7fffffffull || tloads > 4096) return static_cast<int>(hipErrorInvalidValue);
+    hipLaunchKernelGGL(stream_read_touch_kernel, dim3(static_cast<uint32_t>(grid)), dim3(kReadThreads), 0, stream,
+                       static_cast<const uint32_t *>(p), bytes / 4, static_cast<uint32_t>(blocks),
+                       static_cast<const uint32_t *>(t), touch_bytes / 4, static_cast<uint32_t>(tloads), sink, 0u);
     return static_cast<int>(hipGetLastError());
 }
 
