@@ -223,25 +223,20 @@ uint32_t q4rdna_policy_split_k(uint32_t rows, uint32_t columns, int device);
 
 /* q4rdna_mul_mat_ex that allocates nothing.  No counterpart in the
  * reference: it is for callers that cannot allocate (code under HIP graph
- * capture, tight serving loops, harnesses that forbid hipMalloc).  The split-K
- * workspace lives in a fixed per-GPU device array of
- * Q4RDNA_NOALLOC_PARTIAL_FLOATS partial sums, Q4RDNA_NOALLOC_COUNTERS arrival
- * counters and Q4RDNA_NOALLOC_SLOTS two-chunk exchange slots (8.06 MiB, held
- * by every GPU the library runs on until the process ends).  A launch that
- * would need more returns Q4RDNA_ERR_ARGUMENT and launches nothing: at
- * split_k 2, rows (doubled with a gate) above the slots; at larger splits,
- * split_k * rows (doubled with a gate) above the partial sums or rows / 32
- * above the counters.  Arguments, statuses and results are those of
- * q4rdna_mul_mat_ex (bit-identical at the same split).  Every call on a GPU
- * shares that GPU's array: calls that overlap on one GPU race, so issue them
- * on one stream or order them with events.  The first call on a GPU looks
- * the array's address up; its counters and slots are zero from the start
- * (a zero-initialised device variable, left zero by every launch), so no
- * set-up runs on any stream and the first call may be captured into a
- * graph. */
-#define Q4RDNA_NOALLOC_PARTIAL_FLOATS (1u << 20)
-#define Q4RDNA_NOALLOC_COUNTERS 16384u
-#define Q4RDNA_NOALLOC_SLOTS (1u << 20)
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The K
+ * chunks of a split launch meet in exchange slots, which here live in a
+ * fixed per-GPU device array of Q4RDNA_NOALLOC_SLOTS 32-bit slots (8 MiB,
+ * held by every GPU the library runs on until the process ends).  A launch
+ * at split_k s > 1 needs (p - 1) * rows slots, p the smallest power of two
+ * >= s, doubled with a gate; one that would need more returns
+ * Q4RDNA_ERR_ARGUMENT and launches nothing.  Arguments, statuses and results
+ * are those of q4rdna_mul_mat_ex (bit-identical at the same split).  Every
+ * call on a GPU shares that GPU's array: calls that overlap on one GPU race,
+ * so issue them on one stream or order them with events.  The first call on
+ * a GPU looks the array's address up; its slots are zero from the start (a
+ * zero-initialised device variable, left zero by every launch), so no set-up
+ * runs on any stream and the first call may be captured into a graph. */
+#define Q4RDNA_NOALLOC_SLOTS (1u << 21)
 int q4rdna_mul_mat_ex_noalloc(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x,
                               const float *add, float *y, const q4rdna_launch_options *options,
                               void *stream);

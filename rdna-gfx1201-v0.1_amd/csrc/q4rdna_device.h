@@ -144,6 +144,35 @@ __device__ __forceinline__ bool exchange_pair(uint32_t *slots, uint32_t row, flo
     return true;
 }
 
+// Chunk s of `split` K chunks (split >= 2) meets the others in a fixed binary
+// tree of exchange slots.  With P the smallest power of two >= split, chunk s
+// is leaf P + s of a heap and internal node k (1 <= k < P) owns slot region
+// k - 1: `rows` slots, two words per row with a gate.  Going up, each node
+// whose other subtree holds a chunk takes one exchange_pair; a node whose
+// right subtree lies past the last chunk is passed straight through.  The
+// first arrival at a node stops there, the second carries both subtrees' sum
+// up, and the thread that clears the root holds the row's whole sum (returns
+// true).  A node's two inputs are fixed sums and fp32 addition is
+// commutative, so the root sum -- ((p0 + p1) + (p2 + p3)) + (p4 + p5) at
+// split 6 -- is the same whichever chunk arrives first; at split 2 the tree
+// is the single exchange.  Every slot a launch uses is swapped into exactly
+// twice, so all are zero again when it ends.
+template <bool GATE>
+__device__ __forceinline__ bool exchange_tree(uint32_t *slots, uint32_t rows, uint32_t split, uint32_t s,
+                                              uint32_t row, float &v, float &gv) {
+    const uint32_t P = 1u << (32 - __builtin_clz(split - 1u));
+    uint32_t node = P + s;
+    for (uint32_t d = 0; node > 1u; ++d, node >>= 1) {
+        // A left child (even node) meets only if its right sibling's first
+        // leaf, (node + 1) << d, is a chunk.
+        if ((node & 1u) != 0u || ((node + 1u) << d) - P < split) {
+            uint32_t *region = slots + static_cast<size_t>((node >> 1) - 1u) * rows * (GATE ? 2u : 1u);
+            if (!exchange_pair<GATE>(region, row, v, gv)) return false;
+        }
+    }
+    return true;
+}
+
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 // A lane's tile slice: dword j of the 1,024 code bytes at 32 * (a + 8j) +

@@ -60,6 +60,16 @@ bool valid_shape(uint32_t rows, uint32_t cols);
 
 constexpr uint32_t kMaxSplit = 64;
 
+// Exchange-slot regions of a launch whose K chunks meet in a binary tree
+// (the per-tensor and group kernels): one per internal node of a heap over
+// the smallest power of two >= split, so split - 1 of them take part; none
+// without a split.
+constexpr uint32_t exchange_nodes(uint32_t split) {
+    uint32_t p = 1;
+    while (p < split) p <<= 1;
+    return p - 1;
+}
+
 // Split-K factor of a per-tensor launch of rows x cols on a GPU with `cus`
 // compute units.
 uint32_t policy_split(uint32_t rows, uint32_t cols, uint32_t cus);

@@ -21,11 +21,9 @@ constexpr uint32_t kSlotKey = 0x7fa5a5a5u;
 constexpr uint32_t kSlotQuietNan = 0x7fc00000u;
 
 // One GEMV launch.  gate != nullptr selects SwiGLU, add != nullptr the bias
-// epilogue.  split == 2 (gemv_kernel) reduces the two K chunks through
-// slots[rows (x2 with gate)], zero on entry and left zero.  Other splits
-// > 1 reduce K chunks across workgroups through partial[split * rows (x2
-// with gate)] and counters[rows / 32], which must be zero on entry and are
-// left zero.
+// epilogue.  split > 1 K chunks meet in an exchange tree over
+// slots[exchange_nodes(split) * vectors * rows (x2 with gate)] (vectors is 1
+// outside gemv_multi_kernel), zero on entry and left zero.
 struct GemvArgs {
     const uint8_t *w;
     const uint8_t *gate;
@@ -35,8 +33,6 @@ struct GemvArgs {
     uint32_t rows;
     uint32_t cols;
     uint32_t split;
-    float *partial;
-    uint32_t *counters;
     uint32_t *slots;
     uint32_t short_waves;  // waves per workgroup: 8 or 4 for K chunks of at most 64 groups,
                            // 16 for chunks of 65..128 groups (gemv_waves)
@@ -156,17 +152,15 @@ constexpr uint32_t kMaxGroup = 8;  // GEMVs of one group launch (Q4RDNA_MAX_GROU
 // sharing x of `cols` floats, the row tiles of all of them numbered GEMV by
 // GEMV from tile_begin (`tiles` in all), each split into `split` K chunks of
 // at most kGroupChunkGroups groups.  The chunks of a row tile meet as in
-// gemv_kernel: split 2 in slots[rows (x2 with gate)], larger splits in
-// partial[split * rows (x2)] through counters[rows / 32].  gate is given for
-// every GEMV or for none; add may be null per GEMV.
+// gemv_kernel: in an exchange tree over slots[exchange_nodes(split) * rows
+// (x2 with gate)] per GEMV.  gate is given for every GEMV or for none; add
+// may be null per GEMV.
 constexpr uint32_t kGroupChunkGroups = 64;
 struct GemvGroupEntry {
     const uint8_t *w;
     const uint8_t *gate;
     const float *add;
     float *y;
-    float *partial;
-    uint32_t *counters;
     uint32_t *slots;
     uint32_t rows;
     uint32_t tile_begin;

@@ -38,9 +38,9 @@
 //
 // Reduction.  Lane partials are summed over a with xor-8/16/32 cross-lane
 // adds (a DPP row rotate and two permlane swaps), the waves' results in LDS
-// in wave order, and K chunks split across
-// workgroups through a partial buffer summed in chunk order by the last
-// workgroup to arrive, so every result is bit-reproducible run to run.
+// in wave order, and K chunks split across workgroups meet in a fixed binary
+// tree of atomic exchange slots (exchange_tree), so every result is
+// bit-reproducible run to run.
 #include <type_traits>
 
 #include "q4rdna_device.h"
@@ -103,7 +103,6 @@ template <int SG, int WR>
 struct SharedT {
     XStageT<SG> st;
     float red[2][WR][32];
-    uint32_t last;
 };
 using Shared = SharedT<kStageGroups, kShortWaves>;
 // The workgroup's shared memory for W waves.
@@ -307,45 +306,17 @@ __device__ __forceinline__ float epilogue(float v, float gv, const float *__rest
 }
 
 // Where a row tile's chunk sums go (threads 0..31 hold row rt*32 + t's sum
-// v and SwiGLU gate sum gv of chunk s): split 1 writes y; split 2 meets the
-// other chunk in the row's exchange slot and the second to arrive writes y;
-// larger splits publish the chunk's partials with device-scope stores, wait
-// for them to complete, then count arrivals, and the last workgroup of the
-// row tile sums the chunks in chunk order and resets the counter.  `add` may
-// be null (ADD false makes it so at compile time).
-template <bool GATE, bool ADD, class Sh>
-__device__ __forceinline__ void finish_rows(Sh &sh, float *__restrict__ y, const float *__restrict__ add,
-                                            float *__restrict__ partial, uint32_t *__restrict__ counters,
+// v and SwiGLU gate sum gv of chunk s): split 1 writes y; larger splits meet
+// the row's other chunks in its exchange tree (exchange_tree), and the thread
+// that clears the root applies the epilogue and writes y.  `add` may be null
+// (ADD false makes it so at compile time).
+template <bool GATE, bool ADD>
+__device__ __forceinline__ void finish_rows(float *__restrict__ y, const float *__restrict__ add,
                                             uint32_t *__restrict__ slots, uint32_t rows, uint32_t split, uint32_t s,
                                             uint32_t rt, float v, float gv) {
     const uint32_t row = rt * kTileRows + (threadIdx.x & 31);
-    if (split == 1) {
-        if (threadIdx.x < 32) y[row] = epilogue<GATE, ADD>(v, gv, add, row);
-        return;
-    }
-    if (split == 2) {
-        if (threadIdx.x < 32 && exchange_pair<GATE>(slots, row, v, gv)) y[row] = epilogue<GATE, ADD>(v, gv, add, row);
-        return;
-    }
-    if (threadIdx.x < 32) {
-        store_agent(&partial[static_cast<size_t>(s) * rows + row], v);
-        if constexpr (GATE) store_agent(&partial[static_cast<size_t>(split + s) * rows + row], gv);
-    }
-    wait_stores();
-    __syncthreads();
-    if (threadIdx.x == 0) sh.last = (add_agent(&counters[rt], 1u) == split - 1) ? 1u : 0u;
-    __syncthreads();
-    if (sh.last == 0u) return;
-    if (threadIdx.x < 32) {
-        float sum = load_agent(&partial[row]);
-        float gsum = GATE ? load_agent(&partial[static_cast<size_t>(split) * rows + row]) : 0.f;
-        for (uint32_t c = 1; c < split; ++c) {
-            sum += load_agent(&partial[static_cast<size_t>(c) * rows + row]);
-            if constexpr (GATE) gsum += load_agent(&partial[static_cast<size_t>(split + c) * rows + row]);
-        }
-        y[row] = epilogue<GATE, ADD>(sum, gsum, add, row);
-    }
-    if (threadIdx.x == 0) store_agent(&counters[rt], 0u);
+    if (threadIdx.x >= 32) return;
+    if (split == 1 || exchange_tree<GATE>(slots, rows, split, s, row, v, gv)) y[row] = epilogue<GATE, ADD>(v, gv, add, row);
 }
 
 // Workgroup b covers row tile rt and K chunk s of `split`, remapped so the
@@ -364,8 +335,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs args) {
         tile_row_partial<GATE>(sh, args.w, args.gate, args.x, args.cols, rt, g_begin, g_end, v, gv);
     else
         tile_row_partial_short<GATE, T, W>(sh, args.w, args.gate, args.x, args.cols, rt, g_begin, g_end, v, gv);
-    finish_rows<GATE, ADD>(sh, args.y, args.add, args.partial, args.counters, args.slots, args.rows, split, s, rt, v,
-                           gv);
+    finish_rows<GATE, ADD>(args.y, args.add, args.slots, args.rows, split, s, rt, v, gv);
 }
 
 // Several GEMVs sharing x (q4rdna_mul_mat_group): the row tiles of all of
@@ -391,9 +361,9 @@ __global__ __launch_bounds__(64 * W) void gemv_group_kernel(GemvGroupArgs a) {
     float v = 0.f, gv = 0.f;
     tile_row_partial_short<GATE, T, W>(sh, G.w, G.gate, a.x, a.cols, rt, g_begin, g_end, v, gv);
     if (G.add != nullptr)
-        finish_rows<GATE, true>(sh, G.y, G.add, G.partial, G.counters, G.slots, G.rows, split, s, rt, v, gv);
+        finish_rows<GATE, true>(G.y, G.add, G.slots, G.rows, split, s, rt, v, gv);
     else
-        finish_rows<GATE, false>(sh, G.y, nullptr, G.partial, G.counters, G.slots, G.rows, split, s, rt, v, gv);
+        finish_rows<GATE, false>(G.y, nullptr, G.slots, G.rows, split, s, rt, v, gv);
 }
 
 // ---- several activation vectors against one weight (n = 2..8) -------------
@@ -416,7 +386,6 @@ struct MvShared {
     float4 v[NV][mv_stage_groups<NV>()][16];  // [vector][g][a] even-k x, [..][8 + a] odd-k x / 16
     float c[NV][mv_stage_groups<NV>()][8];    // -8 * sum of the lane's 8 x values
     float red[2][NV][kMvWaves][32];
-    uint32_t last;
 };
 
 template <bool GATE, bool ADD, int NV, int T>
@@ -541,31 +510,11 @@ __global__ __launch_bounds__(64 * kMvWaves) void gemv_multi_kernel(GemvArgs args
             for (int wv = 1; wv < W; ++wv) gout += sh.red[1][v][wv][rl];
         }
     }
-    if (split == 1) {
-        if (mine) args.y[v * M + row] = epilogue<GATE, ADD>(out, gout, args.add ? args.add + v * M : nullptr, row);
-        return;
-    }
-    // Split K as in gemv_kernel; partials [chunk][vector][rows], gate
-    // partials after the split * n value partials.
-    if (mine) {
-        store_agent(&args.partial[(static_cast<size_t>(s) * nv + v) * M + row], out);
-        if constexpr (GATE) store_agent(&args.partial[(static_cast<size_t>(split + s) * nv + v) * M + row], gout);
-    }
-    wait_stores();
-    __syncthreads();
-    if (threadIdx.x == 0) sh.last = (add_agent(&args.counters[rt], 1u) == split - 1) ? 1u : 0u;
-    __syncthreads();
-    if (sh.last == 0u) return;
-    if (mine) {
-        float sum = load_agent(&args.partial[static_cast<size_t>(v) * M + row]);
-        float gsum = GATE ? load_agent(&args.partial[(static_cast<size_t>(split) * nv + v) * M + row]) : 0.f;
-        for (uint32_t c = 1; c < split; ++c) {
-            sum += load_agent(&args.partial[(static_cast<size_t>(c) * nv + v) * M + row]);
-            if constexpr (GATE) gsum += load_agent(&args.partial[(static_cast<size_t>(split + c) * nv + v) * M + row]);
-        }
-        args.y[v * M + row] = epilogue<GATE, ADD>(sum, gsum, args.add ? args.add + v * M : nullptr, row);
-    }
-    if (threadIdx.x == 0) store_agent(&args.counters[rt], 0u);
+    // Split K as in gemv_kernel: an exchange tree per (vector, row), each
+    // node's region holding [vector][rows] slots.
+    if (mine && (split == 1 || exchange_tree<GATE>(args.slots, nv * static_cast<uint32_t>(M), split, s,
+                                                   v * static_cast<uint32_t>(M) + row, out, gout)))
+        args.y[v * M + row] = epilogue<GATE, ADD>(out, gout, args.add ? args.add + v * M : nullptr, row);
 }
 
 // The reference's old mapping (source/q4rdna.cu:190-234, selected there by

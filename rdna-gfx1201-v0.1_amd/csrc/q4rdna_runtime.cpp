@@ -110,15 +110,10 @@ int parse_index(const uint8_t *image, uint64_t image_size, uint64_t file_size, F
     return host_status(q4rdna::host::parse_index(image, image_size, file_size, header, entries, &error), error);
 }
 
-// Split-K scratch per (device, stream): partial sums, per-row-tile arrival
-// counters (kept zero between launches by the kernels) and two-chunk
-// exchange slots (kept zero between launches by the kernel).
+// Split-K exchange slots per (device, stream), kept zero between launches by
+// the kernels.
 struct Workspace {
-    float *partial = nullptr;
-    uint32_t *counters = nullptr;
     uint32_t *slots = nullptr;
-    size_t partial_floats = 0;
-    size_t counter_count = 0;
     size_t slot_count = 0;
 };
 
@@ -129,48 +124,27 @@ std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 // doubles when it grows, so few are ever retired.
 std::vector<Workspace> g_ws_retired;
 
-int get_workspace(int device, hipStream_t stream, size_t partial_floats, size_t counters, size_t slots,
-                  Workspace **out) {
+int get_workspace(int device, hipStream_t stream, size_t slots, Workspace **out) {
     std::lock_guard<std::mutex> lock(g_ws_mu);
     Workspace &ws = g_ws[{device, stream}];
-    if (ws.partial_floats < partial_floats || ws.counter_count < counters || ws.slot_count < slots) {
-        // Each region at least doubles when the workspace grows (and never
-        // shrinks), so few workspaces are ever retired.
-        const size_t pf = std::max(partial_floats, ws.partial_floats < partial_floats ? 2 * ws.partial_floats : ws.partial_floats);
-        const size_t cc = std::max(counters, ws.counter_count < counters ? 2 * ws.counter_count : ws.counter_count);
-        const size_t sc = std::max(slots, ws.slot_count < slots ? 2 * ws.slot_count : ws.slot_count);
-        if (ws.partial != nullptr || ws.counters != nullptr || ws.slots != nullptr) {
+    if (ws.slot_count < slots) {
+        const size_t sc = std::max(slots, 2 * ws.slot_count);
+        if (ws.slots != nullptr) {
             g_ws_retired.push_back(ws);
             ws = Workspace{};
         }
-        float *p = nullptr;
-        uint32_t *c = nullptr, *sl = nullptr;
-        hipError_t e = hipSuccess;
-        if (pf > 0) e = hipMalloc(&p, pf * sizeof(float));
-        if (e == hipSuccess && cc > 0) e = hipMalloc(&c, cc * sizeof(uint32_t));
-        if (e == hipSuccess && sc > 0) e = hipMalloc(&sl, sc * sizeof(uint32_t));
-        if (e != hipSuccess) {
-            (void)hipFree(p);
-            (void)hipFree(c);
-            (void)hipFree(sl);
-            return set_error(Q4RDNA_ERR_MEMORY, "split-K workspace: %s", hipGetErrorString(e));
-        }
+        uint32_t *sl = nullptr;
+        hipError_t e = hipMalloc(&sl, sc * sizeof(uint32_t));
+        if (e != hipSuccess) return set_error(Q4RDNA_ERR_MEMORY, "split-K workspace: %s", hipGetErrorString(e));
         // Set once, complete before any launch uses them (launches on
         // non-blocking streams are not ordered after the null stream).
-        if (cc > 0) e = hipMemset(c, 0, cc * sizeof(uint32_t));
-        if (e == hipSuccess && sc > 0) e = hipMemset(sl, 0, sc * sizeof(uint32_t));
+        e = hipMemset(sl, 0, sc * sizeof(uint32_t));
         if (e == hipSuccess) e = hipDeviceSynchronize();
         if (e != hipSuccess) {
-            (void)hipFree(p);
-            (void)hipFree(c);
             (void)hipFree(sl);
             return hip_fail(e, "hipMemset");
         }
-        ws.partial = p;
-        ws.counters = c;
         ws.slots = sl;
-        ws.partial_floats = pf;
-        ws.counter_count = cc;
         ws.slot_count = sc;
     }
     *out = &ws;
@@ -193,17 +167,14 @@ uint32_t resolve_split(const q4rdna_weight *w, uint32_t split) {
 // Per-tensor launch with the stream's split-K workspace.
 int launch_one(const q4rdna::TensorLaunch &launch, const q4rdna_weight *w, const uint8_t *gate, const float *x,
                const float *add, float *y, hipStream_t stream) {
-    float *partial = nullptr;
-    uint32_t *counters = nullptr, *slots = nullptr;
-    if (launch.partial_floats > 0 || launch.counters > 0 || launch.slots > 0) {
+    uint32_t *slots = nullptr;
+    if (launch.slots > 0) {
         Workspace *ws = nullptr;
-        int rc = get_workspace(w->device, stream, launch.partial_floats, launch.counters, launch.slots, &ws);
+        int rc = get_workspace(w->device, stream, launch.slots, &ws);
         if (rc != Q4RDNA_OK) return rc;
-        partial = ws->partial;
-        counters = ws->counters;
         slots = ws->slots;
     }
-    return q4rdna::launch_tensor_in(launch, w, gate, x, add, y, partial, counters, slots, stream);
+    return q4rdna::launch_tensor_in(launch, w, gate, x, add, y, slots, stream);
 }
 
 // Preconditions shared by the GEMV entry points.  NOT_APPLICABLE mirrors the
@@ -280,19 +251,13 @@ int check_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const fl
     if (!gemv_shape_fits(w->rows / kTileRows, w->columns / kGroup, L.split))
         return set_error(Q4RDNA_ERR_ARGUMENT, "shape %ux%u at split %u is beyond the kernels' index range", w->rows,
                          w->columns, L.split);
-    if (L.split == 2) {
-        L.slots = static_cast<size_t>(w->rows) * (gate ? 2 : 1);
-    } else if (L.split > 2) {
-        L.partial_floats = static_cast<size_t>(L.split) * w->rows * (gate ? 2 : 1);
-        L.counters = w->rows / kTileRows;
-    }
+    L.slots = static_cast<size_t>(host::exchange_nodes(L.split)) * w->rows * (gate ? 2 : 1);
     *launch = L;
     return Q4RDNA_OK;
 }
 
 int launch_tensor_in(const TensorLaunch &launch, const q4rdna_weight *w, const uint8_t *gate, const float *x,
-                     const float *add, float *y, float *partial, uint32_t *counters, uint32_t *slots,
-                     hipStream_t stream) {
+                     const float *add, float *y, uint32_t *slots, hipStream_t stream) {
     GemvArgs args{};
     args.w = w->tiles;
     args.gate = gate;
@@ -306,12 +271,7 @@ int launch_tensor_in(const TensorLaunch &launch, const q4rdna_weight *w, const u
     const uint64_t workgroups = static_cast<uint64_t>(w->rows / kTileRows) * launch.split;
     args.short_waves =
         gemv_waves(w->columns / kGroup, launch.split, workgroups, static_cast<uint32_t>(cu_count(w->device)));
-    if (launch.split == 2) {
-        args.slots = slots;
-    } else if (launch.split > 2) {
-        args.partial = partial;
-        args.counters = counters;
-    }
+    args.slots = slots;
     const hipError_t e = launch.sequential ? launch_gemv_sequential(args, stream) : launch_gemv(args, stream);
     if (e != hipSuccess) return hip_fail(e, "GEMV launch");
     return Q4RDNA_OK;
@@ -685,19 +645,14 @@ int launch_group_valu(const q4rdna_group_desc *descs, uint32_t count, const floa
     if (workgroups > 0x7fffffffull || !q4rdna::gemv_shape_fits(tiles, groups, split))
         return set_error(Q4RDNA_ERR_ARGUMENT, "group too large");
     const uint32_t streams = glu ? 2u : 1u;
-    size_t partial_floats = 0, counters = 0, slots = 0;
+    size_t slots = 0;
     for (uint32_t i = 0; i < count; ++i) {
         const uint32_t rows = descs[i].weight.rows;
-        if (split == 2) {
-            slots += static_cast<size_t>(streams) * rows;
-        } else if (split > 2) {
-            partial_floats += static_cast<size_t>(split) * streams * rows;
-            counters += rows / kTileRows;
-        }
+        slots += static_cast<size_t>(q4rdna::host::exchange_nodes(split)) * streams * rows;
     }
     Workspace *ws = nullptr;
     int rc;
-    if (split > 1 && (rc = get_workspace(device, stream, partial_floats, counters, slots, &ws)) != Q4RDNA_OK) return rc;
+    if (split > 1 && (rc = get_workspace(device, stream, slots, &ws)) != Q4RDNA_OK) return rc;
     q4rdna::GemvGroupArgs args{};
     args.x = x;
     args.count = count;
@@ -707,21 +662,14 @@ int launch_group_valu(const q4rdna_group_desc *descs, uint32_t count, const floa
     args.tiles = tiles;
     args.short_waves = workgroups <= 4ull * cu_count(device) ? 8u : 4u;
     uint32_t tile_begin = 0;
-    size_t poff = 0, coff = 0, soff = 0;
+    size_t soff = 0;
     for (uint32_t i = 0; i < count; ++i) {
         const q4rdna_group_desc &d = descs[i];
         const uint32_t rows = d.weight.rows;
         args.g[i] = q4rdna::GemvGroupEntry{d.weight.tiles, d.gate_tiles, d.add, d.y,
-                                           split > 2 ? ws->partial + poff : nullptr,
-                                           split > 2 ? ws->counters + coff : nullptr,
-                                           split == 2 ? ws->slots + soff : nullptr, rows, tile_begin};
+                                           split > 1 ? ws->slots + soff : nullptr, rows, tile_begin};
         tile_begin += rows / kTileRows;
-        if (split == 2) {
-            soff += static_cast<size_t>(streams) * rows;
-        } else if (split > 2) {
-            poff += static_cast<size_t>(split) * streams * rows;
-            coff += rows / kTileRows;
-        }
+        soff += static_cast<size_t>(q4rdna::host::exchange_nodes(split)) * streams * rows;
     }
     hipError_t e = q4rdna::launch_gemv_group(args, stream);
     if (e != hipSuccess) return hip_fail(e, "group GEMV launch");
@@ -842,10 +790,9 @@ int q4rdna_mul_mat_batch(const q4rdna_weight *w, const q4rdna_weight *gate, cons
     args.vectors = n;
     if (split > 1) {
         Workspace *ws = nullptr;
-        const size_t pf = static_cast<size_t>(split) * n * w->rows * (gate ? 2 : 1);
-        if ((rc = get_workspace(w->device, s, pf, w->rows / kTileRows, 0, &ws)) != Q4RDNA_OK) return rc;
-        args.partial = ws->partial;
-        args.counters = ws->counters;
+        const size_t sc = static_cast<size_t>(q4rdna::host::exchange_nodes(split)) * n * w->rows * (gate ? 2 : 1);
+        if ((rc = get_workspace(w->device, s, sc, &ws)) != Q4RDNA_OK) return rc;
+        args.slots = ws->slots;
     }
     hipError_t e = q4rdna::launch_gemv_multi(args, s);
     if (e != hipSuccess) return hip_fail(e, "batched GEMV launch");

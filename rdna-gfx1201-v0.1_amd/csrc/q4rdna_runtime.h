@@ -14,13 +14,10 @@ namespace q4rdna {
 int set_error(int code, const char *fmt, ...);
 
 // How a per-tensor GEMV launches: the VALU kernel's split-K factor and the
-// workspace it needs: exchange slots (words, zero between launches) at split
-// 2, else fp32 partials and arrival counters; none when the K dimension is
-// not split.
+// exchange slots (words, zero between launches) its K chunks meet in; none
+// when the K dimension is not split.
 struct TensorLaunch {
     uint32_t split;
-    size_t partial_floats;
-    size_t counters;
     size_t slots;
     bool sequential;  // Q4RDNA_KERNEL_SEQUENTIAL: split 1, no workspace
 };
@@ -30,17 +27,15 @@ struct TensorLaunch {
 int check_mul_mat_ex(const q4rdna_weight *w, const q4rdna_weight *gate, const float *x, const float *add,
                      const float *y, const q4rdna_launch_options *options, TensorLaunch *launch);
 
-// Launch a validated per-tensor GEMV with a caller-provided workspace of at
-// least launch.partial_floats floats, launch.counters counters and
-// launch.slots slot words (each ignored when its count is zero); counters
-// and slots zero on entry, both left zero.
+// Launch a validated per-tensor GEMV with caller-provided exchange slots: at
+// least launch.slots words (ignored when that is zero), zero on entry and
+// left zero.
 // Count one GEMV launch over W (and its SwiGLU gate, may be null) in the
 // library's launch statistics (q4rdna_launch_count, q4rdna_sidecar_hits).
 // Allocates nothing.
 void count_gemv_launch(const uint8_t *w, const uint8_t *gate);
 
 int launch_tensor_in(const TensorLaunch &launch, const q4rdna_weight *w, const uint8_t *gate, const float *x,
-                     const float *add, float *y, float *partial, uint32_t *counters, uint32_t *slots,
-                     hipStream_t stream);
+                     const float *add, float *y, uint32_t *slots, hipStream_t stream);
 
 }  // namespace q4rdna

@@ -31,9 +31,7 @@ ALGO_MSE = 3
 
 GLU_SWIGLU = 0
 MAX_BATCH = 8
-NOALLOC_PARTIAL_FLOATS = 1 << 20
-NOALLOC_COUNTERS = 16384
-NOALLOC_SLOTS = 1 << 20
+NOALLOC_SLOTS = 1 << 21
 
 # Every symbol include/q4rdna.h declares.
 EXPORTS = (

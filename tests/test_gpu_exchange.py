@@ -1,11 +1,12 @@
-"""Two-chunk split-K in the per-tensor VALU kernel: at split 2 the two K
-chunks of a row meet in an exchange slot that every launch must leave empty
-(all-zero memory; a partial is stored XOR a signaling-NaN key).
+"""Split-K in the per-tensor VALU kernel: the K chunks of a row meet in a
+binary tree of exchange slots (one slot at split 2) that every launch must
+leave empty (all-zero memory; a partial is stored XOR a signaling-NaN key).
 Launches of both slot layouts (one word per row; a (sum, SwiGLU gate sum)
 pair per row) alternate on one stream over the same slots: every result is
-bit-identical from round to round and within both parity bars.  NaN partials,
-including the slots' own signaling-NaN key fed in as an activation, still
-finish every row, and the launches after them are unaffected."""
+bit-identical from round to round and within both parity bars, at split 2
+and at every tree shape up to 64 chunks.  NaN partials, including the slots'
+own signaling-NaN key fed in as an activation, still finish every row, and
+the launches after them are unaffected."""
 import numpy as np
 import pytest
 import torch
@@ -163,3 +164,64 @@ def test_group_of_eight_mixed_rows(cuda):
     torch.cuda.synchronize()
     for (t, w, a, rows), y in zip(members, ys):
         assert_gemv_parity(y.cpu().numpy(), t, rows, cols, x_np, add=a, label=rows)
+
+
+TREE_SPLITS = [3, 4, 5, 6, 7, 8, 9, 12, 16, 17, 31, 33, 64]
+
+
+@pytest.mark.parametrize("split", TREE_SPLITS)
+def test_exchange_tree_every_shape(cuda, split):
+    """Splits above 2 meet in the exchange tree (leaves passed through where
+    a subtree holds no chunk).  Plain and SwiGLU + bias launches alternate on
+    one stream for three rounds: each round equals the first bit for bit (so
+    every slot was left empty), and the first is within both bars."""
+    rows, cols = 96, 4096
+    cases = []
+    for i, kind in enumerate(("plain", "glu+add")):
+        t, w = weight(rows, cols, 700 + 10 * split + i)
+        gt, g = weight(rows, cols, 701 + 10 * split + i) if "glu" in kind else (None, None)
+        add_np = O.gaussian_x(rows, 702 + 10 * split + i) if "add" in kind else None
+        x_np = O.gaussian_x(cols, 703 + 10 * split + i)
+        cases.append((kind, t, w, gt, g, add_np, None if add_np is None else torch.from_numpy(add_np).cuda(),
+                      x_np, torch.from_numpy(x_np).cuda()))
+    st = torch.cuda.Stream()
+    first = None
+    for rnd in range(3):
+        outs = []
+        with torch.cuda.stream(st):
+            for kind, t, w, gt, g, add_np, add, x_np, x in cases:
+                y = torch.full((rows,), 7.0, device="cuda")
+                assert api.mul_mat_ex(w, x, y, gate=g, add=add, split_k=split, stream=st.cuda_stream)
+                outs.append(y)
+        st.synchronize()
+        if first is None:
+            first = outs
+            for (kind, t, w, gt, g, add_np, add, x_np, x), y in zip(cases, outs):
+                assert_gemv_parity(y.cpu().numpy(), t, rows, cols, x_np, gate_tiles=gt, add=add_np,
+                                   label=(split, kind))
+        else:
+            for a, b in zip(first, outs):
+                assert torch.equal(a, b), (split, rnd)
+
+
+@pytest.mark.parametrize("gated", [False, True])
+@pytest.mark.parametrize("chunk", [0, 3, 5])
+def test_exchange_tree_nan_partials_finish_every_row(cuda, gated, chunk):
+    """At split 6 (leaves 0..3 three exchanges deep, 4 and 5 two), the slot
+    key's bits as an activation in chunk `chunk`: every row is still written
+    (NaN), and a clean launch right after on the same stream is exact."""
+    rows, cols, split = 4096, 12288, 6
+    t, w = weight(rows, cols, 800)
+    gt, g = weight(rows, cols, 801) if gated else (None, None)
+    x_np = O.gaussian_x(cols, 802)
+    bad = x_np.copy()
+    bad.view(np.uint32)[chunk * (cols // split) + 9] = SLOT_KEY
+    st = torch.cuda.Stream()
+    y_bad = torch.full((rows,), 7.0, device="cuda")
+    y = torch.full((rows,), 7.0, device="cuda")
+    with torch.cuda.stream(st):
+        assert api.mul_mat_ex(w, torch.from_numpy(bad).cuda(), y_bad, gate=g, split_k=split, stream=st.cuda_stream)
+        assert api.mul_mat_ex(w, torch.from_numpy(x_np).cuda(), y, gate=g, split_k=split, stream=st.cuda_stream)
+    st.synchronize()
+    assert torch.isnan(y_bad).all()
+    assert_gemv_parity(y.cpu().numpy(), t, rows, cols, x_np, gate_tiles=gt, label=("after NaN", split, gated, chunk))

@@ -242,7 +242,7 @@ def test_mul_mat_batch_matches_oracle(cuda, n):
                                add=None if add_np is None else add_np[v], label=(rows, cols, kind, n, v))
 
 
-@pytest.mark.parametrize("n,split", [(2, 2), (4, 2), (8, 4), (3, 4)])
+@pytest.mark.parametrize("n,split", [(2, 2), (4, 2), (8, 4), (3, 4), (3, 6), (5, 7)])
 def test_mul_mat_batch_equals_single_vector_launches(cuda, n, split):
     """Each vector of a batched launch equals q4rdna_mul_mat_ex of that vector
     with the same split, bit for bit (same staging, fma order and summation

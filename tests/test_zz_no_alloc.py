@@ -70,15 +70,16 @@ def test_noalloc_equals_mul_mat_ex(cuda):
 
 
 def test_noalloc_refuses_what_does_not_fit(cuda):
-    """151936 x 4096 at split 8 needs 1,215,488 partial floats, more than the
-    1,048,576 the array holds: refused, nothing launched.  Likewise a split-2
-    launch with more rows than exchange slots."""
+    """151936 x 4096 at split 16 meets in a tree of 15 slot regions:
+    2,279,040 slots, more than the 2,097,152 the array holds: refused,
+    nothing launched.  Likewise a split-2 launch with more rows than slots."""
     L = q4rdna.load()
     rows, cols = 151936, 4096
+    assert 15 * rows > _lib.NOALLOC_SLOTS
     w = api.QWeight.from_tiles(torch.zeros(api.packed_size(rows, cols), dtype=torch.uint8, device="cuda"), rows, cols)
     x = torch.zeros(cols, device="cuda")
     y = torch.full((rows,), 7.0, device="cuda")
-    rc = call(L.q4rdna_mul_mat_ex_noalloc, w, None, x, None, y, 8, torch.cuda.current_stream().cuda_stream)
+    rc = call(L.q4rdna_mul_mat_ex_noalloc, w, None, x, None, y, 16, torch.cuda.current_stream().cuda_stream)
     assert rc == q4rdna.ERR_ARGUMENT
     assert "no-alloc scratch" in q4rdna.last_error()
     torch.cuda.synchronize()
@@ -89,9 +90,9 @@ def test_noalloc_refuses_what_does_not_fit(cuda):
     torch.cuda.synchronize()
     assert (y == 0.0).all()
     del w, y
-    # split 2 exchanges through one slot per row: 1,048,608 rows need more
-    # than the 1,048,576 slots
-    rows, cols = 1048608, 128
+    # split 2 exchanges through one slot per row: 2,097,184 rows need more
+    # than the 2,097,152 slots
+    rows, cols = 2097184, 128
     assert rows > _lib.NOALLOC_SLOTS
     w = api.QWeight.from_tiles(torch.zeros(api.packed_size(rows, cols), dtype=torch.uint8, device="cuda"), rows, cols)
     x = torch.zeros(cols, device="cuda")
