@@ -111,8 +111,8 @@ __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)
 // with one device-scope atomic.  The first to arrive reads zero back and is
 // done; the second reads the first's partials, adds its own -- fp32 addition
 // is commutative, so the sum is the same whichever chunk came first -- and
-// puts zero back.  One atomic round trip replaces the store,
-// acknowledgement, arrival count and reload of the arrival chain.  A partial
+// puts zero back.  One atomic round trip replaces a partial store, its
+// acknowledgement, an arrival count and a reload of the partials.  A partial
 // whose bits equal kSlotKey (a signaling NaN, which arithmetic never
 // produces) would store as zero, so it is sent as a quiet NaN.  GATE: the
 // slot is the 64-bit pair (sum, SwiGLU gate sum) at words 2*row, 2*row + 1,

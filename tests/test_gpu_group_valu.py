@@ -2,8 +2,8 @@
 one activation in one launch, their row tiles in one index space.  Every
 output is checked against the fp64 oracle and the sequential-fp32 gate, and
 against q4rdna_mul_mat_ex of the same GEMV at the same split bit for bit
-(same kernel arithmetic, same chunk order); at split 2 the chunks meet in
-exchange slots, at larger splits in the arrival chain."""
+(same kernel arithmetic, same reduction order); at split 2 the chunks meet
+in one exchange slot per row, at larger splits in a tree of them."""
 import ctypes
 
 import numpy as np
@@ -82,9 +82,9 @@ def test_valu_group_swiglu_equals_mul_mat_glu(cuda):
     assert_gemv_parity(y2.cpu().numpy(), ut2, 1024, cols, x_np, gate_tiles=gt2, label="glu 1024")
 
 
-def test_valu_group_long_k_arrival_chain(cuda):
+def test_valu_group_long_k_exchange_tree(cuda):
     """A down projection (K = 12288, split 6 by the policy) and a smaller
-    long-K GEMV with an add: the arrival chain, equal to single launches."""
+    long-K GEMV with an add: the exchange tree, equal to single launches."""
     cols = 12288
     t1, w1 = weight(4096, cols, 740)
     t2, w2 = weight(512, cols, 741)
