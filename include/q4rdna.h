@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define Q4RDNA_ABI_VERSION 3
+#define Q4RDNA_ABI_VERSION 4
 
 /* status codes */
 #define Q4RDNA_OK 0

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(L, name), name
     assert set(names) == set(_lib.EXPORTS)
-    assert L.q4rdna_abi_version() == 3
+    assert L.q4rdna_abi_version() == 4
 
 
 def test_library_is_gfx950_code_object():
