@@ -692,30 +692,13 @@ def chain_parity(y, tiles, rows, cols, xin, add=None, gate_tiles=None):
     return float(np.max(np.abs(y - want) / np.maximum(np.abs(want), 0.01 * rms))), O.rel_l2(y, seq)
 
 
-def layer_chain(tensors, replays: int, check_layers=(0, 17, 35),
-                dispatches=("reference", "grouped")):
-    """The stack as a decoder runs it: layer l+1's input depends on layer l,
-    so every projection waits for the one before.  Per layer: x_l RMS-
-    normalized feeds q, k and v; o on q's output plus the residual x_l (o's
-    real input is the attention output, a step outside this path) gives h;
-    h RMS-normalized feeds the gate/up SwiGLU site; down on that plus the
-    residual h gives x_{l+1}.  The two normalizations stand for the
-    decoder's own (without them the N(0, 0.02) weights grow the activations
-    quadratically through SwiGLU, to inf within five layers); each is one
-    launch of the bench library's RMS-norm kernel.  Two dispatches over the same weights, each captured into
-    one HIP graph of all 36 layers and replayed:
-      reference  the reference's hooks: q, k, v, o(+add), gate/up SwiGLU,
-                 down(+add) as six per-tensor launches (VALU kernel)
-      grouped    q/k/v as one group launch sharing x (the group policy:
-                 the VALU kernel), then o(+add), gate/up SwiGLU and
-                 down(+add) through the per-tensor entry points: four
-                 launches
-    us_per_layer is the whole chain's time per layer, normalizations
-    included; norm_us_per_layer is a graph of the normalizations alone over
-    the same buffers, and gemv_us_per_layer the difference, the GEMV
-    launches' share.  Parity: every launch of layers `check_layers` against
-    both bars on the inputs it actually read; replays equal the eager run."""
-    import numpy as np
+def decoder_chain(tensors):
+    """The decoder-layer chain's pieces, shared by `layer_chain` and
+    `chain_clocks`: (by name, layers, x0, buffers(), run(dispatch, bufs,
+    stream, gemvs=True)).  run issues, per layer, the RMS normalization,
+    q/k/v (three launches for "reference", one group for "grouped"), o + the
+    residual, the second normalization, the gate/up SwiGLU site and down +
+    the residual."""
     import torch
     from q4rdna import api
 
@@ -764,6 +747,37 @@ def layer_chain(tensors, replays: int, check_layers=(0, 17, 35),
             if gemvs:
                 api.mul_mat_glu(w(l, "ffn_up"), w(l, "ffn_gate"), b["hn"], b["act"], stream=stream)
                 api.mul_mat_add(w(l, "ffn_down"), b["act"], b["h"], b["out"], stream=stream)
+
+    return by, layers, x0, buffers, run
+
+
+def layer_chain(tensors, replays: int, check_layers=(0, 17, 35),
+                dispatches=("reference", "grouped")):
+    """The stack as a decoder runs it: layer l+1's input depends on layer l,
+    so every projection waits for the one before.  Per layer: x_l RMS-
+    normalized feeds q, k and v; o on q's output plus the residual x_l (o's
+    real input is the attention output, a step outside this path) gives h;
+    h RMS-normalized feeds the gate/up SwiGLU site; down on that plus the
+    residual h gives x_{l+1}.  The two normalizations stand for the
+    decoder's own (without them the N(0, 0.02) weights grow the activations
+    quadratically through SwiGLU, to inf within five layers); each is one
+    launch of the bench library's RMS-norm kernel.  Two dispatches over the same weights, each captured into
+    one HIP graph of all 36 layers and replayed:
+      reference  the reference's hooks: q, k, v, o(+add), gate/up SwiGLU,
+                 down(+add) as six per-tensor launches (VALU kernel)
+      grouped    q/k/v as one group launch sharing x (the group policy:
+                 the VALU kernel), then o(+add), gate/up SwiGLU and
+                 down(+add) through the per-tensor entry points: four
+                 launches
+    us_per_layer is the whole chain's time per layer, normalizations
+    included; norm_us_per_layer is a graph of the normalizations alone over
+    the same buffers, and gemv_us_per_layer the difference, the GEMV
+    launches' share.  Parity: every launch of layers `check_layers` against
+    both bars on the inputs it actually read; replays equal the eager run."""
+    import numpy as np
+    import torch
+
+    by, layers, x0, buffers, run = decoder_chain(tensors)
 
     def time_graph(graph, st):
         # Untimed replays for about 0.2 s first: the GPU's clocks settle a
@@ -993,6 +1007,82 @@ def stream_runs(data, launches: int = 5):
                            gb_per_s=round(nbytes / min(us[r]) / 1e3, 1)) for r in runs])
 
 
+def chain_clocks(tensors, replays: int = 50):
+    """Per-workgroup phase clocks of the grouped decoder-layer chain's four
+    GEMV launches (q/k/v group, o + add, gate/up SwiGLU, down + add), from
+    the clock build of the library (`--library
+    .../libq4rdna_sweep_clocks_gfx950.so`): each workgroup reads the GPU's
+    100 MHz real-time counter at its start, once x is staged, once its rows
+    are reduced, and at its end, and records its HW_ID.  The chain of
+    `decoder_chain` is captured into one HIP graph, replayed for 0.2 s, then
+    `replays` times; the records are the last replay's launches of the last
+    layer.  Per stage, relative to its first workgroup's start: the 10th /
+    50th / 90th percentile and maximum of each clock and of the phases
+    between them, the gap from the previous stage's last end, and how many
+    workgroups each CU (XCD, shader engine, array, CU from HW_ID) ran."""
+    import ctypes
+    import numpy as np
+    import torch
+    from q4rdna import _lib
+    L = _lib.load()
+    if not hasattr(L, "q4rdna_gemv_clocks"):
+        raise SystemExit("--gemv-clocks needs the clock build: --library "
+                         "rdna-gfx1201-v0.1_amd/q4rdna/libq4rdna_sweep_clocks_gfx950.so")
+    L.q4rdna_gemv_clocks.argtypes = [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_uint32]
+    L.q4rdna_gemv_clocks.restype = ctypes.c_int
+    L.q4rdna_gemv_clock_next.argtypes = []
+    L.q4rdna_gemv_clock_next.restype = ctypes.c_uint32
+    by, layers, x0, buffers, run = decoder_chain(tensors)
+    bufs = buffers()
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        run("grouped", bufs, st.cuda_stream)  # eager: allocates the stream's split-K workspace
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        run("grouped", bufs, st.cuda_stream)
+    last = L.q4rdna_gemv_clock_next()  # the slot after the graph's last launch
+    t_end = time.perf_counter() + 0.2
+    while time.perf_counter() < t_end:
+        with torch.cuda.stream(st):
+            graph.replay()
+        st.synchronize()
+    with torch.cuda.stream(st):
+        for _ in range(replays):
+            graph.replay()
+    torch.cuda.synchronize()
+
+    def pct(v):
+        return [round(float(np.percentile(v, p)), 2) for p in (10, 50, 90)] + [round(float(v.max()), 2)]
+
+    stages = {}
+    prev_end = None
+    for i, name in enumerate(("qkv_group", "o_add", "swiglu", "down_add")):
+        slot = (last - 4 + i) % 256
+        rec = np.zeros((1024, 6), dtype=np.uint64)
+        if L.q4rdna_gemv_clocks(slot, rec.ctypes.data, 1024) != 0:
+            raise RuntimeError("q4rdna_gemv_clocks failed")
+        n = int(rec[0, 5])
+        r = rec[:n].astype(np.int64)
+        if n == 0 or (r[:, 3] < r[:, 0]).any() or (r[:, 1] < r[:, 0]).any() or (r[:, 2] < r[:, 1]).any():
+            raise RuntimeError(f"{name}: incomplete or unordered clock record")
+        t0 = r[:, 0].min()
+        t = (r[:, :4] - t0) / 100.0
+        hw = r[:, 4]
+        cu = (np.arange(n) % 8) * 1000 + ((hw >> 13) & 7) * 100 + ((hw >> 12) & 1) * 16 + ((hw >> 8) & 15)
+        _, per_cu = np.unique(cu, return_counts=True)
+        hist = {int(k): int(v) for k, v in zip(*np.unique(per_cu, return_counts=True))}
+        stages[name] = dict(workgroups=n, start=pct(t[:, 0]), staged=pct(t[:, 1]), reduced=pct(t[:, 2]),
+                            end=pct(t[:, 3]), staged_after_start=pct(t[:, 1] - t[:, 0]),
+                            reduced_after_staged=pct(t[:, 2] - t[:, 1]), end_after_reduced=pct(t[:, 3] - t[:, 2]),
+                            life=pct(t[:, 3] - t[:, 0]),
+                            gap_from_previous_end_us=None if prev_end is None else round(float(t0 - prev_end) / 100.0, 2),
+                            cus=int(len(per_cu)), workgroups_per_cu=hist)
+        prev_end = r[:, 3].max()
+        log(f"[gemv-clocks] {name}: {stages[name]}")
+    return dict(layer=layers - 1, replays=replays, stages=stages)
+
+
 def floors(tensors, data, replays: int = 20):
     """What the GEMV launches are measured against, from plain reads of the
     same bytes (bench library kernels; graph replays, each read a different
@@ -1166,6 +1256,10 @@ def main() -> int:
                     help="per-workgroup start and end clocks of the stack sweep (needs --library with the clock "
                          "build, libq4rdna_sweep_clocks_gfx950.so), of the batched sweeps with --batches; prints "
                          "one JSON line instead of the stack bench")
+    ap.add_argument("--gemv-clocks", action="store_true",
+                    help="per-workgroup phase clocks (start, x staged, reduced, end) of the grouped decoder-layer "
+                         "chain's four GEMV launches (needs --library with the clock build, "
+                         "libq4rdna_sweep_clocks_gfx950.so); prints one JSON line")
     ap.add_argument("--floors", action="store_true",
                     help="plain-read and launch floors (stack read, empty launch, per-stage reads and four "
                          "dependent stage reads per layer); prints one JSON line instead of the stack bench")
@@ -1201,6 +1295,9 @@ def main() -> int:
     stack_bytes = sum(algorithmic_bytes(t["rows"], t["cols"]) for t in tensors)
     if args.layer_chain:
         print(json.dumps({"layer_chain": layer_chain(tensors, max(args.steps, 20))}), flush=True)
+        return 0
+    if args.gemv_clocks:
+        print(json.dumps({"chain_clocks": chain_clocks(tensors)}), flush=True)
         return 0
     if args.floors:
         print(json.dumps({"floors": floors(tensors, _data)}), flush=True)

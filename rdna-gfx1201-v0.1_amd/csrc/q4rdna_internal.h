@@ -38,6 +38,7 @@ struct GemvArgs {
                            // 16 for chunks of 65..128 groups (gemv_waves)
     uint32_t vectors;      // launch_gemv_multi: activation vectors (x [vectors][cols], y/add [vectors][rows])
     uint32_t split_magic;  // split_magic(split)
+    uint32_t clock_slot;   // the clock build's record slot for this launch
 };
 
 // Device-side descriptor of one GEMV in a multi-tensor plan.  Work items are
@@ -81,16 +82,23 @@ constexpr uint32_t kPrepBytes = 288;  // VALU layout: 16 float4 of scaled x + 8 
 constexpr bool kSweepValu = false;
 constexpr uint32_t kPrepBytes = 272;  // int8 digits (256) + the group factor (16)
 #endif
-// The library built with -DQ4RDNA_SWEEP_CLOCKS (make sweep-clocks) records
-// each single-vector sweep workgroup's first and last clock (s_memrealtime,
-// 100 MHz) of the latest launch, for up to kMaxSweepClocks workgroups; the
-// product build records nothing.
+// The library built with -DQ4RDNA_SWEEP_CLOCKS (make sweep-clocks, "the
+// clock build") records each single-vector sweep workgroup's first and last
+// clock (s_memrealtime, 100 MHz) of the latest launch, for up to
+// kMaxSweepClocks workgroups, and for the single-launch kernels (gemv_kernel's
+// short-range path, gemv_group_kernel) each workgroup's clocks at its start,
+// once x is staged, once its rows are reduced and at its end, with its
+// HW_ID, in launch slot clock_slot (one of kGemvClockSlots, given per launch
+// by the host); the product build records nothing.
 #if defined(Q4RDNA_SWEEP_CLOCKS)
 constexpr bool kSweepClocks = true;
 #else
 constexpr bool kSweepClocks = false;
 #endif
 constexpr uint32_t kMaxSweepClocks = 4096;
+constexpr uint32_t kGemvClockSlots = 256;
+constexpr uint32_t kGemvClockWorkgroups = 1024;
+constexpr uint32_t kGemvClockWords = 6;  // start, staged, reduced, end, HW_ID, grid size
 // K chunk of a single-vector plan item: 192 groups holds a whole 12288-wide
 // row in one item, so such GEMVs need no split-K partials.
 constexpr uint32_t kChunkGroups = 192;
@@ -171,6 +179,7 @@ struct GemvGroupArgs {
     uint32_t count, cols, split, tiles;
     uint32_t short_waves;  // 8 or 4, as GemvArgs::short_waves
     uint32_t split_magic;  // split_magic(split)
+    uint32_t clock_slot;   // as GemvArgs::clock_slot
 };
 hipError_t launch_gemv_group(const GemvGroupArgs &args, hipStream_t stream);
 

@@ -67,6 +67,36 @@ struct TileRegs {
     uint32_t s01, s23;
 };
 
+// The clock build's phase clocks of a single-launch workgroup (see
+// kGemvClockSlots): read at its start, once x is staged, once its rows are
+// reduced, and at its end; the product build compiles them away.
+struct PhaseClocks {
+    uint64_t t[4];
+};
+__device__ __forceinline__ void phase_clock(PhaseClocks &c, int i) {
+    if constexpr (kSweepClocks) c.t[i] = __builtin_amdgcn_s_memrealtime();
+}
+#if defined(Q4RDNA_SWEEP_CLOCKS)
+__device__ uint64_t g_gemv_clocks[kGemvClockSlots][kGemvClockWorkgroups][kGemvClockWords];
+#endif
+// After every thread has finished: the end clock, then thread 0 stores the
+// workgroup's record with one vector store per word.
+__device__ __forceinline__ void phase_record(PhaseClocks &c, uint32_t slot) {
+#if defined(Q4RDNA_SWEEP_CLOCKS)
+    __syncthreads();
+    phase_clock(c, 3);
+    if (threadIdx.x == 0 && blockIdx.x < kGemvClockWorkgroups && slot < kGemvClockSlots) {
+        uint64_t *r = g_gemv_clocks[slot][blockIdx.x];
+        for (int i = 0; i < 4; ++i) r[i] = c.t[i];
+        r[4] = __builtin_amdgcn_s_getreg((31 << 11) | 4);  // HW_REG_HW_ID, all 32 bits
+        r[5] = gridDim.x;
+    }
+#else
+    (void)c;
+    (void)slot;
+#endif
+}
+
 // Weights are read exactly once per GEMV: nontemporal loads stream them past
 // the caches instead of evicting the activations and partial sums.
 __device__ __forceinline__ TileRegs load_tile(const uint8_t *__restrict__ tile, int q, int a) {
@@ -226,7 +256,8 @@ template <bool GATE, int T, int W, class Sh>
 __device__ __forceinline__ void tile_row_partial_short(Sh &sh, const uint8_t *__restrict__ w,
                                                        const uint8_t *__restrict__ gw,
                                                        const float *__restrict__ x, uint32_t cols, uint32_t rt,
-                                                       uint32_t g_begin, uint32_t g_end, float &out, float &gout) {
+                                                       uint32_t g_begin, uint32_t g_end, float &out, float &gout,
+                                                       PhaseClocks &clk) {
     static_assert(W * T <= static_cast<int>(sizeof(sh.st.c) / sizeof(sh.st.c[0])) &&
                       W <= static_cast<int>(sizeof(sh.red[0]) / sizeof(sh.red[0][0])),
                   "the range fits one stage");
@@ -282,6 +313,7 @@ __device__ __forceinline__ void tile_row_partial_short(Sh &sh, const uint8_t *__
         }
     }
     __syncthreads();
+    phase_clock(clk, 1);
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     float gacc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -296,6 +328,7 @@ __device__ __forceinline__ void tile_row_partial_short(Sh &sh, const uint8_t *__
         }
     }
     reduce_rows<GATE, W>(sh, acc, gacc, out, gout);
+    phase_clock(clk, 2);
 }
 
 template <bool GATE, bool ADD>
@@ -324,6 +357,8 @@ __device__ __forceinline__ void finish_rows(float *__restrict__ y, const float *
 template <bool GATE, bool ADD, int T, int W>
 __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs args) {
     __shared__ SharedFor<W> sh;
+    PhaseClocks clk;
+    phase_clock(clk, 0);
     const uint32_t groups = args.cols / kGroup;
     const uint32_t split = args.split;
     const uint32_t logical = xcd_remap(blockIdx.x, gridDim.x);
@@ -334,8 +369,9 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs args) {
     if constexpr (T == 0)
         tile_row_partial<GATE>(sh, args.w, args.gate, args.x, args.cols, rt, g_begin, g_end, v, gv);
     else
-        tile_row_partial_short<GATE, T, W>(sh, args.w, args.gate, args.x, args.cols, rt, g_begin, g_end, v, gv);
+        tile_row_partial_short<GATE, T, W>(sh, args.w, args.gate, args.x, args.cols, rt, g_begin, g_end, v, gv, clk);
     finish_rows<GATE, ADD>(args.y, args.add, args.slots, args.rows, split, s, rt, v, gv);
+    if constexpr (T != 0) phase_record(clk, args.clock_slot);
 }
 
 // Several GEMVs sharing x (q4rdna_mul_mat_group): the row tiles of all of
@@ -345,6 +381,8 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs args) {
 template <bool GATE, int T, int W>
 __global__ __launch_bounds__(64 * W) void gemv_group_kernel(GemvGroupArgs a) {
     __shared__ Shared sh;
+    PhaseClocks clk;
+    phase_clock(clk, 0);
     const uint32_t groups = a.cols / kGroup;
     const uint32_t split = a.split;
     const uint32_t logical = xcd_remap(blockIdx.x, gridDim.x);
@@ -359,11 +397,12 @@ __global__ __launch_bounds__(64 * W) void gemv_group_kernel(GemvGroupArgs a) {
     const uint32_t g_begin = div_split(s * groups, split, a.split_magic);
     const uint32_t g_end = div_split((s + 1) * groups, split, a.split_magic);
     float v = 0.f, gv = 0.f;
-    tile_row_partial_short<GATE, T, W>(sh, G.w, G.gate, a.x, a.cols, rt, g_begin, g_end, v, gv);
+    tile_row_partial_short<GATE, T, W>(sh, G.w, G.gate, a.x, a.cols, rt, g_begin, g_end, v, gv, clk);
     if (G.add != nullptr)
         finish_rows<GATE, true>(G.y, G.add, G.slots, G.rows, split, s, rt, v, gv);
     else
         finish_rows<GATE, false>(G.y, nullptr, G.slots, G.rows, split, s, rt, v, gv);
+    phase_record(clk, a.clock_slot);
 }
 
 // ---- several activation vectors against one weight (n = 2..8) -------------
@@ -976,3 +1015,15 @@ hipError_t launch_pack(const float *w, uint32_t rows, uint32_t cols, int algorit
 }
 
 }  // namespace q4rdna
+
+#if defined(Q4RDNA_SWEEP_CLOCKS)
+// Clock build only: the record of launch slot `slot`, kGemvClockWords words
+// for each of workgroups 0..count-1 (count <= kGemvClockWorkgroups).
+extern "C" int q4rdna_gemv_clocks(uint32_t slot, uint64_t *out, uint32_t count) {
+    if (out == nullptr || slot >= q4rdna::kGemvClockSlots || count > q4rdna::kGemvClockWorkgroups) return -1;
+    const size_t words = q4rdna::kGemvClockWords;
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(q4rdna::g_gemv_clocks), words * sizeof(uint64_t) * count,
+                               words * sizeof(uint64_t) * q4rdna::kGemvClockWorkgroups * slot,
+                               hipMemcpyDeviceToHost) == hipSuccess ? 0 : -4;
+}
+#endif

@@ -151,6 +151,14 @@ int get_workspace(int device, hipStream_t stream, size_t slots, Workspace **out)
     return Q4RDNA_OK;
 }
 
+// The clock build's record slot for the next single-launch GEMV (0 in the
+// product build, which records nothing).
+std::atomic<uint32_t> g_clock_launches{0};
+uint32_t next_clock_slot() {
+    if constexpr (!q4rdna::kSweepClocks) return 0;
+    return g_clock_launches.fetch_add(1, std::memory_order_relaxed) % q4rdna::kGemvClockSlots;
+}
+
 bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 uint32_t policy_split(uint32_t rows, uint32_t cols, int device) {
@@ -272,6 +280,7 @@ int launch_tensor_in(const TensorLaunch &launch, const q4rdna_weight *w, const u
     args.short_waves =
         gemv_waves(w->columns / kGroup, launch.split, workgroups, static_cast<uint32_t>(cu_count(w->device)));
     args.slots = slots;
+    args.clock_slot = next_clock_slot();
     const hipError_t e = launch.sequential ? launch_gemv_sequential(args, stream) : launch_gemv(args, stream);
     if (e != hipSuccess) return hip_fail(e, "GEMV launch");
     return Q4RDNA_OK;
@@ -661,6 +670,7 @@ int launch_group_valu(const q4rdna_group_desc *descs, uint32_t count, const floa
     args.split_magic = q4rdna::split_magic(split);
     args.tiles = tiles;
     args.short_waves = workgroups <= 4ull * cu_count(device) ? 8u : 4u;
+    args.clock_slot = next_clock_slot();
     uint32_t tile_begin = 0;
     size_t soff = 0;
     for (uint32_t i = 0; i < count; ++i) {
@@ -979,3 +989,11 @@ int q4rdna_dequantize(const q4rdna_weight *w, float *out, void *stream) {
 }
 
 }  // extern "C"
+
+#if defined(Q4RDNA_SWEEP_CLOCKS)
+// Clock build only: the record slot the next single-launch GEMV will take
+// (launches take slots in order, modulo kGemvClockSlots).
+extern "C" uint32_t q4rdna_gemv_clock_next(void) {
+    return g_clock_launches.load(std::memory_order_relaxed) % q4rdna::kGemvClockSlots;
+}
+#endif

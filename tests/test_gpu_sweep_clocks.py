@@ -1,8 +1,11 @@
 """The clock build of the library (libq4rdna_sweep_clocks_gfx950.so,
--DQ4RDNA_SWEEP_CLOCKS, read by bench.py --clocks): its sweep still meets
-both parity bars, and q4rdna_sweep_clocks returns one (start, end) pair of
-100 MHz counter values per workgroup of the latest sweep, every start before
-its end and the whole launch within a plausible window.  It runs in a fresh
+-DQ4RDNA_SWEEP_CLOCKS, read by bench.py --clocks and --gemv-clocks): its
+sweep and its single launches still meet both parity bars;
+q4rdna_sweep_clocks returns one (start, end) pair of 100 MHz counter values
+per workgroup of the latest sweep, every start before its end and the whole
+launch within a plausible window; and q4rdna_gemv_clocks returns, for the
+slot each single launch took, every workgroup's start, x-staged, reduced and
+end clocks in that order, its HW_ID and the grid size.  It runs in a fresh
 process, since a process binds one build of the library."""
 import os
 import subprocess
@@ -64,6 +67,37 @@ for rep in range(2):
         assert_gemv_parity(y.cpu().numpy(), t, rows, cols, x, gate_tiles=gt, add=add_np, label=(rows, cols))
 assert fn(buf.ctypes.data, 1 << 20) != 0  # beyond the recorded workgroups: refused
 plan.close()
+
+gfn = lib.q4rdna_gemv_clocks
+gfn.restype = ctypes.c_int
+gfn.argtypes = [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_uint32]
+nxt = lib.q4rdna_gemv_clock_next
+nxt.restype = ctypes.c_uint32
+rows, cols = 4096, 4096
+t = random_tiles(rows, cols, 1500)
+x = O.gaussian_x(cols, 1501)
+w = api.QWeight.from_tiles(dev_u8(t), rows, cols)
+y = torch.full((rows,), np.nan, device="cuda")
+t2 = random_tiles(1024, cols, 1502)
+w2 = api.QWeight.from_tiles(dev_u8(t2), 1024, cols)
+y2 = torch.full((1024,), np.nan, device="cuda")
+for split, grid in ((2, 256), (4, 512)):
+    slot = nxt()
+    assert api.mul_mat_ex(w, dev_f32(x), y, split_k=split)
+    gslot = nxt()
+    assert gslot == (slot + 1) % 256
+    assert api.mul_mat_group([(w, y), (w2, y2)], dev_f32(x), split_k=split)
+    torch.cuda.synchronize()
+    assert_gemv_parity(y.cpu().numpy(), t, rows, cols, x, label=("clock build", split))
+    assert_gemv_parity(y2.cpu().numpy(), t2, 1024, cols, x, label=("clock build group", split))
+    for s, n in ((slot, grid), (gslot, grid * 5 // 4)):
+        rec = np.zeros((1024, 6), dtype=np.uint64)
+        assert gfn(s, rec.ctypes.data, 1024) == 0
+        r = rec[:n].astype(np.int64)
+        assert (r[:, 5] == n).all(), (s, r[:4, 5])
+        assert (r[:, 0] > 0).all() and (np.diff(r[:, :4], axis=1) >= 0).all()
+        assert (r[:, 3] - r[:, 0]).max() < 100 * 10000  # under 10 ms
+assert gfn(256, buf.ctypes.data, 1) != 0 and gfn(0, buf.ctypes.data, 1025) != 0  # out of range: refused
 print("ok")
 """
 
