@@ -160,12 +160,10 @@ __device__ __forceinline__ bool exchange_pair(uint32_t *slots, uint32_t row, flo
 template <bool GATE>
 __device__ __forceinline__ bool exchange_tree(uint32_t *slots, uint32_t rows, uint32_t split, uint32_t s,
                                               uint32_t row, float &v, float &gv) {
-    const uint32_t P = 1u << (32 - __builtin_clz(split - 1u));
+    const uint32_t P = 1u << (32 - __builtin_clz(split - 1u));  // exchange_leaves(split)
     uint32_t node = P + s;
     for (uint32_t d = 0; node > 1u; ++d, node >>= 1) {
-        // A left child (even node) meets only if its right sibling's first
-        // leaf, (node + 1) << d, is a chunk.
-        if ((node & 1u) != 0u || ((node + 1u) << d) - P < split) {
+        if (exchange_meets(node, d, P, split)) {
             uint32_t *region = slots + static_cast<size_t>((node >> 1) - 1u) * rows * (GATE ? 2u : 1u);
             if (!exchange_pair<GATE>(region, row, v, gv)) return false;
         }

@@ -64,11 +64,7 @@ constexpr uint32_t kMaxSplit = 64;
 // (the per-tensor and group kernels): one per internal node of a heap over
 // the smallest power of two >= split, so split - 1 of them take part; none
 // without a split.
-constexpr uint32_t exchange_nodes(uint32_t split) {
-    uint32_t p = 1;
-    while (p < split) p <<= 1;
-    return p - 1;
-}
+constexpr uint32_t exchange_nodes(uint32_t split) { return exchange_leaves(split) - 1; }
 
 // Split-K factor of a per-tensor launch of rows x cols on a GPU with `cus`
 // compute units.

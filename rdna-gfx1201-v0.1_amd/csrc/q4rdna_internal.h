@@ -20,6 +20,23 @@ constexpr uint32_t kTileBytes = 1088;
 constexpr uint32_t kSlotKey = 0x7fa5a5a5u;
 constexpr uint32_t kSlotQuietNan = 0x7fc00000u;
 
+// The exchange tree's shape, shared by the kernels (exchange_tree) and the
+// host (slot sizing, the sanitizer check's simulation).  The `split` >= 2
+// K chunks of a row are the leaves P + s of a heap over P =
+// exchange_leaves(split) leaves; internal node k (1 <= k < P) owns slot
+// region k - 1.  Going up from a leaf, node `node` at depth d (0 = the
+// leaves) meets its sibling's subtree in its parent's slot unless it is a
+// left child whose right sibling's first leaf, (node + 1) << d, lies past
+// the last chunk; then the value passes straight up.
+__host__ __device__ constexpr uint32_t exchange_leaves(uint32_t split) {
+    uint32_t p = 1;
+    while (p < split) p <<= 1;
+    return p;
+}
+__host__ __device__ constexpr bool exchange_meets(uint32_t node, uint32_t d, uint32_t leaves, uint32_t split) {
+    return (node & 1u) != 0u || ((node + 1u) << d) - leaves < split;
+}
+
 // One GEMV launch.  gate != nullptr selects SwiGLU, add != nullptr the bias
 // epilogue.  split > 1 K chunks meet in an exchange tree over
 // slots[exchange_nodes(split) * vectors * rows (x2 with gate)] (vectors is 1

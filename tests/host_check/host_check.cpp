@@ -262,11 +262,100 @@ int run_inspect(int argc, char **argv) {
     return 0;
 }
 
+
+// The exchange tree's protocol, run on the CPU with the kernels' own shape
+// functions (exchange_leaves, exchange_meets): for every split 2..64 and
+// random interleavings of the chunks' exchanges, one chunk clears the root,
+// every slot region used is swapped into exactly twice (so all are empty
+// again), split - 1 regions take part, all indices lie inside
+// exchange_nodes(split) regions, and the root's sum -- kept as the
+// expression it adds up, each node writing its two operands in a fixed
+// order since fp32 addition is commutative -- is the same in every
+// interleaving.
+// `meets` is the shape rule under test: the kernels' exchange_meets, or a
+// planted mistake that the check must catch.
+using MeetsFn = bool (*)(uint32_t, uint32_t, uint32_t, uint32_t);
+bool planted_off_by_one(uint32_t node, uint32_t d, uint32_t leaves, uint32_t split) {
+    return (node & 1u) != 0u || ((node + 1u) << d) - leaves <= split;
+}
+bool planted_always(uint32_t, uint32_t, uint32_t, uint32_t) { return true; }
+bool real_meets(uint32_t node, uint32_t d, uint32_t leaves, uint32_t split) {
+    return q4rdna::exchange_meets(node, d, leaves, split);
+}
+
+int run_tree(MeetsFn meets) {
+    std::mt19937 rng(12345);
+    int splits = 0;
+    for (uint32_t split = 2; split <= q4rdna::host::kMaxSplit; ++split) {
+        const uint32_t P = q4rdna::exchange_leaves(split);
+        std::string first;
+        bool ok = true;
+        for (int trial = 0; trial < 200 && ok; ++trial) {
+            std::vector<std::string> slot(P - 1), val(split);
+            std::vector<int> swaps(P - 1, 0);
+            std::vector<uint32_t> node(split), depth(split, 0);
+            std::vector<uint32_t> alive;
+            for (uint32_t s = 0; s < split; ++s) {
+                val[s] = "p" + std::to_string(s);
+                node[s] = P + s;
+                alive.push_back(s);
+            }
+            std::vector<std::string> roots;
+            while (!alive.empty()) {
+                const size_t pick = rng() % alive.size();
+                const uint32_t s = alive[pick];
+                // Advance chunk s to its next meeting (or past the root).
+                while (node[s] > 1u && !meets(node[s], depth[s], P, split)) {
+                    node[s] >>= 1;
+                    ++depth[s];
+                }
+                if (node[s] <= 1u) {
+                    roots.push_back(val[s]);
+                    alive.erase(alive.begin() + pick);
+                    continue;
+                }
+                const uint32_t region = (node[s] >> 1) - 1u;
+                ok = ok && region < q4rdna::host::exchange_nodes(split);
+                if (!ok) break;
+                ++swaps[region];
+                node[s] >>= 1;
+                ++depth[s];
+                if (slot[region].empty()) {
+                    slot[region] = val[s];
+                    alive.erase(alive.begin() + pick);
+                } else {
+                    const std::string &a = slot[region], &b = val[s];
+                    val[s] = a < b ? "(" + a + "+" + b + ")" : "(" + b + "+" + a + ")";
+                    slot[region].clear();
+                }
+            }
+            int used = 0;
+            for (size_t k = 0; k < slot.size(); ++k) {
+                ok = ok && slot[k].empty() && (swaps[k] == 0 || swaps[k] == 2);
+                used += swaps[k] == 2;
+            }
+            ok = ok && roots.size() == 1 && used == static_cast<int>(split) - 1;
+            if (ok && trial == 0) first = roots[0];
+            ok = ok && roots[0] == first;
+        }
+        expect(ok, "tree protocol", ("split " + std::to_string(split)).c_str());
+        if (split == 6) std::printf("{\"split\": 6, \"root\": \"%s\"}\n", first.c_str());
+        ++splits;
+    }
+    std::printf("{\"tree_splits\": %d, \"failures\": %d}\n", splits, g_failures);
+    return g_failures == 0 ? 0 : 1;
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {
     if (argc >= 2 && std::strcmp(argv[1], "layout") == 0) return run_layout();
     if (argc >= 2 && std::strcmp(argv[1], "inspect") == 0) return run_inspect(argc - 2, argv + 2);
-    std::fprintf(stderr, "usage: host_check layout | inspect FILE...\n");
+    if (argc >= 2 && std::strcmp(argv[1], "tree") == 0) return run_tree(real_meets);
+    // Planted mistakes in the shape rule: each must be reported as failures.
+    if (argc >= 2 && std::strcmp(argv[1], "tree-planted-off-by-one") == 0) return run_tree(planted_off_by_one);
+    if (argc >= 2 && std::strcmp(argv[1], "tree-planted-always") == 0) return run_tree(planted_always);
+    std::fprintf(stderr, "usage: host_check layout | inspect FILE... | tree | tree-planted-off-by-one | "
+                         "tree-planted-always\n");
     return 2;
 }

@@ -4,7 +4,8 @@ valid, mutated, truncated and random images (statuses against the oracle's
 restatement of the reference loader, source/q4rdna.cu:129-170), and the plan
 layout with its item deal on the Qwen3-8B stacks, batched plans and mixed
 plans (every item dealt exactly once, each workgroup's list ascending,
-scratch regions aligned and disjoint).  CPU only."""
+scratch regions aligned and disjoint), and the split-K exchange tree's
+protocol with the kernels' own shape functions.  CPU only."""
 import json
 import os
 import subprocess
@@ -88,3 +89,21 @@ def test_sidecar_parser_under_sanitizers(host_check, golden, tmp_path):
         assert got[name]["status"] < 0, name
         # The oracle's loader restatement rejects the same images.
         assert O.validate_sidecar(bytearray(data)) < 0, name
+
+
+def test_exchange_tree_protocol_under_sanitizers(host_check):
+    """The kernels' exchange-tree shape (exchange_leaves / exchange_meets in
+    csrc/q4rdna_internal.h) under random interleavings of the chunks'
+    exchanges for every split 2..64: one root, every slot used exactly twice
+    and left empty, split - 1 regions used, one sum expression.  Two planted
+    mistakes in the shape rule (an off-by-one bound; meeting at every node)
+    must fail it for every split that is not a power of two."""
+    r, lines = run(host_check, "tree")
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert {"split": 6, "root": "(((p0+p1)+(p2+p3))+(p4+p5))"} in lines
+    assert lines[-1] == {"tree_splits": 63, "failures": 0}
+    non_powers = sum(1 for s in range(2, 65) if s & (s - 1))
+    for planted in ("tree-planted-off-by-one", "tree-planted-always"):
+        r, lines = run(host_check, planted)
+        assert r.returncode == 1
+        assert lines[-1] == {"tree_splits": 63, "failures": non_powers}, planted
