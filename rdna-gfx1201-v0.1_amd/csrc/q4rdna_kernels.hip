@@ -349,7 +349,15 @@ __device__ __forceinline__ void finish_rows(float *__restrict__ y, const float *
                                             uint32_t rt, float v, float gv) {
     const uint32_t row = rt * kTileRows + (threadIdx.x & 31);
     if (threadIdx.x >= 32) return;
-    if (split == 1 || exchange_tree<GATE>(slots, rows, split, s, row, v, gv)) y[row] = epilogue<GATE, ADD>(v, gv, add, row);
+    // The bias is loaded before the exchanges, so its round trip overlaps
+    // theirs instead of following the last one.
+    float b = 0.f;
+    if constexpr (ADD) b = add[row];
+    if (split == 1 || exchange_tree<GATE>(slots, rows, split, s, row, v, gv)) {
+        if constexpr (ADD) v += b;
+        if constexpr (GATE) v *= silu(gv);
+        y[row] = v;
+    }
 }
 
 // Workgroup b covers row tile rt and K chunk s of `split`, remapped so the
