@@ -117,3 +117,20 @@ def test_argument_errors_before_any_device_call():
 def test_glu_op_other_than_swiglu_is_not_applicable():
     L = q4rdna.load()
     assert L.q4rdna_mul_mat_glu(None, None, None, 0, 7, None, 0, None) == q4rdna.NOT_APPLICABLE
+
+
+def test_python_constants_match_the_header():
+    """Every Q4RDNA_* constant the header defines that the ctypes harness
+    mirrors (status codes, format, algorithms, kernels, limits, the no-alloc
+    slot count) has the header's value, so the two cannot drift apart."""
+    import re
+    from q4rdna import _lib
+    header = open(os.path.join(ROOT, "include", "q4rdna.h")).read()
+    seen = 0
+    for name, expr in re.findall(r"^#define Q4RDNA_(\w+)\s+([^/\n]+)", header, flags=re.M):
+        if name in ("H", "ABI_VERSION") or not hasattr(_lib, name):
+            continue
+        value = eval(re.sub(r"(\d+)u\b", r"\1", expr.strip()), {})
+        assert getattr(_lib, name) == value, (name, getattr(_lib, name), value)
+        seen += 1
+    assert seen >= 18, seen
