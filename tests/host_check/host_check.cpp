@@ -127,8 +127,11 @@ void check_layout(const std::string &name, const std::vector<Shape> &shapes, uin
             expect(align_check(L.part_off[i]) == 0 && align_check(L.cnt_off[i]) == 0, "tail alignment", name);
             const uint64_t part_end = L.part_off[i] + 4ull * p.chunks * p.streams * n * p.rows;
             expect(part_end <= L.cnt_off[i], "partials before counters", name);
-            expect(L.tail_off + L.cnt_off[i] + 4ull * ((p.rows + 63) / 64) <= L.scratch_bytes, "counters in scratch",
-                   name);
+            // one counter per block: 64-row blocks for single vectors, 256-row
+            // blocks for batches
+            const uint64_t block_rows = n == 1 ? q4rdna::kBlockRows : q4rdna::kBatchBlockRows;
+            expect(L.tail_off + L.cnt_off[i] + 4ull * ((p.rows + block_rows - 1) / block_rows) <= L.scratch_bytes,
+                   "counters in scratch", name);
         }
     }
     expect(items == L.items && groups == L.groups, "totals", name);
@@ -192,6 +195,7 @@ int run_layout() {
     check_layout("qwen3_216_swiglu", qwen3_stack(true), 1, 256);
     check_layout("qwen3_252_batch4", qwen3_stack(false), 4, 256);
     check_layout("qwen3_252_batch8", qwen3_stack(false), 8, 256);
+    check_layout("qwen3_216_swiglu_batch8", qwen3_stack(true), 8, 256);
     check_layout("mixed", mixed_plan(7), 1, 256);
     check_layout("mixed_batch3", mixed_plan(8), 3, 256);
     check_layout("mixed_small_gpu", mixed_plan(9), 1, 8);

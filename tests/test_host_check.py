@@ -49,6 +49,8 @@ def test_plan_layout_and_deal_under_sanitizers(host_check):
     f = by["qwen3_216_swiglu"]
     assert f["gemvs"] == 216 and f["both_streams"] and f["all_per_one"]
     assert by["qwen3_252_batch8"]["items"] == by["qwen3_252_batch4"]["items"]
+    g8 = by["qwen3_216_swiglu_batch8"]
+    assert g8["gemvs"] == 216 and not g8["all_per_one"] and not g8["both_streams"]
     assert not by["mixed"]["all_per_one"] and by["mixed"]["both_streams"]
     assert by["mixed_small_gpu"]["workgroups"] == 16
     assert by["one_gemv"]["items"] == 1
