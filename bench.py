@@ -532,25 +532,35 @@ def time_tensor(rows: int, cols: int, split: int, seed: int, reps: int = 40):
     return us, copies
 
 
-def batch_plan(tensors, n: int, seed: int):
+def batch_plan(tensors, n: int, seed: int, fused: bool = False):
     """The stack's GEMVs with n fresh N(0, 1) activation vectors each, as one
-    batched plan: (plan, [(weight, x [n, K], y [n, M])])."""
+    batched plan: (plan, [(weight, x [n, K], y [n, M])]).  With fused, each
+    layer's gate and up are one SwiGLU GEMV on up's x (216 GEMVs, the
+    reference's fused dispatch)."""
     import torch
     from q4rdna import api
+    by = {t["name"]: t for t in tensors}
     gen = torch.Generator(device="cuda")
     items = []
     for i, t in enumerate(tensors):
+        if fused and t["name"].endswith("ffn_gate.weight"):
+            continue
         gen.manual_seed(seed + 0x4000 + 1000 * n + i)
         x = torch.randn(n, t["cols"], generator=gen, device="cuda", dtype=torch.float32)
         y = torch.empty(n, t["rows"], device="cuda", dtype=torch.float32)
-        items.append((t["w"], x, y))
+        if fused and t["name"].endswith("ffn_up.weight"):
+            items.append((t["w"], x, y, by[t["name"].replace("ffn_up", "ffn_gate")]["w"], None))
+        else:
+            items.append((t["w"], x, y))
     return api.Plan(items, batch=n), items
 
 
 def batch_table(tensors, batches, steps: int, warmup: int, seed: int):
     """The stack's 252 GEMVs with N activation vectors each (the small-batch
     decode shapes): one batched plan per N over the same weights, timed like
-    the main bench; parity of every vector of three tensors vs the oracle."""
+    the main bench; parity of every vector of three tensors vs the oracle.
+    Each row also times the same stack with gate/up fused into one SwiGLU
+    GEMV per layer (fused_us_per_stack, fused_sweep_us)."""
     import oracle as O
     out = []
     for n in batches:
@@ -574,6 +584,12 @@ def batch_table(tensors, batches, steps: int, warmup: int, seed: int):
                    sweep_gb_per_s=round(step_bytes / mean(sweep_ms) / 1e6, 1),
                    tflops=round(sum(2 * t["rows"] * t["cols"] * n for t in tensors) / ms_per_step / 1e9, 3),
                    parity_gate_max=worst)
+        plan.close()
+        del items
+        plan, items = batch_plan(tensors, n, seed, fused=True)
+        settle(plan, 0.2)
+        ms_fused, sweep_fused, _ = time_plan(plan, steps, warmup)
+        row.update(fused_us_per_stack=round(ms_fused * 1000, 2), fused_sweep_us=round(mean(sweep_fused) * 1000, 2))
         log(f"[batch] N={n}: {row}")
         out.append(row)
         plan.close()

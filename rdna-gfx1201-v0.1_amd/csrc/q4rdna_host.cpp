@@ -297,10 +297,10 @@ int layout_plan(const q4rdna_gemv_desc *descs, uint32_t count, uint32_t n, int d
     // end of the sweep, where workgroups run out of items, deals short ones.
     L.order.resize(count);
     for (uint32_t i = 0; i < count; ++i) L.order[i] = i;
-    // A single-vector SwiGLU GEMV whose rows fit one chunk runs both weight
-    // streams in one item per block (no split-K partials).
+    // A SwiGLU GEMV whose rows fit one chunk runs both weight streams in one
+    // item per block (no split-K partials), single vectors and batches alike.
     auto both_streams = [&](uint32_t i) {
-        return n == 1 && descs[i].gate_tiles != nullptr && descs[i].weight.columns / kGroup <= chunk_groups;
+        return descs[i].gate_tiles != nullptr && descs[i].weight.columns / kGroup <= chunk_groups;
     };
     // A single-vector GEMV with no gate whose rows fit one 64-group step
     // block runs two 64-row blocks per item: half the item ends.

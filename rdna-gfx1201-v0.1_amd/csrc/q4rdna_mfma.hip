@@ -914,7 +914,8 @@ __global__ __launch_bounds__(256) void plan_valu_kernel(const PlanDesc *__restri
 // MFMA per operand, not more loads or transposes.
 //  * Item: (256-row block = 8 row tiles, stream, K chunk of up to
 //    kBatchChunkGroups = 192 groups); wave w takes groups
-//    chunk start + w + 4s, one per step.
+//    chunk start + w + 4s, one per step.  A SwiGLU GEMV whose rows fit one
+//    chunk has one item per block that streams up and then gate.
 //  * Loads per step: load instruction c reads the whole code area of row
 //    tile c at the step's group (1 KB contiguous), restaged through LDS as in
 //    the single-vector sweep; lane (kslot, j) then reads rows 16h..16h+15 of
@@ -1007,7 +1008,10 @@ __device__ __forceinline__ void run_batch_item(BatchShared<NQ> &sh, const PlanDe
                                                int lane, int wave) {
     const uint32_t groups = d.cols / kGroup;
     const uint32_t tiles = d.rows / kTileRows;
-    const uint32_t per = d.streams * d.chunks;
+    const uint32_t per = d.per;
+    // A SwiGLU GEMV whose rows fit one chunk has one item per block that
+    // streams up, then gate, into two accumulator sets (no partials).
+    const bool both = d.streams > 1 && per == 1;
     const uint32_t block = local / per, part = local - block * per;
     const uint32_t stream = part / d.chunks, chunk = part - stream * d.chunks;
     const uint32_t g_begin = chunk * kBatchChunkGroups;
@@ -1060,25 +1064,20 @@ __device__ __forceinline__ void run_batch_item(BatchShared<NQ> &sh, const PlanDe
     // single-vector sweep).  Loading the next item's first step across this
     // item's end, after the barrier that follows the last step (the next
     // item is claimed one ahead), measured 0.6-1.3 % slower at N = 2, 4, 8.
-    for (uint32_t g = g_begin + wave; g < g_end; g += kBatchWaves) {
-        BatchRegs r;
-        load(g, r);
-        step(g, r);
-    }
-
     // Lane (kslot, j) holds vector 4*vq + kslot, rows 32T + 16h + n; the
     // wave's partials go to red[vector][row] in its own stage.
     float *red = reinterpret_cast<float *>(sh.stage[wave]);
+    auto publish = [&]() {
 #pragma unroll
-    for (int vq = 0; vq < NQ; ++vq) {
-        const uint32_t vec = 4 * vq + kslot;
-        if (vec < nvec) {
-            float *dst = red + (4 * vq + kslot) * kBatchRows + 32 * T + 16 * h;
+        for (int vq = 0; vq < NQ; ++vq) {
+            const uint32_t vec = 4 * vq + kslot;
+            if (vec < nvec) {
+                float *dst = red + (4 * vq + kslot) * kBatchRows + 32 * T + 16 * h;
 #pragma unroll
-            for (int n = 0; n < 16; ++n) dst[n] = acc[vq][n];
+                for (int n = 0; n < 16; ++n) dst[n] = acc[vq][n];
+            }
         }
-    }
-    __syncthreads();
+    };
     // Threads split the block's rows; each sums its rows' partials over the
     // waves in wave order.
     auto total = [&](uint32_t vec, uint32_t r) {
@@ -1087,7 +1086,52 @@ __device__ __forceinline__ void run_batch_item(BatchShared<NQ> &sh, const PlanDe
         for (int w = 0; w < kBatchWaves; ++w) v += reinterpret_cast<const float *>(sh.stage[w])[vec * kBatchRows + r];
         return v;
     };
+
+    for (uint32_t g = g_begin + wave; g < g_end; g += kBatchWaves) {
+        BatchRegs r;
+        load(g, r);
+        step(g, r);
+    }
+    // Both streams: the up sums go to registers, one row per thread
+    // (blockDim.x == kBatchRows), and the accumulators start over on the gate.
+    constexpr int V = 4 * NQ;
+    float u[V];
+    if (both) {
+        publish();
+        __syncthreads();
+#pragma unroll
+        for (int vec = 0; vec < V; ++vec) u[vec] = static_cast<uint32_t>(vec) < nvec ? total(vec, threadIdx.x) : 0.0f;
+        __syncthreads();
+#pragma unroll
+        for (int vq = 0; vq < NQ; ++vq)
+#pragma unroll
+            for (int n = 0; n < 16; ++n) acc[vq][n] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            rt[c] = d.gate + static_cast<size_t>(min(8 * block + c, tiles - 1)) * row_tile_bytes;
+        for (uint32_t g = g_begin + wave; g < g_end; g += kBatchWaves) {
+            BatchRegs r;
+            load(g, r);
+            step(g, r);
+        }
+    }
+    publish();
+    __syncthreads();
     const size_t M = d.rows;
+    if (both) {
+        // y = (up + add) * silu(gate), the up sums from registers.
+        const uint32_t r = threadIdx.x, row = block * kBatchRows + r;
+        if (row < d.rows) {
+#pragma unroll
+            for (int vec = 0; vec < V; ++vec) {
+                if (static_cast<uint32_t>(vec) >= nvec) break;
+                float v = u[vec];
+                if (d.add != nullptr) v += ((gptr_cf32)d.add)[vec * M + row];
+                __builtin_nontemporal_store(v * silu(total(vec, r)), (gptr_f32)d.y + vec * M + row);
+            }
+        }
+        return;
+    }
     if (per == 1) {
         for (uint32_t r = threadIdx.x; r < kBatchRows; r += blockDim.x) {
             const uint32_t row = block * kBatchRows + r;

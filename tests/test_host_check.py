@@ -49,8 +49,10 @@ def test_plan_layout_and_deal_under_sanitizers(host_check):
     f = by["qwen3_216_swiglu"]
     assert f["gemvs"] == 216 and f["both_streams"] and f["all_per_one"]
     assert by["qwen3_252_batch8"]["items"] == by["qwen3_252_batch4"]["items"]
+    # Batched, 256-row blocks: q, o 16 each, k, v 4 each, the SwiGLU GEMV 48
+    # (up and gate in one item), down 16: 104 items per layer, no partials.
     g8 = by["qwen3_216_swiglu_batch8"]
-    assert g8["gemvs"] == 216 and not g8["all_per_one"] and not g8["both_streams"]
+    assert g8["gemvs"] == 216 and g8["all_per_one"] and g8["both_streams"] and g8["items"] == 104 * 36
     assert not by["mixed"]["all_per_one"] and by["mixed"]["both_streams"]
     assert by["mixed_small_gpu"]["workgroups"] == 16
     assert by["one_gemv"]["items"] == 1
