@@ -472,7 +472,10 @@ def test_batched_plan_matches_oracle(cuda, batch):
     full chunks, several chunks, odd row-tile counts, row counts that are not
     a multiple of 256, add and SwiGLU epilogues."""
     shapes = [(256, 4096, None), (96, 512, None), (1024, 4096, "add"), (160, 8192, "glu"),
-              (4096, 4096, None), (288, 12288, "add"), (32, 4736, "glu"), (512, 1536, None)]
+              (4096, 4096, None), (288, 12288, "add"), (32, 4736, "glu"), (512, 1536, None),
+              (64, 16384, "glu")]
+    # SwiGLU rows of up to 12288 columns run up and gate in one item; the
+    # 16384-column SwiGLU GEMV meets its chunks and streams in the partials.
     items, checks = [], []
     for i, (rows, cols, kind) in enumerate(shapes):
         t = random_tiles(rows, cols, 500 + 17 * batch + i)
